@@ -1,0 +1,145 @@
+/*
+ * tda.h -- C ABI of the MI355X (gfx950) threshold-attention library libtda_hip.so.
+ *
+ * The library computes Threshold Rectified Attention (TRA, one branch) and
+ * Threshold Differential Attention (TDA, two branches), causal, on tensors of
+ * shape (B, H, N, d):
+ *
+ *   tau_i  = beta * sqrt(2 ln(i+1) / d)                 i = 0-based query index
+ *   A_ij   = ReLU(s(q_i, k_j) - tau_i)^p  for j <= i    s = dot, or cosine when normalize
+ *   out    = A(q1,k1) V                                 branches == 1
+ *   out    = (A(q1,k1) - clamp(lambda,0,1) A(q2,k2)) V  branches == 2
+ *
+ * Reference interface replaced (reference = snap-research/TDA,
+ * triton_threshold_attention.py, cited as TTA:<line>):
+ *   tda_fwd  <- ThresholdRelaFunction.forward host code and the
+ *               _threshold_rela_fwd_kernel launch (TTA:336-403, TTA:374-389);
+ *               branches == 2 also replaces the two-call composition, the
+ *               F.normalize calls and the lambda combine of
+ *               differential_threshold_rela_triton (TTA:505-517).
+ *   tda_bwd  <- ThresholdRelaFunction.backward and the
+ *               _threshold_rela_bwd_kernel_dq / _dkv launches (TTA:406-469,
+ *               TTA:433-460), plus the torch-autograd backward of the
+ *               normalize/clamp/combine ops (TTA:505-517) and dbeta, which the
+ *               reference does not compute (it returns None, TTA:469).
+ *   tda_validate_fwd / tda_validate_bwd <- the shape assert (TTA:348), extended
+ *               to every argument; host-only, never touches a GPU.
+ *
+ * Conventions
+ *   - Every pointer in the argument structs is a device pointer, except the
+ *     struct itself.  The caller allocates everything; the library never
+ *     allocates or frees device memory and keeps no per-call state.
+ *   - Strides are in elements, for the (B, H, N, d) axes.  stride[3] must be 1;
+ *     the other strides and every base pointer must keep 16-byte alignment.
+ *     stride[0] is honoured (the reference ignores it, TTA:49).
+ *   - beta and lambda are read on the device (no host synchronisation);
+ *     lambda is clamped to [0, 1] on the device.
+ *   - All work is enqueued on `stream` (a hipStream_t; NULL = default stream);
+ *     there is no device-wide synchronisation.  Calls are thread-safe.
+ *   - Return value: 0 on success, a negative TDA_ERR_* code otherwise;
+ *     tda_error_string() gives a static description.
+ */
+#ifndef TDA_H_
+#define TDA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TDA_ABI_VERSION 1
+
+/* element types of q, k, v, out and gradients */
+#define TDA_DTYPE_F32  0
+#define TDA_DTYPE_BF16 1
+
+/* error codes */
+#define TDA_OK                 0
+#define TDA_ERR_NULL_POINTER  -1   /* a required pointer is NULL */
+#define TDA_ERR_SHAPE         -2   /* batch/heads/seq_len out of range */
+#define TDA_ERR_HEAD_DIM      -3   /* head_dim not in {64, 128} */
+#define TDA_ERR_DTYPE         -4   /* dtype not TDA_DTYPE_F32 / TDA_DTYPE_BF16 */
+#define TDA_ERR_LAYOUT        -5   /* stride[3] != 1 or 16-byte alignment broken */
+#define TDA_ERR_POWER         -6   /* relu_power negative or not finite */
+#define TDA_ERR_BRANCHES      -7   /* branches not 1 or 2 */
+#define TDA_ERR_WORKSPACE     -8   /* workspace missing or too small */
+#define TDA_ERR_ABI           -9   /* abi_version != TDA_ABI_VERSION */
+#define TDA_ERR_CAUSAL       -10   /* causal != 1 (only the causal form exists) */
+#define TDA_ERR_NORMS        -11   /* normalize set but the norms buffer is missing */
+#define TDA_ERR_HIP         -100   /* a HIP launch failed; see tda_last_hip_error() */
+
+/* One (B, H, N, d) tensor: data pointer plus strides in elements. */
+typedef struct tda_tensor {
+  void*   data;
+  int64_t stride[4];
+} tda_tensor;
+
+typedef struct tda_fwd_args {
+  int32_t abi_version;      /* TDA_ABI_VERSION */
+  int32_t dtype;            /* TDA_DTYPE_* of every tensor */
+  int32_t branches;         /* 1 = TRA (q1, k1, v), 2 = TDA (q1, k1, q2, k2, v) */
+  int32_t normalize;        /* 1 = cosine scores (F.normalize of q and k rows) */
+  int32_t causal;           /* must be 1 */
+  float   relu_power;       /* p >= 0; p == 1 and p == 2 take integer fast paths */
+  int64_t batch, heads, seq_len, head_dim;
+  tda_tensor q1, k1, q2, k2, v;   /* inputs (q2, k2 ignored when branches == 1) */
+  tda_tensor out;                 /* output, same dtype as the inputs */
+  const float* beta;        /* device scalar */
+  const float* lambda_param;/* device scalar, raw (clamped on device); branches == 2 */
+  /* optional outputs for the backward pass (may be NULL): */
+  float*    norms;          /* [2*branches][B*H][N] inverse row norms 1/max(|x|,1e-12)
+                               of q1, k1 (, q2, k2); written when normalize == 1 */
+  uint32_t* occupancy;      /* tile-occupancy bitmask, tda_occupancy_words() words:
+                               bit (qt, kt) set when any A_ij != 0 in the 32x32 tile
+                               of query tile qt and key tile kt */
+  unsigned long long* stats;/* [0] += causal 32x32 tiles visited,
+                               [1] += tiles whose A.V product was computed */
+} tda_fwd_args;
+
+typedef struct tda_bwd_args {
+  int32_t abi_version;
+  int32_t dtype;
+  int32_t branches;
+  int32_t normalize;
+  int32_t causal;
+  float   relu_power;
+  int64_t batch, heads, seq_len, head_dim;
+  tda_tensor q1, k1, q2, k2, v;   /* forward inputs */
+  tda_tensor dout;                /* upstream gradient of out */
+  tda_tensor dq1, dk1, dq2, dk2, dv;  /* outputs (dq2, dk2 ignored when branches == 1) */
+  const float* beta;
+  const float* lambda_param;
+  float* dbeta;             /* device scalar out, may be NULL */
+  float* dlambda;           /* device scalar out (branches == 2), may be NULL */
+  const float*    norms;    /* the forward's norms output; required when normalize == 1 */
+  const uint32_t* occupancy;/* the forward's bitmask, or NULL to test every causal tile */
+  void*  workspace;         /* device scratch of tda_bwd_workspace_bytes() bytes */
+  size_t workspace_bytes;
+  unsigned long long* stats;/* optional: [0] += tiles visited, [1] += tiles computed */
+} tda_bwd_args;
+
+int32_t     tda_abi_version(void);
+const char* tda_error_string(int32_t code);
+/* hipError_t of the last failed launch on this thread (0 if none) */
+int32_t     tda_last_hip_error(void);
+
+/* Host-only argument checks (no GPU access). */
+int32_t tda_validate_fwd(const tda_fwd_args* args);
+int32_t tda_validate_bwd(const tda_bwd_args* args);
+
+/* Buffer sizes for the optional forward outputs and the backward workspace. */
+size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len);
+size_t tda_norms_floats(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
+size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim);
+
+/* Enqueue the forward / backward pass on `stream` (a hipStream_t). */
+int32_t tda_fwd(const tda_fwd_args* args, void* stream);
+int32_t tda_bwd(const tda_bwd_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TDA_H_ */

@@ -1,0 +1,97 @@
+"""Public entry points, drop-in for snap-research/TDA's triton_threshold_attention module.
+
+Same names, argument order, defaults and meaning as the reference
+(triton_threshold_attention.py, TTA:472-519, README.md:54-60):
+
+  threshold_rela_triton(q, k, v, beta, relu_power=2.0, normalize=False)
+  differential_threshold_rela_triton(q1, q2, k1, k2, v, beta, lambda_param,
+                                     relu_power=2.0, normalize=True)
+
+Superset behaviour (all results identical where the reference is defined):
+  * `normalize` also exists on the single-branch function (default False, which is what the
+    reference computes: it never normalises there, TTA:472-486);
+  * beta and lambda_param may be Python floats or tensors; when they require grad they
+    receive a gradient (the reference returns None for beta, TTA:469);
+  * all four (B, H, N, d) strides are honoured (the reference ignores the batch stride,
+    TTA:49);
+  * errors raise ValueError with a message instead of an assert (TTA:348).
+Only the causal form exists, as in the reference.  Supported head_dim: 64, 128.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+_COMPUTE = {torch.float32: torch.float32, torch.bfloat16: torch.bfloat16,
+            torch.float16: torch.float32, torch.float64: torch.float32}
+
+
+def _scalar(x, device, name):
+    """0-dim float32 device tensor for beta / lambda, differentiable when x is a tensor."""
+    if isinstance(x, torch.Tensor):
+        if x.numel() != 1:
+            raise ValueError(f"{name} must be a scalar, got shape {tuple(x.shape)}")
+        return x.to(device=device, dtype=torch.float32).reshape(())
+    return torch.full((), float(x), dtype=torch.float32, device=device)
+
+
+def _power(relu_power) -> float:
+    p = float(relu_power.item() if isinstance(relu_power, torch.Tensor) else relu_power)
+    if not (p >= 0.0 and p < float("inf")):
+        raise ValueError(f"relu_power must be finite and >= 0, got {p}")
+    return p
+
+
+def _run(tensors, names, beta, lam, relu_power, normalize, branches):
+    ops._check_inputs(tensors, names)
+    ref = tensors[0]
+    if ref.shape[-1] not in (64, 128):
+        raise ValueError(f"head_dim must be 64 or 128, got {ref.shape[-1]}")
+    p = _power(relu_power)
+    dev = ref.device
+    cdt = _COMPUTE.get(ref.dtype)
+    if cdt is None:
+        raise ValueError(f"unsupported dtype {ref.dtype}")
+    beta_t = _scalar(beta, dev, "beta")
+    lam_t = _scalar(lam, dev, "lambda_param") if branches == 2 else None
+    if ref.shape[2] == 0 or ref.numel() == 0:
+        zero = sum(t.sum() for t in tensors) * 0.0 + beta_t * 0.0
+        if lam_t is not None:
+            zero = zero + lam_t * 0.0
+        return torch.zeros_like(ref) + zero
+    xs = [t if t.dtype == cdt else t.to(cdt) for t in tensors]
+    if branches == 2:
+        q1, q2, k1, k2, v = xs
+    else:
+        (q1, k1, v), q2, k2 = xs, None, None
+    out = ops.TDAFunction.apply(q1, k1, q2, k2, v, beta_t, lam_t, p, bool(normalize), branches)
+    return out if out.dtype == ref.dtype else out.to(ref.dtype)
+
+
+def threshold_rela_triton(q, k, v, beta, relu_power=2.0, normalize=False):
+    """Threshold Rectified Attention: out = ReLU(Q K^T - tau)^p V, causal,
+    tau_i = beta * sqrt(2 ln(i+1) / d)  (TTA:472-486).
+
+    q, k, v: (batch, heads, seq_len, head_dim) on the GPU, float32 or bfloat16 (float16 and
+    float64 are computed in float32).  beta: float or scalar tensor.  relu_power: float
+    (p == 1 and p == 2 take integer fast paths).  normalize: cosine scores."""
+    return _run((q, k, v), ("q", "k", "v"), beta, None, relu_power, normalize, 1)
+
+
+def differential_threshold_rela_triton(q1, q2, k1, k2, v, beta, lambda_param, relu_power=2.0,
+                                       normalize=True):
+    """Threshold Differential Attention (TTA:489-519):
+    TRA(n(q1), n(k1), v) - clamp(lambda_param, 0, 1) * TRA(n(q2), n(k2), v),
+    computed by one fused kernel; n() is the L2 row normalisation when normalize=True."""
+    return _run((q1, q2, k1, k2, v), ("q1", "q2", "k1", "k2", "v"), beta, lambda_param,
+                relu_power, normalize, 2)
+
+
+class ThresholdRelaFunction:
+    """Name-compatible stand-in for the reference's autograd Function (TTA:327-469):
+    ThresholdRelaFunction.apply(q, k, v, beta, relu_power) == threshold_rela_triton(...)."""
+
+    @staticmethod
+    def apply(q, k, v, beta, relu_power):
+        return threshold_rela_triton(q, k, v, beta, relu_power)

@@ -1,0 +1,477 @@
+// tda_bwd.hip -- backward pass of threshold attention (TRA / differential TDA) for gfx950.
+//
+// Reference semantics (snap-research/TDA triton_threshold_attention.py, "TTA"):
+//   dQ kernel TTA:118-223, dK/dV kernel TTA:226-324, host backward TTA:406-469; the
+//   normalize / clamp / combine gradients come from torch autograd of TTA:505-517; dbeta is
+//   new (the reference returns None for beta, TTA:469).
+//
+// With x_ij = s_ij * rk_j * rq_i - tau_i (s = raw dot product, rq/rk = inverse row norms or 1),
+// G = d(ReLU(x)^p)/dx, Dp_ij = dO_i . v_j:
+//   dS1 = G1 * Dp,  dS2 = -lam * G2 * Dp               (lam = clamp(lambda, 0, 1))
+//   dq^_i = sum_j dS_ij rk_j k_j,   dk^_j = sum_i dS_ij rq_i q_i
+//   dv_j  = sum_i (A1_ij - lam A2_ij) dO_i
+//   dq    = (dq^ - q^ (q^ . dq^)) rq          (F.normalize backward; dq = dq^ when not normalized)
+//   dbeta = -sum_i c_i sum_j (dS1_ij + dS2_ij),  tau_i = beta c_i
+//   dlam  = -[0 <= lambda <= 1] sum_ij A2_ij Dp_ij
+// Two passes keep every output single-writer (no atomics, bitwise reproducible): a query-major
+// pass (dq1, dq2 and the dbeta/dlambda partials) and a key-major pass (dk1, dk2, dv).  When the
+// forward's tile-occupancy bitmask is given, both passes visit only tiles with a non-zero
+// score: A = 0 on a tile implies G = 0 there, so nothing else contributes.
+#include "tda_common.hpp"
+#include "tda_params.hpp"
+
+namespace tda {
+
+template <class Pol, int D> struct TTileSelB;
+template <int D> struct TTileSelB<PolBF16, D> { using type = TTileBF16<D>; };
+template <int D> struct TTileSelB<PolF32, D> { using type = TTileF32<D>; };
+
+template <class Pol, int D, class TT>
+__device__ __forceinline__ void prepare_tile(TT& tt, const TRef<const typename Pol::T>& x, int b, int h,
+                                             int r0, int n) {
+  if constexpr (sizeof(typename Pol::T) == 2) {
+    tt.stage(x, b, h, r0, n);
+    wave_lds_sync();
+  } else {
+    tt.set(x, b, h, r0, n);
+  }
+}
+template <class Pol, class TT>
+__device__ __forceinline__ void release_tile(TT&) {
+  if constexpr (sizeof(typename Pol::T) == 2) wave_lds_sync();
+}
+
+// Apply the F.normalize backward to a gradient tile held in the transposed C layout
+// (lane = one row, value r of column block c = element 32c + crow(r, g)) and store it.
+template <class Pol, int D, bool NORM>
+__device__ __forceinline__ void finish_rows(const f32x16 (&acc)[D / 32], const typename Pol::T* xrow,
+                                            typename Pol::T* grow, float rinv) {
+  constexpr int ND = D / 32;
+  const int g = lane_id() >> 5;
+  if constexpr (NORM) {
+    f32x4 xh[ND][4];
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < ND; ++c)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        f32x4 x = xrow ? load4(xrow + 32 * c + 8 * u + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xh[c][u][e] = x[e] * rinv;
+          dot = __builtin_fmaf(xh[c][u][e], acc[c][4 * u + e], dot);
+        }
+      }
+    dot += __shfl_xor(dot, 32);
+    const bool clamped = rinv >= 1.0f / kNormEps;  // |x| <= eps: x^ = x / eps is linear in x
+    if (grow) {
+#pragma unroll
+      for (int c = 0; c < ND; ++c)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a = acc[c][4 * u + e];
+            o[e] = clamped ? a * rinv : (a - xh[c][u][e] * dot) * rinv;
+          }
+          store4(grow + 32 * c + 8 * u + 4 * g, o[0], o[1], o[2], o[3]);
+        }
+    }
+  } else {
+    if (grow) {
+#pragma unroll
+      for (int c = 0; c < ND; ++c)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          store4(grow + 32 * c + 8 * u + 4 * g, acc[c][4 * u], acc[c][4 * u + 1], acc[c][4 * u + 2],
+                 acc[c][4 * u + 3]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ query-major pass
+// One wave per 32-row query tile (rows i = 32 qt + lane%32), longest-first.  Score tiles are
+// formed as in the forward (S^T = K Q^T: lane = query, values = keys); the gradient tile
+// dS * rk packs into the B operand of dq^T += K^T (dS rk)^T, with K^T staged as a
+// transposed tile.
+template <class Pol, int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
+  using T = typename Pol::T;
+  using frag = typename Pol::frag;
+  constexpr int NT = D / Pol::KS, NS = 32 / Pol::KS, ND = D / 32;
+  using TT = typename TTileSelB<Pol, D>::type;
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5, wv = threadIdx.x >> 6;
+  const int BH = P.B * P.H;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+  if (item >= (int64_t)BH * P.nqt) return;
+  const int qt = P.nqt - 1 - (int)(item / BH);
+  const int bh = (int)(item % BH);
+  const int b = bh / P.H, h = bh % P.H;
+  const int N = P.N;
+  const int i = qt * 32 + n32;
+  const bool qvalid = i < N;
+
+  const TRef<const T> q1{(const T*)P.in[0], P.s[B_Q1][0], P.s[B_Q1][1], P.s[B_Q1][2]};
+  const TRef<const T> k1{(const T*)P.in[1], P.s[B_K1][0], P.s[B_K1][1], P.s[B_K1][2]};
+  const TRef<const T> q2{(const T*)P.in[2], P.s[B_Q2][0], P.s[B_Q2][1], P.s[B_Q2][2]};
+  const TRef<const T> k2{(const T*)P.in[3], P.s[B_K2][0], P.s[B_K2][1], P.s[B_K2][2]};
+  const TRef<const T> vv{(const T*)P.in[4], P.s[B_V][0], P.s[B_V][1], P.s[B_V][2]};
+  const TRef<const T> dO{(const T*)P.in[5], P.s[B_DO][0], P.s[B_DO][1], P.s[B_DO][2]};
+  const TRef<T> dq1{(T*)P.grad[0], P.s[B_DQ1][0], P.s[B_DQ1][1], P.s[B_DQ1][2]};
+  const TRef<T> dq2{(T*)P.grad[2], P.s[B_DQ2][0], P.s[B_DQ2][1], P.s[B_DQ2][2]};
+
+  frag Q1[NT], Q2[NT], DO[NT];
+  {
+    const T* r1 = qvalid ? q1.row(b, h, i) : nullptr;
+    const T* ro = qvalid ? dO.row(b, h, i) : nullptr;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) { Q1[t] = Pol::load_row(r1, t, g); DO[t] = Pol::load_row(ro, t, g); }
+    if constexpr (BR == 2) {
+      const T* r2 = qvalid ? q2.row(b, h, i) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Q2[t] = Pol::load_row(r2, t, g);
+    }
+  }
+  float rq1 = 1.f, rq2 = 1.f;
+  if constexpr (NORM) {
+    if (qvalid) {
+      rq1 = P.norms[((int64_t)N_Q1 * BH + bh) * N + i];
+      if constexpr (BR == 2) rq2 = P.norms[((int64_t)N_Q2 * BH + bh) * N + i];
+    }
+  }
+  const float pw = P.p;
+  const float ci = tau_coeff(i, P.inv_d);
+  const float tau = (*P.beta) * ci;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+
+  __shared__ __attribute__((aligned(16))) bf16 lds_all[(sizeof(T) == 2) ? 4 * TTileBF16<D>::ELEMS : 8];
+  TT kt_tile;
+  if constexpr (sizeof(T) == 2) kt_tile.lds = lds_all + wv * TTileBF16<D>::ELEMS;
+
+  f32x16 A1[ND], A2[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) { A1[c] = f32x16{}; A2[c] = f32x16{}; }
+  float bsum = 0.f, lsum = 0.f;
+  unsigned visited = 0, computed = 0;
+  const uint32_t* occrow = P.occ ? P.occ + ((int64_t)bh * P.nqt + qt) * P.occ_w : nullptr;
+  const float* nk1 = NORM ? P.norms + ((int64_t)N_K1 * BH + bh) * N : nullptr;
+  const float* nk2 = NORM ? P.norms + ((int64_t)N_K2 * BH + bh) * N : nullptr;
+
+  for (int kt = 0; kt <= qt; ++kt) {
+    if (occrow && !((occrow[kt >> 5] >> (kt & 31)) & 1u)) continue;
+    ++visited;
+    const int k0 = kt * 32;
+    const int j = k0 + n32;
+    f32x16 S1 = f32x16{}, S2 = f32x16{}, Dp = f32x16{};
+    {
+      const T* r = (j < N) ? k1.row(b, h, j) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) S1 = Pol::mma(Pol::load_row(r, t, g), Q1[t], S1);
+    }
+    if constexpr (BR == 2) {
+      const T* r = (j < N) ? k2.row(b, h, j) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) S2 = Pol::mma(Pol::load_row(r, t, g), Q2[t], S2);
+    }
+    {
+      const T* r = (j < N) ? vv.row(b, h, j) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Dp = Pol::mma(Pol::load_row(r, t, g), DO[t], Dp);
+    }
+    f32x16 E1, E2;
+    bool any = false;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = k0 + crow(r, g);
+      const bool valid = qvalid && key <= i;  // key <= i < N
+      float rk1 = 1.f, rk2 = 1.f;
+      if constexpr (NORM) {
+        rk1 = valid ? nk1[key] : 0.f;
+        if constexpr (BR == 2) rk2 = valid ? nk2[key] : 0.f;
+      }
+      const float x1 = __builtin_fmaf(NORM ? S1[r] * rk1 : S1[r], rq1, -tau);
+      const bool p1 = valid && x1 > 0.f;
+      const float ds1 = p1 ? dpow_p<PK>(x1, pw) * Dp[r] : 0.f;
+      float ds2 = 0.f;
+      bool p2 = false;
+      if constexpr (BR == 2) {
+        const float x2 = __builtin_fmaf(NORM ? S2[r] * rk2 : S2[r], rq2, -tau);
+        p2 = valid && x2 > 0.f;
+        ds2 = p2 ? -lam * dpow_p<PK>(x2, pw) * Dp[r] : 0.f;
+        lsum = __builtin_fmaf(p2 ? pow_p<PK>(x2, pw) : 0.f, Dp[r], lsum);
+      }
+      bsum += ds1 + ds2;
+      any = any || p1 || p2;
+      E1[r] = NORM ? ds1 * rk1 : ds1;
+      E2[r] = NORM ? ds2 * rk2 : ds2;
+    }
+    if (!occrow && wave_ballot(any) == 0ull) continue;
+    ++computed;
+    prepare_tile<Pol, D>(kt_tile, k1, b, h, k0, N);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const frag bp = Pol::pack_c(E1, s);
+#pragma unroll
+      for (int c = 0; c < ND; ++c) A1[c] = Pol::mma(kt_tile.frag(s, c), bp, A1[c]);
+    }
+    release_tile<Pol>(kt_tile);
+    if constexpr (BR == 2) {
+      prepare_tile<Pol, D>(kt_tile, k2, b, h, k0, N);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const frag bp = Pol::pack_c(E2, s);
+#pragma unroll
+        for (int c = 0; c < ND; ++c) A2[c] = Pol::mma(kt_tile.frag(s, c), bp, A2[c]);
+      }
+      release_tile<Pol>(kt_tile);
+    }
+  }
+
+  finish_rows<Pol, D, NORM>(A1, qvalid ? q1.row(b, h, i) : nullptr, qvalid ? dq1.row(b, h, i) : nullptr, rq1);
+  if constexpr (BR == 2)
+    finish_rows<Pol, D, NORM>(A2, qvalid ? q2.row(b, h, i) : nullptr, qvalid ? dq2.row(b, h, i) : nullptr, rq2);
+
+  // per-wave dbeta / dlambda partials (lanes with g == 1 hold the same query as g == 0 but
+  // other keys, so every lane contributes)
+  const float pb = wave_sum(-ci * bsum);
+  const float pl = wave_sum(-lsum);
+  if (l == 0) {
+    P.ws[2 * item + 0] = pb;
+    P.ws[2 * item + 1] = pl;
+    if (P.stats) {
+      atomicAdd(P.stats + 0, (unsigned long long)visited);
+      atomicAdd(P.stats + 1, (unsigned long long)computed);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ key-major pass
+// One wave per 32-row key tile (rows j = 32 kt + lane%32), longest-first (small kt has the
+// most query tiles).  Scores are formed as S = Q K^T (lane = key, values = queries) so that the
+// probability and gradient tiles pack into the B operand of dv^T += dO^T A and
+// dk^T += Q^T (dS rq), with dO^T and Q^T staged as transposed tiles.
+template <class Pol, int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
+  using T = typename Pol::T;
+  using frag = typename Pol::frag;
+  constexpr int NT = D / Pol::KS, NS = 32 / Pol::KS, ND = D / 32;
+  using TT = typename TTileSelB<Pol, D>::type;
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5, wv = threadIdx.x >> 6;
+  const int BH = P.B * P.H;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+  if (item >= (int64_t)BH * P.nqt) return;
+  const int kt = (int)(item / BH);
+  const int bh = (int)(item % BH);
+  const int b = bh / P.H, h = bh % P.H;
+  const int N = P.N;
+  const int j = kt * 32 + n32;
+  const bool kvalid = j < N;
+
+  const TRef<const T> q1{(const T*)P.in[0], P.s[B_Q1][0], P.s[B_Q1][1], P.s[B_Q1][2]};
+  const TRef<const T> k1{(const T*)P.in[1], P.s[B_K1][0], P.s[B_K1][1], P.s[B_K1][2]};
+  const TRef<const T> q2{(const T*)P.in[2], P.s[B_Q2][0], P.s[B_Q2][1], P.s[B_Q2][2]};
+  const TRef<const T> k2{(const T*)P.in[3], P.s[B_K2][0], P.s[B_K2][1], P.s[B_K2][2]};
+  const TRef<const T> vv{(const T*)P.in[4], P.s[B_V][0], P.s[B_V][1], P.s[B_V][2]};
+  const TRef<const T> dO{(const T*)P.in[5], P.s[B_DO][0], P.s[B_DO][1], P.s[B_DO][2]};
+  const TRef<T> dk1{(T*)P.grad[1], P.s[B_DK1][0], P.s[B_DK1][1], P.s[B_DK1][2]};
+  const TRef<T> dk2{(T*)P.grad[3], P.s[B_DK2][0], P.s[B_DK2][1], P.s[B_DK2][2]};
+  const TRef<T> dvv{(T*)P.grad[4], P.s[B_DV][0], P.s[B_DV][1], P.s[B_DV][2]};
+
+  frag K1[NT], K2[NT], V[NT];
+  {
+    const T* r1 = kvalid ? k1.row(b, h, j) : nullptr;
+    const T* rv = kvalid ? vv.row(b, h, j) : nullptr;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) { K1[t] = Pol::load_row(r1, t, g); V[t] = Pol::load_row(rv, t, g); }
+    if constexpr (BR == 2) {
+      const T* r2 = kvalid ? k2.row(b, h, j) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) K2[t] = Pol::load_row(r2, t, g);
+    }
+  }
+  float rk1 = 1.f, rk2 = 1.f;
+  if constexpr (NORM) {
+    if (kvalid) {
+      rk1 = P.norms[((int64_t)N_K1 * BH + bh) * N + j];
+      if constexpr (BR == 2) rk2 = P.norms[((int64_t)N_K2 * BH + bh) * N + j];
+    }
+  }
+  const float pw = P.p;
+  const float beta = *P.beta;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+  const float* nq1 = NORM ? P.norms + ((int64_t)N_Q1 * BH + bh) * N : nullptr;
+  const float* nq2 = NORM ? P.norms + ((int64_t)N_Q2 * BH + bh) * N : nullptr;
+
+  __shared__ __attribute__((aligned(16))) bf16 lds_all[(sizeof(T) == 2) ? 4 * TTileBF16<D>::ELEMS : 8];
+  TT tile;
+  if constexpr (sizeof(T) == 2) tile.lds = lds_all + wv * TTileBF16<D>::ELEMS;
+
+  f32x16 AV[ND], AK1[ND], AK2[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) { AV[c] = f32x16{}; AK1[c] = f32x16{}; AK2[c] = f32x16{}; }
+  unsigned visited = 0, computed = 0;
+  const uint32_t* occcol = P.occ ? P.occ + (int64_t)bh * P.nqt * P.occ_w + (kt >> 5) : nullptr;
+
+  for (int qt = kt; qt < P.nqt; ++qt) {
+    if (occcol && !((occcol[(int64_t)qt * P.occ_w] >> (kt & 31)) & 1u)) continue;
+    ++visited;
+    const int q0 = qt * 32;
+    const int ia = q0 + n32;  // query row this lane loads for the A operand
+    f32x16 S1 = f32x16{}, S2 = f32x16{}, Dp = f32x16{};
+    {
+      const T* r = (ia < N) ? q1.row(b, h, ia) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) S1 = Pol::mma(Pol::load_row(r, t, g), K1[t], S1);
+    }
+    if constexpr (BR == 2) {
+      const T* r = (ia < N) ? q2.row(b, h, ia) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) S2 = Pol::mma(Pol::load_row(r, t, g), K2[t], S2);
+    }
+    {
+      const T* r = (ia < N) ? dO.row(b, h, ia) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Dp = Pol::mma(Pol::load_row(r, t, g), V[t], Dp);
+    }
+    f32x16 EV, E1, E2;
+    bool any = false;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qi = q0 + crow(r, g);
+      const bool valid = kvalid && qi < N && j <= qi;
+      float rq1 = 1.f, rq2 = 1.f;
+      if constexpr (NORM) {
+        rq1 = valid ? nq1[qi] : 0.f;
+        if constexpr (BR == 2) rq2 = valid ? nq2[qi] : 0.f;
+      }
+      const float tau = beta * tau_coeff(qi, P.inv_d);
+      const float x1 = __builtin_fmaf(NORM ? S1[r] * rk1 : S1[r], rq1, -tau);
+      const bool p1 = valid && x1 > 0.f;
+      float a = p1 ? pow_p<PK>(x1, pw) : 0.f;
+      const float ds1 = p1 ? dpow_p<PK>(x1, pw) * Dp[r] : 0.f;
+      float ds2 = 0.f;
+      bool p2 = false;
+      if constexpr (BR == 2) {
+        const float x2 = __builtin_fmaf(NORM ? S2[r] * rk2 : S2[r], rq2, -tau);
+        p2 = valid && x2 > 0.f;
+        a = __builtin_fmaf(-lam, p2 ? pow_p<PK>(x2, pw) : 0.f, a);
+        ds2 = p2 ? -lam * dpow_p<PK>(x2, pw) * Dp[r] : 0.f;
+      }
+      any = any || p1 || p2;
+      EV[r] = a;
+      E1[r] = NORM ? ds1 * rq1 : ds1;
+      E2[r] = NORM ? ds2 * rq2 : ds2;
+    }
+    if (!occcol && wave_ballot(any) == 0ull) continue;
+    ++computed;
+    prepare_tile<Pol, D>(tile, dO, b, h, q0, N);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const frag bp = Pol::pack_c(EV, s);
+#pragma unroll
+      for (int c = 0; c < ND; ++c) AV[c] = Pol::mma(tile.frag(s, c), bp, AV[c]);
+    }
+    release_tile<Pol>(tile);
+    prepare_tile<Pol, D>(tile, q1, b, h, q0, N);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const frag bp = Pol::pack_c(E1, s);
+#pragma unroll
+      for (int c = 0; c < ND; ++c) AK1[c] = Pol::mma(tile.frag(s, c), bp, AK1[c]);
+    }
+    release_tile<Pol>(tile);
+    if constexpr (BR == 2) {
+      prepare_tile<Pol, D>(tile, q2, b, h, q0, N);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const frag bp = Pol::pack_c(E2, s);
+#pragma unroll
+        for (int c = 0; c < ND; ++c) AK2[c] = Pol::mma(tile.frag(s, c), bp, AK2[c]);
+      }
+      release_tile<Pol>(tile);
+    }
+  }
+
+  finish_rows<Pol, D, false>(AV, nullptr, kvalid ? dvv.row(b, h, j) : nullptr, 1.f);
+  finish_rows<Pol, D, NORM>(AK1, kvalid ? k1.row(b, h, j) : nullptr, kvalid ? dk1.row(b, h, j) : nullptr, rk1);
+  if constexpr (BR == 2)
+    finish_rows<Pol, D, NORM>(AK2, kvalid ? k2.row(b, h, j) : nullptr, kvalid ? dk2.row(b, h, j) : nullptr, rk2);
+  if (P.stats && l == 0) {
+    atomicAdd(P.stats + 0, (unsigned long long)visited);
+    atomicAdd(P.stats + 1, (unsigned long long)computed);
+  }
+}
+
+// Deterministic second stage: fixed-order fp64 sum of the per-wave partials.
+__global__ void __launch_bounds__(256) bwd_finish(const float* ws, int64_t items, const float* lam,
+                                                  float* dbeta, float* dlam, int branches) {
+  __shared__ double sb[256], sl[256];
+  double a = 0.0, c = 0.0;
+  for (int64_t k = threadIdx.x; k < items; k += 256) {
+    a += (double)ws[2 * k];
+    c += (double)ws[2 * k + 1];
+  }
+  sb[threadIdx.x] = a;
+  sl[threadIdx.x] = c;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) {
+      sb[threadIdx.x] += sb[threadIdx.x + o];
+      sl[threadIdx.x] += sl[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (dbeta) dbeta[0] = (float)sb[0];
+    if (dlam && branches == 2) {
+      const float lv = lam[0];
+      const bool gate = lv >= 0.f && lv <= 1.f;  // torch.clamp passes the gradient on [0, 1]
+      dlam[0] = gate ? (float)sl[0] : 0.f;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+template <class Pol, int D, int BR, int PK, bool NORM>
+static int launch_bwd_t(const BwdParams& p, void* stream) {
+  const int64_t items = (int64_t)p.B * p.H * p.nqt;
+  const unsigned grid = (unsigned)((items + 3) / 4);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL((bwd_dq<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((bwd_dkv<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(bwd_finish, dim3(1), dim3(256), 0, s, (const float*)p.ws, items, p.lam, p.dbeta, p.dlam,
+                     BR);
+  return (int)hipGetLastError();
+}
+
+template <class Pol, int D, int BR, int PK>
+static int bsel_norm(const BwdParams& p, const KernelKey& k, void* s) {
+  return k.normalize ? launch_bwd_t<Pol, D, BR, PK, true>(p, s) : launch_bwd_t<Pol, D, BR, PK, false>(p, s);
+}
+template <class Pol, int D, int BR>
+static int bsel_pk(const BwdParams& p, const KernelKey& k, void* s) {
+  switch (k.pkind) {
+    case 2: return bsel_norm<Pol, D, BR, 2>(p, k, s);
+    case 1: return bsel_norm<Pol, D, BR, 1>(p, k, s);
+    default: return bsel_norm<Pol, D, BR, 0>(p, k, s);
+  }
+}
+template <class Pol, int D>
+static int bsel_br(const BwdParams& p, const KernelKey& k, void* s) {
+  return k.branches == 2 ? bsel_pk<Pol, D, 2>(p, k, s) : bsel_pk<Pol, D, 1>(p, k, s);
+}
+template <class Pol>
+static int bsel_d(const BwdParams& p, const KernelKey& k, void* s) {
+  return k.d == 128 ? bsel_br<Pol, 128>(p, k, s) : bsel_br<Pol, 64>(p, k, s);
+}
+
+int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream) {
+  return k.dtype == 1 ? bsel_d<PolBF16>(p, k, stream) : bsel_d<PolF32>(p, k, stream);
+}
+
+}  // namespace tda

@@ -1,0 +1,223 @@
+// tda_common.hpp -- device building blocks shared by the gfx950 threshold-attention kernels.
+//
+// Matrix-core conventions (CDNA3/CDNA4 32x32 MFMA family, wave64):
+//   C/D (32x32 fp32, 16 values per lane): lane l holds column n = l % 32 and,
+//       in value r (0..15), row  crow(r, g) = 8*(r/4) + 4*g + (r%4),  g = l / 32.
+//   A (M x K): lane l holds row m = l % 32 and E consecutive K indices starting at E*g.
+//   B (K x N): lane l holds column n = l % 32 and E consecutive K indices starting at E*g.
+// bf16 uses v_mfma_f32_32x32x16_bf16 (K = 16 per instruction, E = 8 elements per lane);
+// fp32 uses v_mfma_f32_32x32x2f32 (K = 2, E = 1).
+//
+// Two operand shapes appear in every kernel:
+//   * "row fragments": a 32-row tile of a (N, d) tensor contracted over d.  Lane (m, g) holds
+//     row m, elements d = KS*t + E*g + [0, E) for step t.  Rows load straight from HBM.
+//   * "transposed fragments": the same kind of tile contracted over its rows (the sequence
+//     axis), with lane (n, g) holding column d = n.  For step s, element j sits at tile row
+//     crow(s*E + j, g): that matches the C layout of a score tile, so a score tile in
+//     registers feeds the next MFMA as the B operand with no data movement (pack_c below).
+//     bf16 stages such a tile through LDS in a transposed, row-permuted layout; fp32 reads
+//     its single element per step straight from memory.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tda {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kNormEps = 1e-12f;  // torch.nn.functional.normalize default eps
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// Row of C value r for lane group g (see header comment).
+__device__ __forceinline__ constexpr int crow(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+// ------------------------------------------------------------------ MFMA policies
+struct PolBF16 {
+  using T = bf16;
+  using frag = bf16x8;
+  static constexpr int KS = 16;  // contraction length of one instruction
+  static constexpr int E = 8;    // operand elements per lane
+  __device__ __forceinline__ static f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static frag zero() { return frag{}; }
+  // Row-fragment step t of a row whose first element is `row` (null -> zeros).
+  __device__ __forceinline__ static frag load_row(const T* row, int t, int g) {
+    if (!row) return zero();
+    return *reinterpret_cast<const frag*>(row + KS * t + E * g);
+  }
+  // Pack values [s*E, s*E+E) of a C tile into a B operand (round to nearest even).
+  __device__ __forceinline__ static frag pack_c(const f32x16& c, int s) {
+    frag f;
+#pragma unroll
+    for (int j = 0; j < E; ++j) f[j] = (bf16)c[s * E + j];
+    return f;
+  }
+  __device__ __forceinline__ static float sumsq(frag f) {
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < E; ++j) { float x = (float)f[j]; a = __builtin_fmaf(x, x, a); }
+    return a;
+  }
+};
+
+struct PolF32 {
+  using T = float;
+  using frag = float;
+  static constexpr int KS = 2;
+  static constexpr int E = 1;
+  __device__ __forceinline__ static f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static frag zero() { return 0.f; }
+  __device__ __forceinline__ static frag load_row(const T* row, int t, int g) {
+    if (!row) return 0.f;
+    return row[KS * t + g];
+  }
+  __device__ __forceinline__ static frag pack_c(const f32x16& c, int s) { return c[s]; }
+  __device__ __forceinline__ static float sumsq(frag f) { return f * f; }
+};
+
+// ------------------------------------------------------------------ tensors
+template <class T>
+struct TRef {
+  T* p;
+  int64_t sb, sh, st;  // element strides of the batch, head and sequence axes (d stride == 1)
+  __device__ __forceinline__ T* row(int b, int h, int t) const {
+    return p + (int64_t)b * sb + (int64_t)h * sh + (int64_t)t * st;
+  }
+};
+
+// ------------------------------------------------------------------ threshold and power
+// c_i = sqrt(2 ln(i+1) / d); tau_i = beta * c_i  (reference: TTA:59-63)
+__device__ __forceinline__ float tau_coeff(int i, float inv_d) {
+  return sqrtf(2.0f * logf((float)i + 1.0f) * inv_d);
+}
+
+// x^p and d(x^p)/dx for x > 0.  PK: 2 -> p == 2, 1 -> p == 1, 0 -> general p via
+// 2^(p log2 x) on the hardware exp2/log2 units.
+template <int PK>
+__device__ __forceinline__ float pow_p(float x, float p) {
+  if constexpr (PK == 2) return x * x;
+  else if constexpr (PK == 1) return x;
+  else return __builtin_amdgcn_exp2f(p * __builtin_amdgcn_logf(x));
+}
+template <int PK>
+__device__ __forceinline__ float dpow_p(float x, float p) {
+  if constexpr (PK == 2) return 2.0f * x;
+  else if constexpr (PK == 1) return 1.0f;
+  else return p * __builtin_amdgcn_exp2f((p - 1.0f) * __builtin_amdgcn_logf(x));
+}
+
+__device__ __forceinline__ float clamp01(float x) { return fminf(fmaxf(x, 0.0f), 1.0f); }
+
+// inverse row norm 1/max(|x|, eps) from a sum of squares
+__device__ __forceinline__ float inv_norm(float ss) { return 1.0f / fmaxf(sqrtf(ss), kNormEps); }
+
+// Sum over the lane's row fragments plus the partner lane (l ^ 32), which holds the rest of
+// the row: every lane ends with the full sum of squares of its row.
+template <class Pol, int NT>
+__device__ __forceinline__ float row_sumsq(const typename Pol::frag (&f)[NT]) {
+  float a = 0.f;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) a += Pol::sumsq(f[t]);
+  return a + __shfl_xor(a, 32);
+}
+
+// Deterministic wave-wide sum (fixed butterfly order).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ unsigned long long wave_ballot(bool b) { return __ballot(b); }
+
+// ------------------------------------------------------------------ transposed tiles
+// A 32-row x D tile used as the A operand of a contraction over its rows.
+// bf16: staged in (wave-private) LDS as T[d][pos(row)], pos() swapping bits 2 and 3 of the
+// row index, row stride TS elements.  Then the E = 8 elements of step s for lane group g
+// (tile rows crow(8s + j, g), j = 0..7) are the 8 contiguous positions 16s + 8g + j.
+template <int D>
+struct TTileBF16 {
+  static constexpr int TS = 40;  // 32 positions + 8 padding: 80-byte rows, conflict-free b128 reads
+  static constexpr int ELEMS = D * TS;
+  bf16* lds;
+
+  __device__ __forceinline__ static int pos4(int a) {  // position of row 4a (a = 0..7)
+    return 4 * ((a & 4) | ((a & 1) << 1) | ((a >> 1) & 1));
+  }
+  // Stage rows r0..r0+31 of the tensor `base` (rows >= n read as zeros) into LDS.
+  __device__ __forceinline__ void stage(const TRef<const bf16>& x, int b, int h, int r0, int n) const {
+    const int l = lane_id();
+#pragma unroll
+    for (int it = 0; it < D / 64; ++it) {
+      const int mt = l + 64 * it;      // micro-tile: 4 rows x 8 columns
+      const int a = mt / (D / 8);      // row group (rows 4a..4a+3)
+      const int d0 = (mt % (D / 8)) * 8;
+      bf16x8 v[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int r = r0 + 4 * a + c;
+        v[c] = (r < n) ? *reinterpret_cast<const bf16x8*>(x.row(b, h, r) + d0) : bf16x8{};
+      }
+      const int p = pos4(a);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        bf16x4 w = {v[0][j], v[1][j], v[2][j], v[3][j]};
+        *reinterpret_cast<bf16x4*>(lds + (d0 + j) * TS + p) = w;
+      }
+    }
+  }
+  __device__ __forceinline__ bf16x8 frag(int s, int dsub) const {
+    const int l = lane_id();
+    return *reinterpret_cast<const bf16x8*>(lds + (32 * dsub + (l & 31)) * TS + 16 * s + 8 * (l >> 5));
+  }
+};
+
+// fp32: the single element of step s for lane (n, g) is X[r0 + crow(s, g)][32 dsub + n],
+// read straight from memory (coalesced over n).
+template <int D>
+struct TTileF32 {
+  TRef<const float> x;
+  int b, h, r0, n;
+  __device__ __forceinline__ void set(const TRef<const float>& x_, int b_, int h_, int r0_, int n_) {
+    x = x_; b = b_; h = h_; r0 = r0_; n = n_;
+  }
+  __device__ __forceinline__ float frag(int s, int dsub) const {
+    const int l = lane_id();
+    const int r = r0 + crow(s, l >> 5);
+    return (r < n) ? x.row(b, h, r)[32 * dsub + (l & 31)] : 0.f;
+  }
+};
+
+// Make LDS writes of this wave visible to its own later LDS reads (and order reads before
+// later overwrites).  LDS instructions of one wave execute in order; the fences keep the
+// compiler from reordering across the hand-off and wait for outstanding LDS traffic.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Store 4 consecutive output elements (fp32 accumulators -> T).
+__device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float d) {
+  bf16x4 w = {(bf16)a, (bf16)b, (bf16)c, (bf16)d};
+  *reinterpret_cast<bf16x4*>(p) = w;
+}
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{a, b, c, d};
+}
+__device__ __forceinline__ f32x4 load4(const bf16* p) {
+  bf16x4 w = *reinterpret_cast<const bf16x4*>(p);
+  return f32x4{(float)w[0], (float)w[1], (float)w[2], (float)w[3]};
+}
+__device__ __forceinline__ f32x4 load4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+
+}  // namespace tda

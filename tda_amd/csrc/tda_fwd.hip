@@ -1,0 +1,228 @@
+// tda_fwd.hip -- forward pass of threshold attention (TRA / differential TDA) for gfx950.
+//
+// Reference semantics (snap-research/TDA triton_threshold_attention.py, "TTA"):
+//   forward kernel TTA:19-115, differential composition TTA:489-519.
+// Every 32x32 (query tile, key tile) pair on or below the diagonal is visited; the scores of
+// both branches are formed on the matrix cores, thresholded in registers, and the A.V
+// product is issued only when a wave-wide ballot finds a non-zero entry (ReLU leaves almost
+// every tile empty: TDA is ultra-sparse).  The two branches share one accumulator:
+// out = sum_j (A1_ij - clamp(lambda) A2_ij) v_j, so the differential combine is free.
+#include "tda_common.hpp"
+#include "tda_params.hpp"
+
+namespace tda {
+
+template <class Pol, int D> struct TTileSel;
+template <int D> struct TTileSel<PolBF16, D> { using type = TTileBF16<D>; };
+template <int D> struct TTileSel<PolF32, D> { using type = TTileF32<D>; };
+
+// One wave per 32-row query tile, four independent waves per workgroup.  Work items are
+// ordered longest-first (the last query tiles have the most causal key tiles).
+//
+// Layouts (see tda_common.hpp): the score tile is computed transposed, S^T = K Q^T, with the
+// key rows as the A operand (row fragments loaded from HBM per key tile) and the wave's query
+// rows as the resident B operand.  In the C layout each lane then owns one query and 16 keys,
+// so the per-query threshold, inverse norm and the causal test are per-lane scalars, and the
+// thresholded tile packs directly into the B operand of O^T += V^T A^T.
+template <class Pol, int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
+  using T = typename Pol::T;
+  using frag = typename Pol::frag;
+  constexpr int NT = D / Pol::KS;  // MFMA steps over d
+  constexpr int NS = 32 / Pol::KS; // MFMA steps over a 32-key tile
+  constexpr int ND = D / 32;       // 32-wide column blocks of the output
+  using TT = typename TTileSel<Pol, D>::type;
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5, wv = threadIdx.x >> 6;
+  const int BH = P.B * P.H;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+  if (item >= (int64_t)BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
+  const int qt = P.nqt - 1 - (int)(item / BH);
+  const int bh = (int)(item % BH);
+  const int b = bh / P.H, h = bh % P.H;
+  const int N = P.N;
+  const int i = qt * 32 + n32;  // this lane's query row
+  const bool qvalid = i < N;
+
+  const TRef<const T> q1{(const T*)P.in[0], P.s[F_Q1][0], P.s[F_Q1][1], P.s[F_Q1][2]};
+  const TRef<const T> k1{(const T*)P.in[1], P.s[F_K1][0], P.s[F_K1][1], P.s[F_K1][2]};
+  const TRef<const T> q2{(const T*)P.in[2], P.s[F_Q2][0], P.s[F_Q2][1], P.s[F_Q2][2]};
+  const TRef<const T> k2{(const T*)P.in[3], P.s[F_K2][0], P.s[F_K2][1], P.s[F_K2][2]};
+  const TRef<const T> vv{(const T*)P.in[4], P.s[F_V][0], P.s[F_V][1], P.s[F_V][2]};
+  const TRef<T> out{(T*)P.out, P.s[F_OUT][0], P.s[F_OUT][1], P.s[F_OUT][2]};
+
+  frag Q1[NT], Q2[NT];
+  {
+    const T* r1 = qvalid ? q1.row(b, h, i) : nullptr;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) Q1[t] = Pol::load_row(r1, t, g);
+    if constexpr (BR == 2) {
+      const T* r2 = qvalid ? q2.row(b, h, i) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Q2[t] = Pol::load_row(r2, t, g);
+    }
+  }
+  float rq1 = 1.f, rq2 = 1.f;
+  if constexpr (NORM) {
+    rq1 = inv_norm(row_sumsq<Pol, NT>(Q1));
+    if constexpr (BR == 2) rq2 = inv_norm(row_sumsq<Pol, NT>(Q2));
+    if (P.norms && qvalid && g == 0) {
+      P.norms[((int64_t)N_Q1 * BH + bh) * N + i] = rq1;
+      if constexpr (BR == 2) P.norms[((int64_t)N_Q2 * BH + bh) * N + i] = rq2;
+    }
+  }
+  const float pw = P.p;
+  const float tau = (*P.beta) * tau_coeff(i, P.inv_d);
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+
+  __shared__ __attribute__((aligned(16))) bf16 lds_all[(sizeof(T) == 2) ? 4 * TTileBF16<D>::ELEMS : 8];
+  TT vt;
+  if constexpr (sizeof(T) == 2) vt.lds = lds_all + wv * TTileBF16<D>::ELEMS;
+
+  f32x16 O[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) O[c] = f32x16{};
+
+  uint32_t* occrow = P.occ ? P.occ + ((int64_t)bh * P.nqt + qt) * P.occ_w : nullptr;
+  uint32_t word = 0;
+  unsigned visited = 0, computed = 0;
+
+  for (int kt = 0; kt <= qt; ++kt) {
+    const int k0 = kt * 32;
+    const int j = k0 + n32;  // key row this lane loads for the A operand
+    f32x16 S1 = f32x16{}, S2 = f32x16{};
+    float rk1r[16], rk2r[16];
+    {
+      frag K1[NT];
+      const T* r1 = (j < N) ? k1.row(b, h, j) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) K1[t] = Pol::load_row(r1, t, g);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) S1 = Pol::mma(K1[t], Q1[t], S1);
+      if constexpr (NORM) {
+        const float rk = inv_norm(row_sumsq<Pol, NT>(K1));
+        if (P.norms && kt == qt && g == 0 && j < N) P.norms[((int64_t)N_K1 * BH + bh) * N + j] = rk;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rk1r[r] = __shfl(rk, crow(r, g));
+      }
+    }
+    if constexpr (BR == 2) {
+      frag K2[NT];
+      const T* r2 = (j < N) ? k2.row(b, h, j) : nullptr;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) K2[t] = Pol::load_row(r2, t, g);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) S2 = Pol::mma(K2[t], Q2[t], S2);
+      if constexpr (NORM) {
+        const float rk = inv_norm(row_sumsq<Pol, NT>(K2));
+        if (P.norms && kt == qt && g == 0 && j < N) P.norms[((int64_t)N_K2 * BH + bh) * N + j] = rk;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rk2r[r] = __shfl(rk, crow(r, g));
+      }
+    }
+
+    // Threshold test.  x = fma(s * rk_j, rq_i, -tau_i) is monotone in s * rk_j, so the tile
+    // max decides "any x > 0" exactly.
+    float m1 = -INFINITY, m2 = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const bool valid = qvalid && (k0 + crow(r, g) <= i);
+      if constexpr (NORM) S1[r] *= rk1r[r];
+      m1 = fmaxf(m1, valid ? S1[r] : -INFINITY);
+      if constexpr (BR == 2) {
+        if constexpr (NORM) S2[r] *= rk2r[r];
+        m2 = fmaxf(m2, valid ? S2[r] : -INFINITY);
+      }
+    }
+    bool act = __builtin_fmaf(m1, rq1, -tau) > 0.f;
+    if constexpr (BR == 2) act = act || (__builtin_fmaf(m2, rq2, -tau) > 0.f);
+    ++visited;
+    if (wave_ballot(act) != 0ull) {
+      ++computed;
+      word |= 1u << (kt & 31);
+      f32x16 C;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool valid = qvalid && (k0 + crow(r, g) <= i);
+        const float x1 = __builtin_fmaf(S1[r], rq1, -tau);
+        float a = (valid && x1 > 0.f) ? pow_p<PK>(x1, pw) : 0.f;
+        if constexpr (BR == 2) {
+          const float x2 = __builtin_fmaf(S2[r], rq2, -tau);
+          const float a2 = (valid && x2 > 0.f) ? pow_p<PK>(x2, pw) : 0.f;
+          a = __builtin_fmaf(-lam, a2, a);
+        }
+        C[r] = a;
+      }
+      if constexpr (sizeof(T) == 2) {
+        vt.stage(vv, b, h, k0, N);
+        wave_lds_sync();
+      } else {
+        vt.set(vv, b, h, k0, N);
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const frag bp = Pol::pack_c(C, s);
+#pragma unroll
+        for (int c = 0; c < ND; ++c) O[c] = Pol::mma(vt.frag(s, c), bp, O[c]);
+      }
+      if constexpr (sizeof(T) == 2) wave_lds_sync();
+    }
+    if (occrow && (((kt & 31) == 31) || kt == qt)) {
+      if (l == 0) occrow[kt >> 5] = word;
+      word = 0;
+    }
+  }
+  if (occrow && l == 0) {
+    for (int w = (qt >> 5) + 1; w < P.occ_w; ++w) occrow[w] = 0u;
+  }
+
+  if (qvalid) {
+    T* orow = out.row(b, h, i);
+#pragma unroll
+    for (int c = 0; c < ND; ++c)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        store4(orow + 32 * c + 8 * u + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2], O[c][4 * u + 3]);
+  }
+  if (P.stats && l == 0) {
+    atomicAdd(P.stats + 0, (unsigned long long)visited);
+    atomicAdd(P.stats + 1, (unsigned long long)computed);
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+template <class Pol, int D, int BR, int PK, bool NORM>
+static int launch_fwd_t(const FwdParams& p, void* stream) {
+  const int64_t items = (int64_t)p.B * p.H * p.nqt;
+  const unsigned grid = (unsigned)((items + 3) / 4);
+  hipLaunchKernelGGL((fwd_wave<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}
+
+template <class Pol, int D, int BR, int PK>
+static int sel_norm(const FwdParams& p, const KernelKey& k, void* s) {
+  return k.normalize ? launch_fwd_t<Pol, D, BR, PK, true>(p, s) : launch_fwd_t<Pol, D, BR, PK, false>(p, s);
+}
+template <class Pol, int D, int BR>
+static int sel_pk(const FwdParams& p, const KernelKey& k, void* s) {
+  switch (k.pkind) {
+    case 2: return sel_norm<Pol, D, BR, 2>(p, k, s);
+    case 1: return sel_norm<Pol, D, BR, 1>(p, k, s);
+    default: return sel_norm<Pol, D, BR, 0>(p, k, s);
+  }
+}
+template <class Pol, int D>
+static int sel_br(const FwdParams& p, const KernelKey& k, void* s) {
+  return k.branches == 2 ? sel_pk<Pol, D, 2>(p, k, s) : sel_pk<Pol, D, 1>(p, k, s);
+}
+template <class Pol>
+static int sel_d(const FwdParams& p, const KernelKey& k, void* s) {
+  return k.d == 128 ? sel_br<Pol, 128>(p, k, s) : sel_br<Pol, 64>(p, k, s);
+}
+
+int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream) {
+  return k.dtype == 1 ? sel_d<PolBF16>(p, k, stream) : sel_d<PolF32>(p, k, stream);
+}
+
+}  // namespace tda

@@ -1,0 +1,223 @@
+// tda_host.cpp -- C ABI of libtda_hip.so: argument validation, buffer sizing and dispatch.
+//
+// Replaces the host side of the reference (snap-research/TDA triton_threshold_attention.py):
+// ThresholdRelaFunction.forward/backward (TTA:336-469) and their Triton launches
+// (TTA:374-389, TTA:433-460).  Unlike the reference, beta and lambda stay on the device (no
+// .item() synchronisation, TTA:352), nothing is up-cast or copied (TTA:356-360), and every
+// argument is checked before any GPU work (the reference only asserts equal shapes, TTA:348).
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+
+#include "../../include/tda.h"
+#include "tda_params.hpp"
+
+namespace {
+
+thread_local int32_t g_last_hip_error = 0;
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int32_t check_tensor(const tda_tensor& t, int64_t elem_bytes) {
+  if (!t.data) return TDA_ERR_NULL_POINTER;
+  if (t.stride[3] != 1) return TDA_ERR_LAYOUT;
+  if (reinterpret_cast<uintptr_t>(t.data) % 16 != 0) return TDA_ERR_LAYOUT;
+  for (int k = 0; k < 3; ++k) {
+    if (t.stride[k] < 0) return TDA_ERR_LAYOUT;
+    if ((t.stride[k] * elem_bytes) % 16 != 0) return TDA_ERR_LAYOUT;
+  }
+  return TDA_OK;
+}
+
+struct Common {
+  int32_t abi_version, dtype, branches, normalize, causal;
+  float relu_power;
+  int64_t batch, heads, seq_len, head_dim;
+  const float* beta;
+  const float* lambda_param;
+};
+
+int32_t check_common(const Common& c) {
+  if (c.abi_version != TDA_ABI_VERSION) return TDA_ERR_ABI;
+  if (c.dtype != TDA_DTYPE_F32 && c.dtype != TDA_DTYPE_BF16) return TDA_ERR_DTYPE;
+  if (c.branches != 1 && c.branches != 2) return TDA_ERR_BRANCHES;
+  if (c.causal != 1) return TDA_ERR_CAUSAL;
+  if (c.head_dim != 64 && c.head_dim != 128) return TDA_ERR_HEAD_DIM;
+  if (c.batch < 1 || c.heads < 1 || c.seq_len < 1) return TDA_ERR_SHAPE;
+  if (c.seq_len > (int64_t(1) << 30)) return TDA_ERR_SHAPE;
+  if (c.batch * c.heads > (int64_t(1) << 24)) return TDA_ERR_SHAPE;
+  if (c.batch * c.heads * ceil_div(c.seq_len, 32) > (int64_t(1) << 31) - 4) return TDA_ERR_SHAPE;
+  if (!std::isfinite(c.relu_power) || c.relu_power < 0.f) return TDA_ERR_POWER;
+  if (!c.beta) return TDA_ERR_NULL_POINTER;
+  if (c.branches == 2 && !c.lambda_param) return TDA_ERR_NULL_POINTER;
+  return TDA_OK;
+}
+
+int pkind_of(float p) { return p == 2.0f ? 2 : (p == 1.0f ? 1 : 0); }
+
+template <class A>
+Common common_of(const A& a) {
+  return Common{a.abi_version, a.dtype, a.branches, a.normalize, a.causal, a.relu_power,
+                a.batch, a.heads, a.seq_len, a.head_dim, a.beta, a.lambda_param};
+}
+
+void copy_strides(int64_t dst[3], const tda_tensor& t) {
+  dst[0] = t.stride[0];
+  dst[1] = t.stride[1];
+  dst[2] = t.stride[2];
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t tda_abi_version(void) { return TDA_ABI_VERSION; }
+
+int32_t tda_last_hip_error(void) { return g_last_hip_error; }
+
+const char* tda_error_string(int32_t code) {
+  switch (code) {
+    case TDA_OK: return "ok";
+    case TDA_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case TDA_ERR_SHAPE: return "batch, heads or seq_len out of range";
+    case TDA_ERR_HEAD_DIM: return "head_dim must be 64 or 128";
+    case TDA_ERR_DTYPE: return "dtype must be float32 or bfloat16";
+    case TDA_ERR_LAYOUT: return "tensor layout unsupported: last-dim stride must be 1 and strides/pointers 16-byte aligned";
+    case TDA_ERR_POWER: return "relu_power must be finite and >= 0";
+    case TDA_ERR_BRANCHES: return "branches must be 1 or 2";
+    case TDA_ERR_WORKSPACE: return "backward workspace missing or too small";
+    case TDA_ERR_ABI: return "abi_version mismatch";
+    case TDA_ERR_CAUSAL: return "only the causal form is implemented (causal must be 1)";
+    case TDA_ERR_NORMS: return "normalize requires the forward pass's norms buffer";
+    case TDA_ERR_HIP: return "HIP kernel launch failed";
+    default: return "unknown error";
+  }
+}
+
+size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len) {
+  if (batch < 1 || heads < 1 || seq_len < 1) return 0;
+  const int64_t nqt = ceil_div(seq_len, 32);
+  return (size_t)(batch * heads * nqt * ceil_div(nqt, 32));
+}
+
+size_t tda_norms_floats(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches) {
+  if (batch < 1 || heads < 1 || seq_len < 1 || (branches != 1 && branches != 2)) return 0;
+  return (size_t)(2 * branches * batch * heads * seq_len);
+}
+
+size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim) {
+  (void)head_dim;
+  if (batch < 1 || heads < 1 || seq_len < 1) return 0;
+  return (size_t)(batch * heads * ceil_div(seq_len, 32)) * 2 * sizeof(float);
+}
+
+int32_t tda_validate_fwd(const tda_fwd_args* a) {
+  if (!a) return TDA_ERR_NULL_POINTER;
+  int32_t rc = check_common(common_of(*a));
+  if (rc) return rc;
+  const int64_t eb = a->dtype == TDA_DTYPE_BF16 ? 2 : 4;
+  const tda_tensor* ts[] = {&a->q1, &a->k1, &a->v, &a->out, &a->q2, &a->k2};
+  const int n = a->branches == 2 ? 6 : 4;
+  for (int k = 0; k < n; ++k)
+    if ((rc = check_tensor(*ts[k], eb))) return rc;
+  return TDA_OK;
+}
+
+int32_t tda_validate_bwd(const tda_bwd_args* a) {
+  if (!a) return TDA_ERR_NULL_POINTER;
+  int32_t rc = check_common(common_of(*a));
+  if (rc) return rc;
+  const int64_t eb = a->dtype == TDA_DTYPE_BF16 ? 2 : 4;
+  const tda_tensor* ts[] = {&a->q1, &a->k1, &a->v, &a->dout, &a->dq1, &a->dk1, &a->dv, &a->q2, &a->k2, &a->dq2,
+                            &a->dk2};
+  const int n = a->branches == 2 ? 11 : 7;
+  for (int k = 0; k < n; ++k)
+    if ((rc = check_tensor(*ts[k], eb))) return rc;
+  if (a->normalize && !a->norms) return TDA_ERR_NORMS;
+  if (!a->workspace ||
+      a->workspace_bytes < tda_bwd_workspace_bytes(a->batch, a->heads, a->seq_len, a->head_dim))
+    return TDA_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0) return TDA_ERR_WORKSPACE;
+  return TDA_OK;
+}
+
+int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
+  int32_t rc = tda_validate_fwd(a);
+  if (rc) return rc;
+  tda::FwdParams p;
+  std::memset(&p, 0, sizeof(p));
+  const tda_tensor* in[5] = {&a->q1, &a->k1, &a->q2, &a->k2, &a->v};
+  const bool two = a->branches == 2;
+  for (int k = 0; k < 5; ++k) {
+    const tda_tensor& t = (!two && (k == 2 || k == 3)) ? *in[k - 2] : *in[k];
+    p.in[k] = t.data;
+    copy_strides(p.s[k], t);
+  }
+  p.out = a->out.data;
+  copy_strides(p.s[tda::F_OUT], a->out);
+  p.B = (int)a->batch;
+  p.H = (int)a->heads;
+  p.N = (int)a->seq_len;
+  p.nqt = (int)ceil_div(a->seq_len, 32);
+  p.occ_w = (int)ceil_div(p.nqt, 32);
+  p.p = a->relu_power;
+  p.inv_d = 1.0f / (float)a->head_dim;
+  p.beta = a->beta;
+  p.lam = a->lambda_param;
+  p.norms = a->normalize ? a->norms : nullptr;
+  p.occ = a->occupancy;
+  p.stats = a->stats;
+  const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};
+  const int e = tda::launch_fwd(p, key, stream);
+  if (e != 0) {
+    g_last_hip_error = e;
+    return TDA_ERR_HIP;
+  }
+  return TDA_OK;
+}
+
+int32_t tda_bwd(const tda_bwd_args* a, void* stream) {
+  int32_t rc = tda_validate_bwd(a);
+  if (rc) return rc;
+  tda::BwdParams p;
+  std::memset(&p, 0, sizeof(p));
+  const bool two = a->branches == 2;
+  const tda_tensor* in[6] = {&a->q1, &a->k1, &a->q2, &a->k2, &a->v, &a->dout};
+  for (int k = 0; k < 6; ++k) {
+    const tda_tensor& t = (!two && (k == 2 || k == 3)) ? *in[k - 2] : *in[k];
+    p.in[k] = t.data;
+    copy_strides(p.s[k], t);
+  }
+  // Single-branch calls alias the second-branch gradient slots to the first: the kernels
+  // never write them when branches == 1.
+  const tda_tensor* gr[5] = {&a->dq1, &a->dk1, &a->dq2, &a->dk2, &a->dv};
+  for (int k = 0; k < 5; ++k) {
+    const tda_tensor& t = (!two && (k == 2 || k == 3)) ? *gr[k - 2] : *gr[k];
+    p.grad[k] = t.data;
+    copy_strides(p.s[tda::B_DQ1 + k], t);
+  }
+  p.B = (int)a->batch;
+  p.H = (int)a->heads;
+  p.N = (int)a->seq_len;
+  p.nqt = (int)ceil_div(a->seq_len, 32);
+  p.occ_w = (int)ceil_div(p.nqt, 32);
+  p.p = a->relu_power;
+  p.inv_d = 1.0f / (float)a->head_dim;
+  p.beta = a->beta;
+  p.lam = a->lambda_param;
+  p.dbeta = a->dbeta;
+  p.dlam = a->dlambda;
+  p.norms = a->normalize ? a->norms : nullptr;
+  p.occ = a->occupancy;
+  p.ws = static_cast<float*>(a->workspace);
+  p.stats = a->stats;
+  const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};
+  const int e = tda::launch_bwd(p, key, stream);
+  if (e != 0) {
+    g_last_hip_error = e;
+    return TDA_ERR_HIP;
+  }
+  return TDA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+// tda_params.hpp -- kernel argument blocks passed by value from the host launcher to the
+// gfx950 kernels, plus the launcher entry points each kernel file exports.
+#pragma once
+
+#include <stdint.h>
+
+namespace tda {
+
+// Tensor slots in the stride table.
+enum FwdSlot { F_Q1 = 0, F_K1, F_Q2, F_K2, F_V, F_OUT, F_NSLOT };
+enum BwdSlot { B_Q1 = 0, B_K1, B_Q2, B_K2, B_V, B_DO, B_DQ1, B_DK1, B_DQ2, B_DK2, B_DV, B_NSLOT };
+
+// Row-norm table layout: [slot][B*H][N] with slot 0 = q1, 1 = k1, 2 = q2, 3 = k2.
+enum NormSlot { N_Q1 = 0, N_K1 = 1, N_Q2 = 2, N_K2 = 3 };
+
+struct FwdParams {
+  const void* in[5];         // q1, k1, q2, k2, v
+  void* out;
+  int64_t s[F_NSLOT][3];     // batch, head, sequence strides in elements
+  int B, H, N;
+  int nqt;                   // ceil(N / 32): query tiles == key tiles
+  int occ_w;                 // bitmask words per query tile: ceil(nqt / 32)
+  float p;                   // relu_power
+  float inv_d;               // 1 / head_dim
+  const float* beta;
+  const float* lam;
+  float* norms;              // may be null
+  uint32_t* occ;             // may be null
+  unsigned long long* stats; // may be null
+};
+
+struct BwdParams {
+  const void* in[6];         // q1, k1, q2, k2, v, dout
+  void* grad[5];             // dq1, dk1, dq2, dk2, dv
+  int64_t s[B_NSLOT][3];
+  int B, H, N;
+  int nqt, occ_w;
+  float p, inv_d;
+  const float* beta;
+  const float* lam;
+  float* dbeta;
+  float* dlam;
+  const float* norms;
+  const uint32_t* occ;       // may be null: every causal tile is tested
+  float* ws;                 // [BH * nqt][2] dbeta / dlambda partials of the dQ pass
+  unsigned long long* stats;
+};
+
+// Kernel-family launchers (return a hipError_t value).  Template selection happens inside.
+struct KernelKey {
+  int dtype;      // 0 f32, 1 bf16
+  int d;          // 64 or 128
+  int branches;   // 1 or 2
+  int pkind;      // 2: p == 2, 1: p == 1, 0: general
+  int normalize;  // 0 or 1
+};
+
+int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream);
+int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
+
+}  // namespace tda

@@ -1,0 +1,180 @@
+"""Host side of the threshold-attention operator: tensor checks, buffer allocation, the C-ABI
+calls and the autograd.Function.
+
+Mirrors ThresholdRelaFunction of the reference (snap-research/TDA
+triton_threshold_attention.py, TTA:327-469) with these differences:
+  * one Function covers both the single-branch (TRA) and the fused two-branch (TDA) form;
+  * beta and lambda are device tensors read by the kernels: no .item() sync (TTA:352);
+  * inputs are neither up-cast nor copied (TTA:356-360); bf16 stays bf16 with fp32
+    accumulation, fp32 stays fp32 (float16 and float64 are computed in fp32 and cast back,
+    as the reference does for every dtype);
+  * the backward also returns d beta and d lambda (the reference returns None, TTA:469);
+  * the forward saves the inputs, the inverse row norms and a tile-occupancy bitmask instead
+    of fp32 copies of q, k, v (TTA:396).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _abi
+
+_NATIVE = {torch.float32: _abi.DTYPE_F32, torch.bfloat16: _abi.DTYPE_BF16}
+
+
+def _tensor(t: torch.Tensor | None) -> _abi.TdaTensor:
+    x = _abi.TdaTensor()
+    if t is None:
+        return x
+    x.data = t.data_ptr()
+    for k in range(4):
+        x.stride[k] = t.stride(k)
+    return x
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _usable(t: torch.Tensor) -> torch.Tensor:
+    """Return t itself when the kernels can read it in place (last-dim stride 1, 16-byte
+    aligned base and strides), else a contiguous copy."""
+    es = t.element_size()
+    ok = (t.stride(3) == 1 and t.data_ptr() % 16 == 0
+          and all(s >= 0 and (s * es) % 16 == 0 for s in t.stride()[:3]))
+    return t if ok else t.contiguous()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_inputs(tensors, names):
+    ref = tensors[0]
+    if ref.dim() != 4:
+        raise ValueError(f"{names[0]} must have shape (batch, heads, seq_len, head_dim), got {tuple(ref.shape)}")
+    for t, n in zip(tensors, names):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{n} must be a torch.Tensor")
+        if t.shape != ref.shape:
+            raise ValueError(f"shape mismatch: {names[0]} {tuple(ref.shape)} vs {n} {tuple(t.shape)}")
+        if t.dtype != ref.dtype:
+            raise ValueError(f"dtype mismatch: {names[0]} {ref.dtype} vs {n} {t.dtype}")
+        if t.device != ref.device:
+            raise ValueError(f"device mismatch: {names[0]} {ref.device} vs {n} {t.device}")
+    if ref.device.type != "cuda":
+        raise ValueError(f"tda_amd runs on the GPU only (HIP); got tensors on {ref.device}")
+    if not ref.dtype.is_floating_point:
+        raise ValueError(f"floating-point inputs required, got {ref.dtype}")
+
+
+def _common(args, t: torch.Tensor, branches: int, normalize: bool, relu_power: float):
+    b, h, n, d = t.shape
+    args.abi_version = _abi.ABI_VERSION
+    args.dtype = _NATIVE[t.dtype]
+    args.branches = branches
+    args.normalize = 1 if normalize else 0
+    args.causal = 1
+    args.relu_power = float(relu_power)
+    args.batch, args.heads, args.seq_len, args.head_dim = b, h, n, d
+
+
+def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, branches: int,
+            norms=None, occupancy=None, stats=None) -> torch.Tensor:
+    """One forward launch.  Tensors must already be in a native dtype (float32 / bfloat16)
+    on one device; beta (and lam) are 0-dim float32 tensors on that device.  The optional
+    norms / occupancy / stats buffers receive the side outputs described in include/tda.h."""
+    lib = _abi.load()
+    q1, k1, v = _usable(q1), _usable(k1), _usable(v)
+    if branches == 2:
+        q2, k2 = _usable(q2), _usable(k2)
+    out = torch.empty(q1.shape, dtype=q1.dtype, device=q1.device)
+    a = _abi.TdaFwdArgs()
+    _common(a, q1, branches, normalize, relu_power)
+    a.q1, a.k1, a.v, a.out = _tensor(q1), _tensor(k1), _tensor(v), _tensor(out)
+    if branches == 2:
+        a.q2, a.k2 = _tensor(q2), _tensor(k2)
+    a.beta = _ptr(beta)
+    a.lambda_param = _ptr(lam) if branches == 2 else None
+    a.norms, a.occupancy, a.stats = _ptr(norms), _ptr(occupancy), _ptr(stats)
+    with torch.cuda.device(q1.device):
+        _abi.check(lib.tda_fwd(ctypes.byref(a), _stream(q1.device)), "tda_fwd")
+    return out
+
+
+def backward(q1, k1, q2, k2, v, dout, beta, lam, relu_power: float, normalize: bool,
+             branches: int, norms=None, occupancy=None, stats=None):
+    """One backward launch: returns (dq1, dk1, dq2, dk2, dv, dbeta, dlambda); the branch-2
+    entries and dlambda are None when branches == 1."""
+    lib = _abi.load()
+    q1, k1, v, dout = _usable(q1), _usable(k1), _usable(v), _usable(dout)
+    if branches == 2:
+        q2, k2 = _usable(q2), _usable(k2)
+    dev = q1.device
+    dq1, dk1, dv = (torch.empty(q1.shape, dtype=q1.dtype, device=dev) for _ in range(3))
+    dq2 = dk2 = dlam = None
+    if branches == 2:
+        dq2, dk2 = (torch.empty(q1.shape, dtype=q1.dtype, device=dev) for _ in range(2))
+        dlam = torch.empty((), dtype=torch.float32, device=dev)
+    dbeta = torch.empty((), dtype=torch.float32, device=dev)
+    b, h, n, d = q1.shape
+    ws_bytes = lib.tda_bwd_workspace_bytes(b, h, n, d)
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev)
+    a = _abi.TdaBwdArgs()
+    _common(a, q1, branches, normalize, relu_power)
+    a.q1, a.k1, a.v, a.dout = _tensor(q1), _tensor(k1), _tensor(v), _tensor(dout)
+    a.dq1, a.dk1, a.dv = _tensor(dq1), _tensor(dk1), _tensor(dv)
+    if branches == 2:
+        a.q2, a.k2, a.dq2, a.dk2 = _tensor(q2), _tensor(k2), _tensor(dq2), _tensor(dk2)
+    a.beta = _ptr(beta)
+    a.lambda_param = _ptr(lam) if branches == 2 else None
+    a.dbeta, a.dlambda = _ptr(dbeta), _ptr(dlam)
+    a.norms, a.occupancy = _ptr(norms), _ptr(occupancy)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
+    a.stats = _ptr(stats)
+    with torch.cuda.device(dev):
+        _abi.check(lib.tda_bwd(ctypes.byref(a), _stream(dev)), "tda_bwd")
+    return dq1, dk1, dq2, dk2, dv, dbeta, dlam
+
+
+def side_buffers(shape, branches: int, normalize: bool, device):
+    """Allocate the forward's norms and occupancy outputs (uninitialised: the forward writes
+    every element)."""
+    lib = _abi.load()
+    b, h, n, _ = shape
+    occ = torch.empty(lib.tda_occupancy_words(b, h, n), dtype=torch.int32, device=device)
+    norms = (torch.empty(lib.tda_norms_floats(b, h, n, branches), dtype=torch.float32, device=device)
+             if normalize else None)
+    return norms, occ
+
+
+class TDAFunction(torch.autograd.Function):
+    """Autograd node for TRA (branches == 1) and fused TDA (branches == 2).
+
+    forward(ctx, q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches):
+    q2, k2, lam are None when branches == 1; beta / lam are 0-dim float32 device tensors."""
+
+    @staticmethod
+    def forward(ctx, q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches):
+        need = any(ctx.needs_input_grad[:7])
+        norms = occ = None
+        if need:
+            norms, occ = side_buffers(q1.shape, branches, normalize, q1.device)
+        out = forward(q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches, norms, occ)
+        ctx.save_for_backward(q1, k1, q2, k2, v, beta, lam, norms, occ)
+        ctx.cfg = (float(relu_power), bool(normalize), int(branches))
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q1, k1, q2, k2, v, beta, lam, norms, occ = ctx.saved_tensors
+        relu_power, normalize, branches = ctx.cfg
+        dout = dout.to(q1.dtype)
+        dq1, dk1, dq2, dk2, dv, dbeta, dlam = backward(
+            q1, k1, q2, k2, v, dout, beta, lam, relu_power, normalize, branches, norms, occ)
+        ng = ctx.needs_input_grad
+        return (dq1 if ng[0] else None, dk1 if ng[1] else None,
+                dq2 if ng[2] else None, dk2 if ng[3] else None,
+                dv if ng[4] else None, dbeta if ng[5] else None,
+                dlam if (branches == 2 and ng[6]) else None, None, None, None)

@@ -1,0 +1,235 @@
+"""C-ABI tests that need no GPU: the library loads, exports every function include/tda.h
+declares, the ctypes mirror matches the C struct layout, and every invalid argument maps to
+its error code without touching a device."""
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+import torch
+
+from tda_amd import _abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tda.h")
+
+
+def _lib():
+    if not os.path.exists(_abi.lib_path()):
+        pytest.skip("libtda_hip.so not built (python -m tda_amd.build)")
+    return _abi.load()
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(tda_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_expected_api():
+    names = _declared_functions()
+    assert set(names) == set(_abi.SIGNATURES), names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.tda_abi_version() == _abi.ABI_VERSION
+
+
+def test_struct_layout_matches_c_header(tmp_path):
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc missing")
+    fields = {
+        "tda_fwd_args": _abi.TdaFwdArgs, "tda_bwd_args": _abi.TdaBwdArgs, "tda_tensor": _abi.TdaTensor,
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+    for cname, py in fields.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {}
+    for ln in out:
+        if ln:
+            c, f, v = ln.split()
+            got[(c, f)] = int(v)
+    for cname, py in fields.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for f, _ in py._fields_:
+            assert got[(cname, f)] == getattr(py, f).offset, (cname, f)
+
+
+FAKE = 0x10000  # aligned, never dereferenced: validation is host-only
+
+
+def _tensor(shape, es=2, strides=None):
+    t = _abi.TdaTensor()
+    t.data = FAKE
+    b, h, n, d = shape
+    st = strides or (h * n * d, n * d, d, 1)
+    for k in range(4):
+        t.stride[k] = st[k]
+    return t
+
+
+def _fwd_args(shape=(2, 3, 100, 128), branches=2, dtype=_abi.DTYPE_BF16):
+    a = _abi.TdaFwdArgs()
+    a.abi_version, a.dtype, a.branches, a.normalize, a.causal = _abi.ABI_VERSION, dtype, branches, 1, 1
+    a.relu_power = 2.0
+    a.batch, a.heads, a.seq_len, a.head_dim = shape
+    for f in ("q1", "k1", "q2", "k2", "v", "out"):
+        setattr(a, f, _tensor(shape))
+    a.beta = FAKE
+    a.lambda_param = FAKE
+    return a
+
+
+def _bwd_args(shape=(2, 3, 100, 128), branches=2):
+    lib = _lib()
+    a = _abi.TdaBwdArgs()
+    a.abi_version, a.dtype, a.branches, a.normalize, a.causal = _abi.ABI_VERSION, _abi.DTYPE_BF16, branches, 1, 1
+    a.relu_power = 2.0
+    a.batch, a.heads, a.seq_len, a.head_dim = shape
+    for f in ("q1", "k1", "q2", "k2", "v", "dout", "dq1", "dk1", "dq2", "dk2", "dv"):
+        setattr(a, f, _tensor(shape))
+    a.beta = a.lambda_param = a.norms = FAKE
+    a.workspace = FAKE
+    a.workspace_bytes = lib.tda_bwd_workspace_bytes(*shape)
+    return a
+
+
+def test_valid_args_pass():
+    lib = _lib()
+    assert lib.tda_validate_fwd(ctypes.byref(_fwd_args())) == _abi.OK
+    assert lib.tda_validate_fwd(ctypes.byref(_fwd_args(branches=1, dtype=_abi.DTYPE_F32))) == _abi.OK
+    assert lib.tda_validate_bwd(ctypes.byref(_bwd_args())) == _abi.OK
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (lambda a: setattr(a, "abi_version", 99), _abi.ERR_ABI),
+    (lambda a: setattr(a, "dtype", 7), _abi.ERR_DTYPE),
+    (lambda a: setattr(a, "branches", 3), _abi.ERR_BRANCHES),
+    (lambda a: setattr(a, "causal", 0), _abi.ERR_CAUSAL),
+    (lambda a: setattr(a, "head_dim", 96), _abi.ERR_HEAD_DIM),
+    (lambda a: setattr(a, "head_dim", 256), _abi.ERR_HEAD_DIM),
+    (lambda a: setattr(a, "seq_len", 0), _abi.ERR_SHAPE),
+    (lambda a: setattr(a, "batch", 0), _abi.ERR_SHAPE),
+    (lambda a: setattr(a, "relu_power", -1.0), _abi.ERR_POWER),
+    (lambda a: setattr(a, "relu_power", float("nan")), _abi.ERR_POWER),
+    (lambda a: setattr(a, "relu_power", float("inf")), _abi.ERR_POWER),
+    (lambda a: setattr(a, "beta", None), _abi.ERR_NULL_POINTER),
+    (lambda a: setattr(a, "lambda_param", None), _abi.ERR_NULL_POINTER),
+    (lambda a: setattr(a.q2, "data", None), _abi.ERR_NULL_POINTER),
+    (lambda a: setattr(a.out, "data", None), _abi.ERR_NULL_POINTER),
+    (lambda a: a.v.stride.__setitem__(3, 2), _abi.ERR_LAYOUT),
+    (lambda a: a.k1.stride.__setitem__(2, 129), _abi.ERR_LAYOUT),
+    (lambda a: a.q1.stride.__setitem__(0, -128), _abi.ERR_LAYOUT),
+    (lambda a: setattr(a.q1, "data", FAKE + 2), _abi.ERR_LAYOUT),
+])
+def test_fwd_validator_rejects(mutate, code):
+    lib = _lib()
+    a = _fwd_args()
+    mutate(a)
+    assert lib.tda_validate_fwd(ctypes.byref(a)) == code
+    assert lib.tda_fwd(ctypes.byref(a), None) == code  # rejected before any launch
+
+
+def test_single_branch_ignores_second_branch_pointers():
+    lib = _lib()
+    a = _fwd_args(branches=1)
+    a.q2.data = None
+    a.lambda_param = None
+    assert lib.tda_validate_fwd(ctypes.byref(a)) == _abi.OK
+
+
+def test_zero_strides_are_layout_valid():
+    # an expanded (broadcast) tensor: all-zero strides except the unit last-dim stride
+    lib = _lib()
+    a = _bwd_args()
+    for k in range(3):
+        a.dout.stride[k] = 0
+    assert lib.tda_validate_bwd(ctypes.byref(a)) == _abi.OK
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (lambda a: setattr(a, "norms", None), _abi.ERR_NORMS),
+    (lambda a: setattr(a, "workspace", None), _abi.ERR_WORKSPACE),
+    (lambda a: setattr(a, "workspace_bytes", 8), _abi.ERR_WORKSPACE),
+    (lambda a: setattr(a.dk2, "data", None), _abi.ERR_NULL_POINTER),
+    (lambda a: setattr(a.dout, "data", None), _abi.ERR_NULL_POINTER),
+    (lambda a: setattr(a, "head_dim", 32), _abi.ERR_HEAD_DIM),
+])
+def test_bwd_validator_rejects(mutate, code):
+    lib = _lib()
+    a = _bwd_args()
+    mutate(a)
+    assert lib.tda_validate_bwd(ctypes.byref(a)) == code
+    assert lib.tda_bwd(ctypes.byref(a), None) == code
+
+
+def test_bwd_norms_optional_without_normalize():
+    lib = _lib()
+    a = _bwd_args()
+    a.normalize = 0
+    a.norms = None
+    assert lib.tda_validate_bwd(ctypes.byref(a)) == _abi.OK
+
+
+def test_buffer_sizes():
+    lib = _lib()
+    assert lib.tda_occupancy_words(4, 16, 4096) == 64 * 128 * 4
+    assert lib.tda_occupancy_words(1, 1, 1) == 1
+    assert lib.tda_occupancy_words(1, 1, 33) == 2
+    assert lib.tda_norms_floats(4, 16, 4096, 2) == 4 * 64 * 4096
+    assert lib.tda_norms_floats(1, 8, 128, 1) == 2 * 8 * 128
+    assert lib.tda_bwd_workspace_bytes(4, 16, 4096, 128) == 64 * 128 * 2 * 4
+    assert lib.tda_occupancy_words(0, 1, 1) == 0
+
+
+def test_error_strings():
+    lib = _lib()
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11, -100):
+        s = lib.tda_error_string(code).decode()
+        assert s and s != "unknown error", code
+    assert lib.tda_error_string(-55).decode() == "unknown error"
+
+
+# ------------------------------------------------------------- Python boundary
+def test_cpu_tensors_rejected_no_fallback():
+    from tda_amd import differential_threshold_rela_triton, threshold_rela_triton
+    x = torch.randn(1, 1, 8, 64)
+    with pytest.raises(ValueError, match="GPU only"):
+        threshold_rela_triton(x, x, x, 1.0)
+    with pytest.raises(ValueError, match="GPU only"):
+        differential_threshold_rela_triton(x, x, x, x, x, 1.0, 0.5)
+
+
+def test_shape_mismatch_rejected():
+    from tda_amd import threshold_rela_triton
+    with pytest.raises(ValueError, match="shape mismatch"):
+        threshold_rela_triton(torch.randn(1, 1, 8, 64), torch.randn(1, 1, 9, 64), torch.randn(1, 1, 8, 64), 1.0)
+    with pytest.raises(ValueError, match="batch, heads, seq_len, head_dim"):
+        threshold_rela_triton(torch.randn(8, 64), torch.randn(8, 64), torch.randn(8, 64), 1.0)
+
+
+def test_missing_library_is_a_clear_error(tmp_path):
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        _abi.load(str(tmp_path / "nope.so"))
+
+
+def test_error_code_mapping():
+    _lib()
+    with pytest.raises(ValueError, match="head_dim"):
+        _abi.check(_abi.ERR_HEAD_DIM, "tda_fwd")
+    with pytest.raises(RuntimeError, match="launch failed"):
+        _abi.check(_abi.ERR_HIP, "tda_fwd")
+    _abi.check(_abi.OK, "tda_fwd")
