@@ -88,14 +88,17 @@ typedef struct tda_fwd_args {
   tda_tensor out;                 /* output, same dtype as the inputs */
   const float* beta;        /* device scalar */
   const float* lambda_param;/* device scalar, raw (clamped on device); branches == 2 */
-  /* optional outputs for the backward pass (may be NULL): */
   float*    norms;          /* [2*branches][B*H][N] inverse row norms 1/max(|x|,1e-12)
-                               of q1, k1 (, q2, k2); written when normalize == 1 */
-  uint32_t* occupancy;      /* tile-occupancy bitmask, tda_occupancy_words() words:
-                               bit (qt, kt) set when any A_ij != 0 in the 32x32 tile
-                               of query tile qt and key tile kt */
-  unsigned long long* stats;/* [0] += causal 32x32 tiles visited,
-                               [1] += tiles whose A.V product was computed */
+                               of q1, k1 (, q2, k2); required and written when
+                               normalize == 1 (the backward pass reads them), else unused */
+  /* optional outputs (may be NULL): */
+  uint32_t* occupancy;      /* tile-occupancy bitmask, tda_occupancy_words() words laid
+                               out [branch][B*H][query tile][ceil(tiles/32)]: bit kt of
+                               row (branch, bh, qt) is set when some A_ij of that branch is
+                               non-zero in the 32x32 tile (query tile qt, key tile kt) */
+  unsigned long long* stats;/* [0] += (query tile, key tile, branch) triples on or below
+                               the diagonal, [1] += those with a non-zero weight tile
+                               (A.V issued); tiles are 32x32 */
 } tda_fwd_args;
 
 typedef struct tda_bwd_args {
@@ -130,7 +133,7 @@ int32_t tda_validate_fwd(const tda_fwd_args* args);
 int32_t tda_validate_bwd(const tda_bwd_args* args);
 
 /* Buffer sizes for the optional forward outputs and the backward workspace. */
-size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len);
+size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 size_t tda_norms_floats(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim);
 

@@ -80,7 +80,7 @@ SIGNATURES = {
     "tda_last_hip_error": (ctypes.c_int32, []),
     "tda_validate_fwd": (ctypes.c_int32, [ctypes.POINTER(TdaFwdArgs)]),
     "tda_validate_bwd": (ctypes.c_int32, [ctypes.POINTER(TdaBwdArgs)]),
-    "tda_occupancy_words": (ctypes.c_size_t, [ctypes.c_int64] * 3),
+    "tda_occupancy_words": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
     "tda_norms_floats": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
     "tda_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4),
     "tda_fwd": (ctypes.c_int32, [ctypes.POINTER(TdaFwdArgs), ctypes.c_void_p]),

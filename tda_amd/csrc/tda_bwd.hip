@@ -157,11 +157,16 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
   float bsum = 0.f, lsum = 0.f;
   unsigned visited = 0, computed = 0;
   const uint32_t* occrow = P.occ ? P.occ + ((int64_t)bh * P.nqt + qt) * P.occ_w : nullptr;
+  const int64_t occ_br = (int64_t)BH * P.nqt * P.occ_w;  // branch-plane distance of the bitmask
   const float* nk1 = NORM ? P.norms + ((int64_t)N_K1 * BH + bh) * N : nullptr;
   const float* nk2 = NORM ? P.norms + ((int64_t)N_K2 * BH + bh) * N : nullptr;
 
   for (int kt = 0; kt <= qt; ++kt) {
-    if (occrow && !((occrow[kt >> 5] >> (kt & 31)) & 1u)) continue;
+    if (occrow) {  // tile holds a non-zero score of either branch?
+      uint32_t w = occrow[kt >> 5];
+      if constexpr (BR == 2) w |= occrow[occ_br + (kt >> 5)];
+      if (!((w >> (kt & 31)) & 1u)) continue;
+    }
     ++visited;
     const int k0 = kt * 32;
     const int j = k0 + n32;
@@ -316,9 +321,14 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
   for (int c = 0; c < ND; ++c) { AV[c] = f32x16{}; AK1[c] = f32x16{}; AK2[c] = f32x16{}; }
   unsigned visited = 0, computed = 0;
   const uint32_t* occcol = P.occ ? P.occ + (int64_t)bh * P.nqt * P.occ_w + (kt >> 5) : nullptr;
+  const int64_t occ_br = (int64_t)BH * P.nqt * P.occ_w;  // branch-plane distance of the bitmask
 
   for (int qt = kt; qt < P.nqt; ++qt) {
-    if (occcol && !((occcol[(int64_t)qt * P.occ_w] >> (kt & 31)) & 1u)) continue;
+    if (occcol) {  // tile holds a non-zero score of either branch?
+      uint32_t w = occcol[(int64_t)qt * P.occ_w];
+      if constexpr (BR == 2) w |= occcol[occ_br + (int64_t)qt * P.occ_w];
+      if (!((w >> (kt & 31)) & 1u)) continue;
+    }
     ++visited;
     const int q0 = qt * 32;
     const int ia = q0 + n32;  // query row this lane loads for the A operand

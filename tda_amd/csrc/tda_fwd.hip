@@ -84,8 +84,10 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
 #pragma unroll
   for (int c = 0; c < ND; ++c) O[c] = f32x16{};
 
+  // bitmask rows [branch][B*H][query tile][word] of this query tile
   uint32_t* occrow = P.occ ? P.occ + ((int64_t)bh * P.nqt + qt) * P.occ_w : nullptr;
-  uint32_t word = 0;
+  const int64_t occ_br = (int64_t)BH * P.nqt * P.occ_w;  // distance between the branch planes
+  uint32_t word = 0, word2 = 0;
   unsigned visited = 0, computed = 0;
 
   for (int kt = 0; kt <= qt; ++kt) {
@@ -135,12 +137,14 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
         m2 = fmaxf(m2, valid ? S2[r] : -INFINITY);
       }
     }
-    bool act = __builtin_fmaf(m1, rq1, -tau) > 0.f;
-    if constexpr (BR == 2) act = act || (__builtin_fmaf(m2, rq2, -tau) > 0.f);
-    ++visited;
-    if (wave_ballot(act) != 0ull) {
-      ++computed;
-      word |= 1u << (kt & 31);
+    const bool any1 = wave_ballot(__builtin_fmaf(m1, rq1, -tau) > 0.f) != 0ull;
+    bool any2 = false;
+    if constexpr (BR == 2) any2 = wave_ballot(__builtin_fmaf(m2, rq2, -tau) > 0.f) != 0ull;
+    visited += BR;
+    computed += (any1 ? 1 : 0) + (any2 ? 1 : 0);
+    if (any1) word |= 1u << (kt & 31);
+    if (any2) word2 |= 1u << (kt & 31);
+    if (any1 || any2) {
       f32x16 C;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -169,12 +173,18 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
       if constexpr (sizeof(T) == 2) wave_lds_sync();
     }
     if (occrow && (((kt & 31) == 31) || kt == qt)) {
-      if (l == 0) occrow[kt >> 5] = word;
-      word = 0;
+      if (l == 0) {
+        occrow[kt >> 5] = word;
+        if constexpr (BR == 2) occrow[occ_br + (kt >> 5)] = word2;
+      }
+      word = word2 = 0;
     }
   }
   if (occrow && l == 0) {
-    for (int w = (qt >> 5) + 1; w < P.occ_w; ++w) occrow[w] = 0u;
+    for (int w = (qt >> 5) + 1; w < P.occ_w; ++w) {
+      occrow[w] = 0u;
+      if constexpr (BR == 2) occrow[occ_br + w] = 0u;
+    }
   }
 
   if (qvalid) {
@@ -221,8 +231,9 @@ static int sel_d(const FwdParams& p, const KernelKey& k, void* s) {
   return k.d == 128 ? sel_br<Pol, 128>(p, k, s) : sel_br<Pol, 64>(p, k, s);
 }
 
+// bf16 runs the LDS-staged kernel (tda_fwd_fast.hip); fp32 runs fwd_wave.
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream) {
-  return k.dtype == 1 ? sel_d<PolBF16>(p, k, stream) : sel_d<PolF32>(p, k, stream);
+  return k.dtype == 1 ? launch_fwd_fast(p, k, stream) : sel_d<PolF32>(p, k, stream);
 }
 
 }  // namespace tda

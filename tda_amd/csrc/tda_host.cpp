@@ -88,16 +88,16 @@ const char* tda_error_string(int32_t code) {
     case TDA_ERR_WORKSPACE: return "backward workspace missing or too small";
     case TDA_ERR_ABI: return "abi_version mismatch";
     case TDA_ERR_CAUSAL: return "only the causal form is implemented (causal must be 1)";
-    case TDA_ERR_NORMS: return "normalize requires the forward pass's norms buffer";
+    case TDA_ERR_NORMS: return "normalize requires the norms buffer (forward: output, backward: the forward's output)";
     case TDA_ERR_HIP: return "HIP kernel launch failed";
     default: return "unknown error";
   }
 }
 
-size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len) {
-  if (batch < 1 || heads < 1 || seq_len < 1) return 0;
+size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches) {
+  if (batch < 1 || heads < 1 || seq_len < 1 || (branches != 1 && branches != 2)) return 0;
   const int64_t nqt = ceil_div(seq_len, 32);
-  return (size_t)(batch * heads * nqt * ceil_div(nqt, 32));
+  return (size_t)(branches * batch * heads * nqt * ceil_div(nqt, 32));
 }
 
 size_t tda_norms_floats(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches) {
@@ -120,6 +120,7 @@ int32_t tda_validate_fwd(const tda_fwd_args* a) {
   const int n = a->branches == 2 ? 6 : 4;
   for (int k = 0; k < n; ++k)
     if ((rc = check_tensor(*ts[k], eb))) return rc;
+  if (a->normalize && !a->norms) return TDA_ERR_NORMS;
   return TDA_OK;
 }
 

@@ -56,6 +56,7 @@ struct KernelKey {
 };
 
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream);
+int launch_fwd_fast(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
 
 }  // namespace tda

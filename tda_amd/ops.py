@@ -97,6 +97,8 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
         a.q2, a.k2 = _tensor(q2), _tensor(k2)
     a.beta = _ptr(beta)
     a.lambda_param = _ptr(lam) if branches == 2 else None
+    if normalize and norms is None:  # scratch: the kernels need the row norms either way
+        norms = torch.empty(lib.tda_norms_floats(*q1.shape[:3], branches), dtype=torch.float32, device=q1.device)
     a.norms, a.occupancy, a.stats = _ptr(norms), _ptr(occupancy), _ptr(stats)
     with torch.cuda.device(q1.device):
         _abi.check(lib.tda_fwd(ctypes.byref(a), _stream(q1.device)), "tda_fwd")
@@ -143,7 +145,7 @@ def side_buffers(shape, branches: int, normalize: bool, device):
     every element)."""
     lib = _abi.load()
     b, h, n, _ = shape
-    occ = torch.empty(lib.tda_occupancy_words(b, h, n), dtype=torch.int32, device=device)
+    occ = torch.empty(lib.tda_occupancy_words(b, h, n, branches), dtype=torch.int32, device=device)
     norms = (torch.empty(lib.tda_norms_floats(b, h, n, branches), dtype=torch.float32, device=device)
              if normalize else None)
     return norms, occ

@@ -90,6 +90,7 @@ def _fwd_args(shape=(2, 3, 100, 128), branches=2, dtype=_abi.DTYPE_BF16):
         setattr(a, f, _tensor(shape))
     a.beta = FAKE
     a.lambda_param = FAKE
+    a.norms = FAKE
     return a
 
 
@@ -134,6 +135,7 @@ def test_valid_args_pass():
     (lambda a: a.k1.stride.__setitem__(2, 129), _abi.ERR_LAYOUT),
     (lambda a: a.q1.stride.__setitem__(0, -128), _abi.ERR_LAYOUT),
     (lambda a: setattr(a.q1, "data", FAKE + 2), _abi.ERR_LAYOUT),
+    (lambda a: setattr(a, "norms", None), _abi.ERR_NORMS),
 ])
 def test_fwd_validator_rejects(mutate, code):
     lib = _lib()
@@ -186,13 +188,15 @@ def test_bwd_norms_optional_without_normalize():
 
 def test_buffer_sizes():
     lib = _lib()
-    assert lib.tda_occupancy_words(4, 16, 4096) == 64 * 128 * 4
-    assert lib.tda_occupancy_words(1, 1, 1) == 1
-    assert lib.tda_occupancy_words(1, 1, 33) == 2
+    assert lib.tda_occupancy_words(4, 16, 4096, 2) == 2 * 64 * 128 * 4
+    assert lib.tda_occupancy_words(4, 16, 4096, 1) == 64 * 128 * 4
+    assert lib.tda_occupancy_words(1, 1, 1, 1) == 1
+    assert lib.tda_occupancy_words(1, 1, 33, 2) == 4
+    assert lib.tda_occupancy_words(1, 1, 33, 3) == 0
     assert lib.tda_norms_floats(4, 16, 4096, 2) == 4 * 64 * 4096
     assert lib.tda_norms_floats(1, 8, 128, 1) == 2 * 8 * 128
     assert lib.tda_bwd_workspace_bytes(4, 16, 4096, 128) == 64 * 128 * 2 * 4
-    assert lib.tda_occupancy_words(0, 1, 1) == 0
+    assert lib.tda_occupancy_words(0, 1, 1, 1) == 0
 
 
 def test_error_strings():

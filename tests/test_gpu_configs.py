@@ -119,7 +119,7 @@ def test_c4_long_context(p):
         assert rel_err(o, r) <= 2e-2
     visited, computed = (int(x) for x in stats.tolist())
     nt = 16384 // 32
-    assert visited == 32 * nt * (nt + 1) // 2
+    assert visited == 2 * 32 * nt * (nt + 1) // 2  # (query tile, key tile, branch) triples
     assert computed / visited < 0.01  # ultra-sparse: almost every tile is skipped
 
 
@@ -140,21 +140,20 @@ def test_occupancy_and_norms_match_oracle():
         want = 1.0 / x.float().norm(dim=-1).clamp_min(1e-12).reshape(BH, N).cpu()
         torch.testing.assert_close(nrm[slot], want, rtol=1e-5, atol=0)
     nqt = N // 32
-    words = occ.view(BH, nqt, -1).cpu()
-    bits = ((words.unsqueeze(-1).to(torch.int64) >> torch.arange(32)) & 1).reshape(BH, nqt, -1)[:, :, :nqt]
+    words = occ.view(2, BH, nqt, -1).cpu()
+    bits = ((words.unsqueeze(-1).to(torch.int64) >> torch.arange(32)) & 1).reshape(2, BH, nqt, -1)[..., :nqt]
     t = tau(N, 128, 1.0, dtype=torch.float32)[:, None]
     causal = torch.ones(N, N, dtype=torch.bool).tril()
     mism = 0
     for bh in (0, 63):
         b, h = divmod(bh, 16)
-        any_nz = torch.zeros(N, N, dtype=torch.bool)
-        for q, k in ((q1, k1), (q2, k2)):
+        for br, (q, k) in enumerate(((q1, k1), (q2, k2))):
             qf = torch.nn.functional.normalize(q[b, h].float().cpu(), dim=-1)
             kf = torch.nn.functional.normalize(k[b, h].float().cpu(), dim=-1)
-            any_nz |= ((qf @ kf.T - t) > 0) & causal
-        tiles = any_nz.view(nqt, 32, nqt, 32).any(3).any(1)
-        mism += (tiles != bits[bh].bool()).sum().item()
-        assert 0.02 < tiles.float().sum().item() / (nqt * (nqt + 1) / 2) < 0.5
+            nz = ((qf @ kf.T - t) > 0) & causal
+            tiles = nz.view(nqt, 32, nqt, 32).any(3).any(1)
+            mism += (tiles != bits[br, bh].bool()).sum().item()
+            assert 0.01 < tiles.float().sum().item() / (nqt * (nqt + 1) / 2) < 0.5
     assert mism <= 4, mism  # only threshold ties within rounding may differ
 
 
