@@ -454,9 +454,8 @@ static int launch_bwd_t(const BwdParams& p, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL((bwd_dq<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, s, p);
   hipLaunchKernelGGL((bwd_dkv<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, s, p);
-  hipLaunchKernelGGL(bwd_finish, dim3(1), dim3(256), 0, s, (const float*)p.ws, items, p.lam, p.dbeta, p.dlam,
-                     BR);
-  return (int)hipGetLastError();
+  const int e = (int)hipGetLastError();
+  return e ? e : launch_bwd_finish(p, BR, stream);
 }
 
 template <class Pol, int D, int BR, int PK>
@@ -480,8 +479,16 @@ static int bsel_d(const BwdParams& p, const KernelKey& k, void* s) {
   return k.d == 128 ? bsel_br<Pol, 128>(p, k, s) : bsel_br<Pol, 64>(p, k, s);
 }
 
+int launch_bwd_finish(const BwdParams& p, int branches, void* stream) {
+  const int64_t items = (int64_t)p.B * p.H * p.nqt;
+  hipLaunchKernelGGL(bwd_finish, dim3(1), dim3(256), 0, (hipStream_t)stream, (const float*)p.ws, items, p.lam,
+                     p.dbeta, p.dlam, branches);
+  return (int)hipGetLastError();
+}
+
+// bf16 runs the bitmask-driven kernels of tda_bwd_fast.hip; fp32 runs bwd_dq / bwd_dkv.
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream) {
-  return k.dtype == 1 ? bsel_d<PolBF16>(p, k, stream) : bsel_d<PolF32>(p, k, stream);
+  return k.dtype == 1 ? launch_bwd_fast(p, k, stream) : bsel_d<PolF32>(p, k, stream);
 }
 
 }  // namespace tda

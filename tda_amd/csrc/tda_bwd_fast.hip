@@ -1,0 +1,436 @@
+// tda_bwd_fast.hip -- bf16 backward of threshold attention for gfx950, driven by the forward's
+// tile-occupancy bitmask.
+//
+// Reference semantics: snap-research/TDA triton_threshold_attention.py backward kernels
+// (TTA:118-324) and host backward (TTA:406-469); the normalize / clamp / combine gradients
+// follow torch autograd of TTA:505-517; dbeta is new (the reference returns None, TTA:469).
+// The formulas are listed at the top of tda_bwd.hip.
+//
+// Layout of the work:
+//   * query-major pass (bwd_dq_fast): one wave per 32-row query tile; for each branch it walks
+//     the set bits of that branch's bitmask row, so only key tiles with a non-zero score are
+//     touched.  dq_br is finished (F.normalize backward) at the end of the branch; the dbeta /
+//     dlambda partials accumulate over both branches.
+//   * key-major pass (bwd_dkv_fast): one wave per 32-row key tile; for each branch it walks
+//     the set bits of the bitmask column.  dv accumulates over both branches (A1 - lam A2);
+//     dk_br is finished at the end of each branch.
+// Each visited tile is fetched by the wave itself with direct global->LDS loads into a
+// wave-private, chunk-swizzled row-major tile that serves both as row fragments (ds_read_b128)
+// and, through the LDS transpose read, as transposed fragments.  Only one branch's resident
+// operands and accumulators are live at a time.
+#include "tda_common.hpp"
+#include "tda_params.hpp"
+
+namespace tda {
+
+#define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte chunk swizzle of a row-major 32-row tile (D/8 chunks per row).  Conflict-free for the
+// row-fragment reads (32 rows, one chunk each) and for the transpose reads (4 rows x 2 chunks
+// per 16 lanes), with 32 or 64 banks.
+template <int D>
+__device__ __forceinline__ int bswz(int r) {
+  if constexpr (D == 128) return (r ^ (4 * (r & 3))) & 15;
+  else return ((r ^ (r >> 1)) ^ (2 * (r & 1)) ^ (4 * ((r >> 1) & 1))) & 7;
+}
+
+// Direct global->LDS load of rows r0..r0+31 of a (N, D) row set (row stride st elements;
+// rows >= n clamped to n-1, their values only meet zero weights) into a swizzled tile.
+// One instruction moves 1 KiB: 64 lanes x 16 bytes.
+template <int D>
+__device__ __forceinline__ void dma_tile(const bf16* rows, int64_t st, int r0, int n, bf16* tile) {
+  constexpr int CH = D / 8, RPI = 64 / CH;
+  const int l = lane_id();
+#pragma unroll
+  for (int u = 0; u < 32 / RPI; ++u) {
+    const int r = u * RPI + l / CH;
+    const int c = (l % CH) ^ bswz<D>(r);
+    const bf16* src = rows + (int64_t)min(r0 + r, n - 1) * st + 8 * c;
+    __builtin_amdgcn_global_load_lds((const void*)src, LDS_PTR(void, tile + u * RPI * D), 16, 0, 0);
+  }
+}
+// 32 floats (one per tile row) by direct load; rows >= n clamped.
+__device__ __forceinline__ void dma_row_vals(const float* vals, int r0, int n, float* dst) {
+  const int l = lane_id();
+  if (l < 32) __builtin_amdgcn_global_load_lds((const void*)(vals + min(r0 + l, n - 1)), LDS_PTR(void, dst), 4, 0, 0);
+}
+__device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Row fragment t of a swizzled tile: lane (m, g) gets elements 16t + 8g .. +7 of row m.
+template <int D>
+__device__ __forceinline__ bf16x8 tile_row_frag(const bf16* tile, int t) {
+  const int l = lane_id(), m = l & 31, g = l >> 5;
+  return *reinterpret_cast<const bf16x8*>(tile + m * D + 8 * ((2 * t + g) ^ bswz<D>(m)));
+}
+// Transposed fragment (step st over the 32 rows, column block dsub): lane (n, g) gets column
+// 32*dsub + n at tile rows crow(8*st + j, g), j = 0..7.
+template <int D>
+__device__ __forceinline__ bf16x8 tile_tr_frag(const bf16* tile, int st, int dsub) {
+  const int l = lane_id(), bk = l >> 4, j = l & 15;
+  const int d = 32 * dsub + 16 * (bk & 1) + 4 * (j & 3);
+  bf16x8 out;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int r = 16 * st + 8 * hh + 4 * (bk >> 1) + (j >> 2);
+    const bf16* p = tile + r * D + 8 * ((d >> 3) ^ bswz<D>(r)) + (d & 7);
+    const bf16x4 w = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, p)));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[4 * hh + e] = w[e];
+  }
+  return out;
+}
+
+// Load this lane's 16 values of a 32-float row table at C rows crow(r, g).
+__device__ __forceinline__ void crow_vals(const float* tab, float (&v)[16]) {
+  const int g = lane_id() >> 5;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(tab + 8 * u + 4 * g);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * u + e] = x[e];
+  }
+}
+
+// Apply the F.normalize backward to a gradient tile in the transposed C layout (lane = row,
+// value r of column block c = element 32c + crow(r, g)) and store it (see finish_rows in
+// tda_bwd.hip; same arithmetic).
+template <int D, bool NORM>
+__device__ __forceinline__ void store_grad_rows(const f32x16 (&acc)[D / 32], const bf16* xrow, bf16* grow,
+                                                float rinv) {
+  constexpr int ND = D / 32;
+  const int g = lane_id() >> 5;
+  float dot = 0.f;
+  f32x4 xh[ND][4];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int c = 0; c < ND; ++c)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f32x4 x = load4(xrow + 32 * c + 8 * u + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xh[c][u][e] = x[e] * rinv;
+          dot = __builtin_fmaf(xh[c][u][e], acc[c][4 * u + e], dot);
+        }
+      }
+    dot += __shfl_xor(dot, 32);
+  }
+  const bool clamped = NORM && rinv >= 1.0f / kNormEps;
+#pragma unroll
+  for (int c = 0; c < ND; ++c)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = acc[c][4 * u + e];
+        if constexpr (NORM) o[e] = clamped ? a * rinv : (a - xh[c][u][e] * dot) * rinv;
+        else o[e] = a;
+      }
+      store4(grow + 32 * c + 8 * u + 4 * g, o[0], o[1], o[2], o[3]);
+    }
+}
+
+template <int D>
+struct BwdWaveLds {
+  bf16 a[32 * D];  // K (dq pass) or Q (dkv pass) tile
+  bf16 b[32 * D];  // V (dq pass) or dO (dkv pass) tile
+  float rows[32];  // key inverse norms (dq) or query inverse norms (dkv)
+  float taus[32];  // tau coefficients of the query rows (dkv)
+};
+
+// ------------------------------------------------------------------ query-major pass
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(256) bwd_dq_fast(BwdParams P) {
+  constexpr int NT = D / 16, ND = D / 32;
+  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> lds_all[4];
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  BwdWaveLds<D>& W = lds_all[wv];
+  const int BH = P.B * P.H;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+  if (item >= (int64_t)BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
+  const int qt = P.nqt - 1 - (int)(item / BH);
+  const int bh = (int)(item % BH);
+  const int b = bh / P.H, h = bh % P.H;
+  const int N = P.N;
+  const int i = qt * 32 + n32;
+  const bool qvalid = i < N;
+  const int ic = min(i, N - 1);
+  auto base = [&](int slot) {
+    return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
+  };
+
+  bf16x8 DO[NT];
+  {
+    const bf16* r = base(B_DO) + (int64_t)ic * P.s[B_DO][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) DO[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+  }
+  const float ci = tau_coeff(i, P.inv_d);
+  const float tau = (*P.beta) * ci;
+  const float pw = P.p;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+  const bf16* vb = base(B_V);
+  const int64_t sv = P.s[B_V][2];
+  float bsum = 0.f, lsum = 0.f;
+  unsigned visited = 0, computed = 0;
+  const int nw = (qt >> 5) + 1;  // bitmask words covering key tiles 0..qt
+
+  for (int br = 0; br < BR; ++br) {
+    const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
+    const bf16* kb = base(kslot);
+    const int64_t sk = P.s[kslot][2];
+    bf16x8 Q[NT];
+    {
+      const bf16* r = base(qslot) + (int64_t)ic * P.s[qslot][2];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Q[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+    }
+    float rq = 1.f;
+    const float* nk = nullptr;
+    if constexpr (NORM) {
+      rq = P.norms[((int64_t)(br == 0 ? N_Q1 : N_Q2) * BH + bh) * N + ic];
+      nk = P.norms + ((int64_t)(br == 0 ? N_K1 : N_K2) * BH + bh) * N;
+    }
+    const float coef = br == 0 ? 1.f : -lam;
+    f32x16 A[ND];
+#pragma unroll
+    for (int c = 0; c < ND; ++c) A[c] = f32x16{};
+    const uint32_t* occrow = P.occ ? P.occ + (((int64_t)br * BH + bh) * P.nqt + qt) * P.occ_w : nullptr;
+
+    for (int w0 = 0; w0 < nw; w0 += 64) {
+      const uint32_t lw = (w0 + l < nw) ? (occrow ? occrow[w0 + l] : 0xffffffffu) : 0u;
+      for (int w = w0; w < min(nw, w0 + 64); ++w) {
+        uint32_t bits = __builtin_amdgcn_readlane(lw, w - w0);
+        if (w == (qt >> 5)) bits &= (qt & 31) == 31 ? 0xffffffffu : ((2u << (qt & 31)) - 1u);
+        while (bits) {
+          const int kt = 32 * w + __builtin_ctz(bits);
+          bits &= bits - 1u;
+          ++visited;
+          const int k0 = 32 * kt;
+          dma_tile<D>(kb, sk, k0, N, W.a);
+          dma_tile<D>(vb, sv, k0, N, W.b);
+          if constexpr (NORM) dma_row_vals(nk, k0, N, W.rows);
+          wait_all_loads();
+          f32x16 S = f32x16{}, Dp = f32x16{};
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            S = PolBF16::mma(tile_row_frag<D>(W.a, t), Q[t], S);
+            Dp = PolBF16::mma(tile_row_frag<D>(W.b, t), DO[t], Dp);
+          }
+          float rk[16];
+          if constexpr (NORM) crow_vals(W.rows, rk);
+          f32x16 E;
+          bool any = false;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const bool valid = qvalid && (k0 + crow(r, g) <= i);
+            const float sr = NORM ? S[r] * rk[r] : S[r];
+            const float x = __builtin_fmaf(sr, rq, -tau);
+            const bool pos = valid && x > 0.f;
+            const float ds = pos ? coef * dpow_p<PK>(x, pw) * Dp[r] : 0.f;
+            bsum += ds;
+            if (br == 1) lsum = __builtin_fmaf(pos ? pow_p<PK>(x, pw) : 0.f, Dp[r], lsum);
+            any = any || pos;
+            E[r] = NORM ? ds * rk[r] : ds;
+          }
+          if (!occrow && wave_ballot(any) == 0ull) continue;
+          ++computed;
+          const bf16x8 E0 = PolBF16::pack_c(E, 0), E1 = PolBF16::pack_c(E, 1);
+#pragma unroll
+          for (int c = 0; c < ND; ++c) {
+            A[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 0, c), E0, A[c]);
+            A[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 1, c), E1, A[c]);
+          }
+        }
+      }
+    }
+    if (qvalid) {
+      const bf16* qrow = base(qslot) + (int64_t)i * P.s[qslot][2];
+      const int gslot = br == 0 ? B_DQ1 : B_DQ2;
+      bf16* grow = (bf16*)P.grad[br == 0 ? 0 : 2] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
+                   (int64_t)i * P.s[gslot][2];
+      store_grad_rows<D, NORM>(A, qrow, grow, rq);
+    }
+  }
+
+  const float pb = wave_sum(-ci * bsum);
+  const float pl = wave_sum(-lsum);
+  if (l == 0) {
+    P.ws[2 * item + 0] = pb;
+    P.ws[2 * item + 1] = pl;
+    if (P.stats) {
+      atomicAdd(P.stats + 0, (unsigned long long)visited);
+      atomicAdd(P.stats + 1, (unsigned long long)computed);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ key-major pass
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(256) bwd_dkv_fast(BwdParams P) {
+  constexpr int NT = D / 16, ND = D / 32;
+  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> lds_all[4];
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  BwdWaveLds<D>& W = lds_all[wv];
+  const int BH = P.B * P.H;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+  if (item >= (int64_t)BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
+  const int kt = (int)(item / BH);
+  const int bh = (int)(item % BH);
+  const int b = bh / P.H, h = bh % P.H;
+  const int N = P.N;
+  const int j = kt * 32 + n32;
+  const bool kvalid = j < N;
+  const int jc = min(j, N - 1);
+  auto base = [&](int slot) {
+    return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
+  };
+
+  bf16x8 V[NT];
+  {
+    const bf16* r = base(B_V) + (int64_t)jc * P.s[B_V][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) V[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+  }
+  const float beta = *P.beta;
+  const float pw = P.p;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+  const bf16* dob = base(B_DO);
+  const int64_t sdo = P.s[B_DO][2];
+  f32x16 AV[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) AV[c] = f32x16{};
+  unsigned visited = 0, computed = 0;
+
+  for (int br = 0; br < BR; ++br) {
+    const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
+    const bf16* qb = base(qslot);
+    const int64_t sq = P.s[qslot][2];
+    bf16x8 K[NT];
+    {
+      const bf16* r = base(kslot) + (int64_t)jc * P.s[kslot][2];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) K[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+    }
+    float rk = 1.f;
+    const float* nq = nullptr;
+    if constexpr (NORM) {
+      rk = P.norms[((int64_t)(br == 0 ? N_K1 : N_K2) * BH + bh) * N + jc];
+      nq = P.norms + ((int64_t)(br == 0 ? N_Q1 : N_Q2) * BH + bh) * N;
+    }
+    const float coef = br == 0 ? 1.f : -lam;
+    f32x16 AK[ND];
+#pragma unroll
+    for (int c = 0; c < ND; ++c) AK[c] = f32x16{};
+    // bitmask column: bit kt % 32 of word (br, bh, qt, kt / 32) for qt = kt .. nqt-1
+    const uint32_t* occcol = P.occ ? P.occ + ((int64_t)br * BH + bh) * P.nqt * P.occ_w + (kt >> 5) : nullptr;
+
+    for (int q0c = kt; q0c < P.nqt; q0c += 64) {
+      const int qtl = q0c + l;
+      const bool has = qtl < P.nqt && (!occcol || ((occcol[(int64_t)qtl * P.occ_w] >> (kt & 31)) & 1u));
+      uint64_t mask = wave_ballot(has);
+      while (mask) {
+        const int qt = q0c + __builtin_ctzll(mask);
+        mask &= mask - 1ull;
+        ++visited;
+        const int q0 = 32 * qt;
+        dma_tile<D>(qb, sq, q0, N, W.a);
+        dma_tile<D>(dob, sdo, q0, N, W.b);
+        if constexpr (NORM) dma_row_vals(nq, q0, N, W.rows);
+        if (l < 32) W.taus[l] = beta * tau_coeff(q0 + l, P.inv_d);
+        wait_all_loads();
+        f32x16 S = f32x16{}, Dp = f32x16{};
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          S = PolBF16::mma(tile_row_frag<D>(W.a, t), K[t], S);
+          Dp = PolBF16::mma(tile_row_frag<D>(W.b, t), V[t], Dp);
+        }
+        float rq[16], tq[16];
+        if constexpr (NORM) crow_vals(W.rows, rq);
+        crow_vals(W.taus, tq);
+        f32x16 EV, EK;
+        bool any = false;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qi = q0 + crow(r, g);
+          const bool valid = kvalid && qi < N && j <= qi;
+          const float sr = NORM ? S[r] * rk : S[r];
+          const float x = __builtin_fmaf(sr, NORM ? rq[r] : 1.f, -tq[r]);
+          const bool pos = valid && x > 0.f;
+          EV[r] = pos ? coef * pow_p<PK>(x, pw) : 0.f;
+          const float ds = pos ? coef * dpow_p<PK>(x, pw) * Dp[r] : 0.f;
+          EK[r] = NORM ? ds * rq[r] : ds;
+          any = any || pos;
+        }
+        if (!occcol && wave_ballot(any) == 0ull) continue;
+        ++computed;
+        const bf16x8 V0 = PolBF16::pack_c(EV, 0), V1 = PolBF16::pack_c(EV, 1);
+        const bf16x8 K0 = PolBF16::pack_c(EK, 0), K1 = PolBF16::pack_c(EK, 1);
+#pragma unroll
+        for (int c = 0; c < ND; ++c) {
+          AV[c] = PolBF16::mma(tile_tr_frag<D>(W.b, 0, c), V0, AV[c]);
+          AV[c] = PolBF16::mma(tile_tr_frag<D>(W.b, 1, c), V1, AV[c]);
+          AK[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 0, c), K0, AK[c]);
+          AK[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 1, c), K1, AK[c]);
+        }
+      }
+    }
+    if (kvalid) {
+      const bf16* krow = base(kslot) + (int64_t)j * P.s[kslot][2];
+      const int gslot = br == 0 ? B_DK1 : B_DK2;
+      bf16* grow = (bf16*)P.grad[br == 0 ? 1 : 3] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
+                   (int64_t)j * P.s[gslot][2];
+      store_grad_rows<D, NORM>(AK, krow, grow, rk);
+    }
+  }
+  if (kvalid) {
+    bf16* vrow = (bf16*)P.grad[4] + (int64_t)b * P.s[B_DV][0] + (int64_t)h * P.s[B_DV][1] + (int64_t)j * P.s[B_DV][2];
+    store_grad_rows<D, false>(AV, nullptr, vrow, 1.f);
+  }
+  if (P.stats && l == 0) {
+    atomicAdd(P.stats + 0, (unsigned long long)visited);
+    atomicAdd(P.stats + 1, (unsigned long long)computed);
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+template <int D, int BR, int PK, bool NORM>
+static int launch_t(const BwdParams& p, void* stream) {
+  const int64_t items = (int64_t)p.B * p.H * p.nqt;
+  const unsigned grid = (unsigned)((items + 3) / 4);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3(grid), dim3(256), 0, s, p);
+  const int e = (int)hipGetLastError();
+  return e ? e : launch_bwd_finish(p, BR, stream);
+}
+template <int D, int BR, int PK>
+static int sel_norm(const BwdParams& p, const KernelKey& k, void* s) {
+  return k.normalize ? launch_t<D, BR, PK, true>(p, s) : launch_t<D, BR, PK, false>(p, s);
+}
+template <int D, int BR>
+static int sel_pk(const BwdParams& p, const KernelKey& k, void* s) {
+  switch (k.pkind) {
+    case 2: return sel_norm<D, BR, 2>(p, k, s);
+    case 1: return sel_norm<D, BR, 1>(p, k, s);
+    default: return sel_norm<D, BR, 0>(p, k, s);
+  }
+}
+template <int D>
+static int sel_br(const BwdParams& p, const KernelKey& k, void* s) {
+  return k.branches == 2 ? sel_pk<D, 2>(p, k, s) : sel_pk<D, 1>(p, k, s);
+}
+
+int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream) {
+  return k.d == 128 ? sel_br<128>(p, k, stream) : sel_br<64>(p, k, stream);
+}
+
+}  // namespace tda

@@ -58,5 +58,7 @@ struct KernelKey {
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_fwd_fast(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
+int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream);
+int launch_bwd_finish(const BwdParams& p, int branches, void* stream);
 
 }  // namespace tda
