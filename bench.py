@@ -122,7 +122,7 @@ def main(argv=None) -> int:
     lam = torch.tensor(LAM, device=dev)
     stream = torch.cuda.current_stream(dev)
 
-    # ---- forward only: one fwd_wave launch per call, timed with events on its stream
+    # ---- forward only (key_norms, fwd_screen, fwd_pv per call), timed with events on its stream
     with torch.no_grad():
         for _ in range(args.warmup):
             ops.forward(q1, k1, q2, k2, v, beta, lam, POWER, True, 2)
@@ -197,7 +197,7 @@ def main(argv=None) -> int:
             "note": "FLOPs of two independent TRA calls (4U fwd, 14U fwd+bwd), as the reference executes",
             "fwd_tflops": units(SHAPE, REF_FWD_UNITS) / (fwd_ms * 1e-3) / 1e12,
             "fwd_bwd_tflops": units(SHAPE, REF_FWDBWD_UNITS) / (max(step_ms, wall_ms) * 1e-3) / 1e12},
-        "roofline": {"kernel": "fwd_fast (forward, one launch per call, plus the key-norm prologue)", "bound": "mfma",
+        "roofline": {"kernel": "forward (key_norms + fwd_screen + fwd_pv), events around the launches", "bound": "mfma",
                      "achieved": fwd_tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": fwd_tf / PEAK_BF16_TFLOPS, "traffic": None,
                      "algorithmic": "3U = 4.1232e11 FLOP per launch (causal dense)"},

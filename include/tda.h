@@ -27,10 +27,12 @@
  *
  * Conventions
  *   - Every pointer in the argument structs is a device pointer, except the
- *     struct itself.  The caller allocates everything; the library never
- *     allocates or frees device memory and keeps no per-call state.
+ *     struct itself.  The caller allocates everything (outputs and the
+ *     workspace of each pass); the library never allocates or frees device
+ *     memory and keeps no per-call state.
  *   - Strides are in elements, for the (B, H, N, d) axes.  stride[3] must be 1;
- *     the other strides and every base pointer must keep 16-byte alignment.
+ *     the other strides and every base pointer must keep 16-byte alignment;
+ *     the sequence stride is at most 2^25 elements.
  *     stride[0] is honoured (the reference ignores it, TTA:49).
  *   - beta and lambda are read on the device (no host synchronisation);
  *     lambda is clamped to [0, 1] on the device.
@@ -49,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TDA_ABI_VERSION 1
+#define TDA_ABI_VERSION 2
 
 /* element types of q, k, v, out and gradients */
 #define TDA_DTYPE_F32  0
@@ -61,10 +63,11 @@ extern "C" {
 #define TDA_ERR_SHAPE         -2   /* batch/heads/seq_len out of range */
 #define TDA_ERR_HEAD_DIM      -3   /* head_dim not in {64, 128} */
 #define TDA_ERR_DTYPE         -4   /* dtype not TDA_DTYPE_F32 / TDA_DTYPE_BF16 */
-#define TDA_ERR_LAYOUT        -5   /* stride[3] != 1 or 16-byte alignment broken */
+#define TDA_ERR_LAYOUT        -5   /* stride[3] != 1, 16-byte alignment broken, or a
+                                      sequence stride above 2^25 elements */
 #define TDA_ERR_POWER         -6   /* relu_power negative or not finite */
 #define TDA_ERR_BRANCHES      -7   /* branches not 1 or 2 */
-#define TDA_ERR_WORKSPACE     -8   /* workspace missing or too small */
+#define TDA_ERR_WORKSPACE     -8   /* workspace missing, too small or misaligned */
 #define TDA_ERR_ABI           -9   /* abi_version != TDA_ABI_VERSION */
 #define TDA_ERR_CAUSAL       -10   /* causal != 1 (only the causal form exists) */
 #define TDA_ERR_NORMS        -11   /* normalize set but the norms buffer is missing */
@@ -99,6 +102,9 @@ typedef struct tda_fwd_args {
   unsigned long long* stats;/* [0] += (query tile, key tile, branch) triples on or below
                                the diagonal, [1] += those with a non-zero weight tile
                                (A.V issued); tiles are 32x32 */
+  void*  workspace;         /* device scratch of tda_fwd_workspace_bytes() bytes, 16-byte
+                               aligned: holds the tile bitmask when occupancy is NULL */
+  size_t workspace_bytes;
 } tda_fwd_args;
 
 typedef struct tda_bwd_args {
@@ -135,6 +141,7 @@ int32_t tda_validate_bwd(const tda_bwd_args* args);
 /* Buffer sizes for the optional forward outputs and the backward workspace. */
 size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 size_t tda_norms_floats(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
+size_t tda_fwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim);
 
 /* Enqueue the forward / backward pass on `stream` (a hipStream_t). */

@@ -13,7 +13,7 @@ import threading
 HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(HERE, "libtda_hip.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
@@ -56,6 +56,7 @@ class TdaFwdArgs(ctypes.Structure):
         ("v", TdaTensor), ("out", TdaTensor),
         ("beta", ctypes.c_void_p), ("lambda_param", ctypes.c_void_p),
         ("norms", ctypes.c_void_p), ("occupancy", ctypes.c_void_p), ("stats", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -82,6 +83,7 @@ SIGNATURES = {
     "tda_validate_bwd": (ctypes.c_int32, [ctypes.POINTER(TdaBwdArgs)]),
     "tda_occupancy_words": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
     "tda_norms_floats": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
+    "tda_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
     "tda_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4),
     "tda_fwd": (ctypes.c_int32, [ctypes.POINTER(TdaFwdArgs), ctypes.c_void_p]),
     "tda_bwd": (ctypes.c_int32, [ctypes.POINTER(TdaBwdArgs), ctypes.c_void_p]),

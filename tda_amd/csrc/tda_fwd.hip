@@ -233,7 +233,7 @@ static int sel_d(const FwdParams& p, const KernelKey& k, void* s) {
 
 // bf16 runs the LDS-staged kernel (tda_fwd_fast.hip); fp32 runs fwd_wave.
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream) {
-  return k.dtype == 1 ? launch_fwd_fast(p, k, stream) : sel_d<PolF32>(p, k, stream);
+  return k.dtype == 1 ? launch_fwd_sparse(p, k, stream) : sel_d<PolF32>(p, k, stream);
 }
 
 }  // namespace tda

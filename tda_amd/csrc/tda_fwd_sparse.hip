@@ -1,0 +1,438 @@
+// tda_fwd_sparse.hip -- bf16 forward of threshold attention for gfx950, built around the
+// sparsity of the weights: with cosine scores and tau_i = beta sqrt(2 ln(i+1)/d), only a few
+// percent of the 32x32 (query tile, key tile) weight blocks hold a non-zero entry.
+//
+// Reference semantics: snap-research/TDA triton_threshold_attention.py forward kernel
+// (TTA:19-115: scores, threshold, ReLU^p, causal mask, A.V) and the differential composition
+// out = A1 V - clamp(lambda, 0, 1) A2 V (TTA:489-519).
+//
+// Three launches, in stream order:
+//   key_norms   inverse L2 norms rk_j of the key rows, into the norms table (normalize only).
+//   fwd_screen  for every causal (query tile, key tile) pair of a branch, the score tile
+//               S = q k^T on the matrix cores and the tile's largest threshold argument
+//               x_ij = fma(s_ij rk_j, rq_i, -tau_i) (the weight is non-zero iff x_ij > 0).
+//               Tiles with some x_ij > 0 get their bit in the occupancy bitmask.  No V and no
+//               output accumulators: the kernel holds only Q fragments and two score tiles per
+//               wave, so MFMA results stay in ordinary VGPRs and several waves share a SIMD.
+//   fwd_pv      one wave per query tile walks the set bits of both branches: recomputes the
+//               score tile with the same instruction sequence (so the same values), forms the
+//               exact weights ReLU(x)^p with the causal mask, and accumulates out += coef A V.
+//               Tiles whose weights are all zero after the mask lose their bit, so the bitmask
+//               ends exact.
+// The screen tests every key of the tile, including keys after the query on the diagonal tile
+// and padding keys past N: it may keep a tile the mask empties, never drop a non-zero one.
+#include "tda_common.hpp"
+#include "tda_params.hpp"
+
+namespace tda {
+namespace {
+
+#define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor over [base, base + bytes): loads past the end return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// Descriptor over the 32-row tile kt of a (N, D) head whose rows are `stride` elements apart:
+// rows past N read as zeros.
+template <int D>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const bf16* head, int64_t stride, int kt, int N) {
+  const int rows = min(32, N - 32 * kt);
+  return make_rsrc(head + (int64_t)(32 * kt) * stride, (uint32_t)(((int64_t)(rows - 1) * stride + D) * 2));
+}
+
+__device__ __forceinline__ float max16(const f32x16& v) {
+  const float a = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+  const float b = fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7]));
+  const float c = fmaxf(fmaxf(v[8], v[9]), fmaxf(v[10], v[11]));
+  const float d = fmaxf(fmaxf(v[12], v[13]), fmaxf(v[14], v[15]));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// XCD-aware order of the (stream, block) work items of a grid: consecutive workgroup ids go to
+// the 8 XCDs in turn, so all blocks of a stream (one head of one branch) run on one XCD and
+// share its L2.  Blocks are handed out from the last (the longest causal row range) down.
+struct WorkItem {
+  int stream, block;
+};
+__device__ __forceinline__ WorkItem xcd_order(int bid, int nstreams, int nblocks) {
+  WorkItem w;
+  if (nstreams % 8 == 0) {
+    const int x = bid & 7, j = bid >> 3, sp = nstreams >> 3;
+    w.block = nblocks - 1 - j / sp;
+    w.stream = x + 8 * (j % sp);
+  } else {
+    w.block = nblocks - 1 - bid / nstreams;
+    w.stream = bid % nstreams;
+  }
+  return w;
+}
+
+// ------------------------------------------------------------------ key_norms
+// Inverse L2 norms of the key rows of every branch.  One group of D/8 lanes per row (16 bytes
+// per lane), rows in order, so each load instruction covers whole rows.
+template <int D>
+__global__ void __launch_bounds__(256) key_norms(FwdParams P, int BR) {
+  constexpr int LPR = D / 8;  // lanes per row
+  const int BH = P.B * P.H, N = P.N;
+  const int64_t rows = (int64_t)BH * N;
+  const int sub = threadIdx.x % LPR;
+  const int64_t gid = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;  // row id over branches
+  const int br = (int)(gid / rows);
+  const int64_t rid = gid - (int64_t)br * rows;
+  const bool ok = br < BR;
+  float ss = 0.f;
+  if (ok) {
+    const int slot = br ? F_K2 : F_K1;
+    const int bh = (int)(rid / N), t = (int)(rid % N);
+    const bf16* row = (const bf16*)P.in[slot] + (int64_t)(bh / P.H) * P.s[slot][0] +
+                      (int64_t)(bh % P.H) * P.s[slot][1] + (int64_t)t * P.s[slot][2];
+    ss = PolBF16::sumsq(*reinterpret_cast<const bf16x8*>(row + 8 * sub));
+  }
+#pragma unroll
+  for (int o = LPR / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  if (ok && sub == 0) P.norms[(int64_t)(br ? N_K2 : N_K1) * rows + rid] = inv_norm(ss);
+}
+
+// ------------------------------------------------------------------ fwd_screen
+// Workgroup = 4 waves x 64 query rows (two 32-row query tiles per wave) of one branch of one
+// head; grid = branches x heads x ceil(N / 256).  Key tiles stream through a 3-stage LDS ring
+// (buffer loads into VGPRs one tile ahead, LDS writes two tiles ahead of use, one barrier per
+// tile).  Score tiles are computed transposed, S^T = K Q^T, so each lane holds one query.
+template <int D, bool NORM>
+__global__ void __launch_bounds__(256, 2) fwd_screen(FwdParams P, int BR) {
+  constexpr int NT = D / 16;   // MFMA steps over d
+  constexpr int KS = D + 8;    // LDS row stride (elements): conflict-free 16-byte fragment reads
+  constexpr int TPR = D / 16;  // staging threads per row, two 16-byte chunks each
+  __shared__ __attribute__((aligned(16))) bf16 kst[3][32 * KS];
+  __shared__ __attribute__((aligned(16))) float krk[3][32];  // inverse key norms of the tile
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5, tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int BH = P.B * P.H, N = P.N, nqt = P.nqt;
+  const WorkItem wi = xcd_order(blockIdx.x, BR * BH, (N + 255) / 256);
+  const int sidx = wi.stream, qb = wi.block;
+  const int br = sidx / BH, bh = sidx % BH;
+  const int b = bh / P.H, h = bh % P.H;
+  const int qslot = br ? F_Q2 : F_Q1, kslot = br ? F_K2 : F_K1;
+  const int q0w = qb * 256 + 64 * wv;  // first row of this wave
+  const int qt0 = q0w >> 5;            // this wave's query tiles: qt0, qt0 + 1
+  const int nkt = min(nqt, 8 * qb + 8);
+  const bool live0 = qt0 < nqt, live1 = qt0 + 1 < nqt;
+
+  // ---- staging
+  const bf16* khead = (const bf16*)P.in[kslot] + (int64_t)b * P.s[kslot][0] + (int64_t)h * P.s[kslot][1];
+  const int64_t sk = P.s[kslot][2];
+  const int srow = tid / TPR, sch = tid % TPR;
+  const bool stager = tid < 32 * TPR;
+  const uint32_t soff = (uint32_t)((srow * sk + 8 * sch) * 2);
+  // key norms: threads 0..7 stage four rows each (rows past N read as 0, never used)
+  const __amdgpu_buffer_rsrc_t rnorm =
+      make_rsrc(NORM ? P.norms + ((int64_t)(br ? N_K2 : N_K1) * BH + bh) * N : nullptr, NORM ? (uint32_t)N * 4 : 0u);
+  u32x4 R0 = {}, R1 = {}, RN = {};
+  auto fetch = [&](int kt) {
+    if (stager) {
+      const __amdgpu_buffer_rsrc_t rs = tile_rsrc<D>(khead, sk, kt, N);
+      R0 = buf_load16(rs, soff);
+      R1 = buf_load16(rs, soff + 16 * TPR);
+    }
+    if constexpr (NORM)
+      if (tid < 8) RN = buf_load16(rnorm, (uint32_t)(32 * kt + 4 * tid) * 4);
+  };
+  auto commit = [&](int s) {
+    if (stager) {
+      bf16* k = &kst[s][srow * KS + 8 * sch];
+      *reinterpret_cast<u32x4*>(k) = R0;
+      *reinterpret_cast<u32x4*>(k + 8 * TPR) = R1;
+    }
+    if constexpr (NORM)
+      if (tid < 8) *reinterpret_cast<u32x4*>(&krk[s][4 * tid]) = RN;
+  };
+
+  // ---- resident query fragments, inverse norms, thresholds
+  const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
+  const float beta = *P.beta;
+  bf16x8 Q[2][NT];
+  float rq[2] = {1.f, 1.f}, tau[2];
+  bool valid[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int iq = q0w + 32 * s + n32;
+    valid[s] = iq < N;
+    const bf16* row = qhead + (int64_t)min(iq, N - 1) * P.s[qslot][2];  // rows >= N: never vote
+#pragma unroll
+    for (int t = 0; t < NT; ++t) Q[s][t] = *reinterpret_cast<const bf16x8*>(row + 16 * t + 8 * g);
+    if constexpr (NORM) {
+      rq[s] = inv_norm(row_sumsq<PolBF16, NT>(Q[s]));
+      if (g == 0 && valid[s]) P.norms[((int64_t)(br ? N_Q2 : N_Q1) * BH + bh) * N + iq] = rq[s];
+    }
+    tau[s] = beta * tau_coeff(iq, P.inv_d);
+  }
+
+  uint32_t* occ0 = P.occ + ((int64_t)sidx * nqt + qt0) * P.occ_w;  // bitmask rows of qt0, qt0 + 1
+  uint32_t word0 = 0u, word1 = 0u;
+  unsigned visited = 0;
+  const int koff = n32 * KS + 8 * g;
+
+  fetch(0);
+  commit(0);
+  if (nkt > 1) {
+    fetch(1);
+    commit(1);
+  }
+  if (nkt > 2) fetch(2);
+  __syncthreads();
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int s = kt % 3;
+    if (live0 && kt <= qt0 + 1) {
+      const bf16* kp = &kst[s][koff];
+      bf16x8 fk[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) fk[t] = *reinterpret_cast<const bf16x8*>(kp + 16 * t);
+      f32x16 S0 = {}, S1 = {};
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        S0 = PolBF16::mma(fk[t], Q[0][t], S0);
+        S1 = PolBF16::mma(fk[t], Q[1][t], S1);
+      }
+      // largest s_ij rk_j per lane; x = fma(s rk, rq, -tau) is monotone in s rk (rq > 0), so
+      // "fma(max, rq, -tau) > 0" is exactly "some x_ij > 0" for the lane's keys
+      if constexpr (NORM) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const f32x4 r4 = *reinterpret_cast<const f32x4*>(&krk[s][8 * u + 4 * g]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            S0[4 * u + e] *= r4[e];
+            S1[4 * u + e] *= r4[e];
+          }
+        }
+      }
+      const float b0 = __builtin_fmaf(max16(S0), rq[0], -tau[0]);
+      const float b1 = __builtin_fmaf(max16(S1), rq[1], -tau[1]);
+      const bool in0 = kt <= qt0;  // key tile qt0 + 1 lies wholly after query tile qt0
+      const bool a0 = wave_ballot(in0 && valid[0] && b0 > 0.f) != 0ull;
+      const bool a1 = wave_ballot(valid[1] && b1 > 0.f) != 0ull;
+      word0 |= (uint32_t)a0 << (kt & 31);
+      word1 |= (uint32_t)a1 << (kt & 31);
+      visited += (unsigned)in0 + (unsigned)live1;
+    }
+    // bitmask words of rows qt0 and qt0 + 1: word kt/32 is complete after key tile kt
+    if (live0 && ((kt & 31) == 31 || kt == nkt - 1)) {
+      if (l == 0) {
+        occ0[kt >> 5] = word0;
+        if (live1) occ0[P.occ_w + (kt >> 5)] = word1;
+        if (kt == nkt - 1) {  // words of key tiles this workgroup never reaches
+          for (int w = (kt >> 5) + 1; w < P.occ_w; ++w) {
+            occ0[w] = 0u;
+            if (live1) occ0[P.occ_w + w] = 0u;
+          }
+        }
+      }
+      word0 = word1 = 0u;
+    }
+    if (kt + 2 < nkt) commit((kt + 2) % 3);
+    if (kt + 3 < nkt) fetch(kt + 3);
+    __syncthreads();
+  }
+  if (P.stats && l == 0 && visited) atomicAdd(P.stats + 0, (unsigned long long)visited);
+}
+
+// ------------------------------------------------------------------ fwd_pv
+// Transposed A fragment of one 32-column block and one 16-row step from a row-major tile
+// with row stride VS: lane (n, g) gets column n of the block at tile rows crow(8*st + j, g),
+// j = 0..7, by two LDS transpose reads.  `p` already includes this lane's base offset.
+template <int VS>
+__device__ __forceinline__ bf16x8 tr_frag(const bf16* p) {
+  const bf16x4 a = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, p)));
+  const bf16x4 c = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, p + 8 * VS)));
+  return bf16x8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
+}
+
+// One wave per query tile (workgroup = 4 consecutive tiles of one head); no barriers.
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(256, 2) fwd_pv(FwdParams P) {
+  constexpr int NT = D / 16, ND = D / 32;
+  constexpr int VS = D + 32;     // LDS row stride of a V tile: conflict-free transpose reads
+  constexpr int CPR = D / 8;     // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;  // rows per V load instruction
+  constexpr int VL = 32 / RPI;   // V load instructions per tile
+  __shared__ __attribute__((aligned(16))) bf16 vst[4][32 * VS];
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int BH = P.B * P.H, N = P.N, nqt = P.nqt;
+  const int nblk = (nqt + 3) / 4;
+  int bh, blk;
+  {
+    const int bid = blockIdx.x;
+    if (BH % 8 == 0) {  // one head's blocks consecutive on one XCD, longest first
+      const int x = bid & 7, j = bid >> 3;
+      bh = x + 8 * (j / nblk);
+      blk = nblk - 1 - j % nblk;
+    } else {
+      bh = bid / nblk;
+      blk = nblk - 1 - bid % nblk;
+    }
+  }
+  const int qt = 4 * blk + wv;
+  if (qt >= nqt) return;
+  const int b = bh / P.H, h = bh % P.H;
+  const int iq = 32 * qt + n32;
+  const bool valid = iq < N;
+  const float tau = *P.beta * tau_coeff(iq, P.inv_d);
+  const float pw = P.p;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+
+  bf16* vt = vst[wv];
+  const int vrow = l / CPR, vch = l % CPR;
+  const int bk = l >> 4, jj = l & 15;
+  const int voff = (4 * (bk >> 1) + (jj >> 2)) * VS + 16 * (bk & 1) + 4 * (jj & 3);
+
+  f32x16 O[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) O[c] = f32x16{};
+  unsigned computed = 0;
+
+#pragma unroll
+  for (int br = 0; br < BR; ++br) {
+    const int qslot = br ? F_Q2 : F_Q1, kslot = br ? F_K2 : F_K1;
+    uint32_t* orow = P.occ + ((int64_t)(br * BH + bh) * nqt + qt) * P.occ_w;
+    const bf16* khead = (const bf16*)P.in[kslot] + (int64_t)b * P.s[kslot][0] + (int64_t)h * P.s[kslot][1];
+    const bf16* vhead = (const bf16*)P.in[F_V] + (int64_t)b * P.s[F_V][0] + (int64_t)h * P.s[F_V][1];
+    const int64_t sk = P.s[kslot][2], sv = P.s[F_V][2];
+    const __amdgpu_buffer_rsrc_t rn =
+        make_rsrc(NORM ? P.norms + ((int64_t)(br ? N_K2 : N_K1) * BH + bh) * N : nullptr, NORM ? (uint32_t)N * 4 : 0u);
+    const float coef = br == 0 ? 1.f : -lam;
+    bool have_q = false;
+    bf16x8 Q[NT];
+    float rq = 1.f;
+    for (int w = 0; w <= (qt >> 5); ++w) {
+      const uint32_t bits0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)orow[w]);
+      uint32_t bits = bits0, keep = bits0;
+      while (bits) {
+        const int kt = 32 * w + __builtin_ctz(bits);
+        bits &= bits - 1u;
+        if (!have_q) {
+          const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
+          const bf16* row = qhead + (int64_t)min(iq, N - 1) * P.s[qslot][2];
+#pragma unroll
+          for (int t = 0; t < NT; ++t) Q[t] = *reinterpret_cast<const bf16x8*>(row + 16 * t + 8 * g);
+          if constexpr (NORM) rq = P.norms[((int64_t)(br ? N_Q2 : N_Q1) * BH + bh) * N + min(iq, N - 1)];
+          have_q = true;
+        }
+        // loads of the key tile (A operand rows), the V tile and the key norms
+        const __amdgpu_buffer_rsrc_t rk = tile_rsrc<D>(khead, sk, kt, N);
+        const __amdgpu_buffer_rsrc_t rv = tile_rsrc<D>(vhead, sv, kt, N);
+        bf16x8 fk[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          fk[t] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((n32 * sk + 16 * t + 8 * g) * 2)));
+        u32x4 vr[VL];
+#pragma unroll
+        for (int i = 0; i < VL; ++i) vr[i] = buf_load16(rv, (uint32_t)(((vrow + RPI * i) * sv + 8 * vch) * 2));
+        f32x4 rk4[4] = {{1.f, 1.f, 1.f, 1.f}, {1.f, 1.f, 1.f, 1.f}, {1.f, 1.f, 1.f, 1.f}, {1.f, 1.f, 1.f, 1.f}};
+        if constexpr (NORM) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            rk4[u] = __builtin_bit_cast(f32x4, buf_load16(rn, (uint32_t)(32 * kt + 8 * u + 4 * g) * 4));
+        }
+        f32x16 S = {};
+#pragma unroll
+        for (int t = 0; t < NT; ++t) S = PolBF16::mma(fk[t], Q[t], S);
+#pragma unroll
+        for (int i = 0; i < VL; ++i) *reinterpret_cast<u32x4*>(vt + (vrow + RPI * i) * VS + 8 * vch) = vr[i];
+
+        // exact weights: keys after the query (diagonal tile only) are masked
+        const bool diag = kt == qt;
+        f32x16 C;
+        bool pos_any = false;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * u + e;
+            const float x = __builtin_fmaf(NORM ? S[r] * rk4[u][e] : S[r], rq, -tau);
+            const bool pos = (!diag || 32 * kt + crow(r, g) <= iq) && x > 0.f;
+            C[r] = pos ? coef * pow_p<PK>(x, pw) : 0.f;
+            pos_any |= pos;
+          }
+        if (wave_ballot(valid && pos_any) == 0ull) {
+          keep &= ~(1u << (kt & 31));
+          continue;
+        }
+        ++computed;
+        const bf16x8 PF0 = PolBF16::pack_c(C, 0), PF1 = PolBF16::pack_c(C, 1);
+        wave_lds_sync();
+        const bf16* vp = vt + voff;
+#pragma unroll
+        for (int c = 0; c < ND; ++c) {
+          O[c] = PolBF16::mma(tr_frag<VS>(vp + 32 * c), PF0, O[c]);
+          O[c] = PolBF16::mma(tr_frag<VS>(vp + 32 * c + 16 * VS), PF1, O[c]);
+        }
+        wave_lds_sync();
+      }
+      if (keep != bits0 && l == 0) orow[w] = keep;
+    }
+  }
+
+  if (valid) {
+    bf16* orow = (bf16*)P.out + (int64_t)b * P.s[F_OUT][0] + (int64_t)h * P.s[F_OUT][1] + (int64_t)iq * P.s[F_OUT][2];
+#pragma unroll
+    for (int c = 0; c < ND; ++c)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        store4(orow + 32 * c + 8 * u + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2], O[c][4 * u + 3]);
+  }
+  if (P.stats && l == 0 && computed) atomicAdd(P.stats + 1, (unsigned long long)computed);
+}
+
+// ------------------------------------------------------------------ dispatch
+template <int D, int BR, int PK, bool NORM>
+int launch_sparse_t(const FwdParams& p, hipStream_t s) {
+  const int BH = p.B * p.H;
+  if constexpr (NORM) {
+    const int64_t lanes = (int64_t)BR * BH * p.N * (D / 8);
+    hipLaunchKernelGGL(key_norms<D>, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, s, p, BR);
+  }
+  const unsigned nqb = (unsigned)((p.N + 255) / 256);
+  hipLaunchKernelGGL((fwd_screen<D, NORM>), dim3((unsigned)(BR * BH) * nqb), dim3(256), 0, s, p, BR);
+  const unsigned nblk = (unsigned)((p.nqt + 3) / 4);
+  hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)BH * nblk), dim3(256), 0, s, p);
+  return (int)hipGetLastError();
+}
+
+template <int D, int BR, int PK>
+int sel_norm(const FwdParams& p, const KernelKey& k, hipStream_t s) {
+  return k.normalize ? launch_sparse_t<D, BR, PK, true>(p, s) : launch_sparse_t<D, BR, PK, false>(p, s);
+}
+template <int D, int BR>
+int sel_pk(const FwdParams& p, const KernelKey& k, hipStream_t s) {
+  switch (k.pkind) {
+    case 2: return sel_norm<D, BR, 2>(p, k, s);
+    case 1: return sel_norm<D, BR, 1>(p, k, s);
+    default: return sel_norm<D, BR, 0>(p, k, s);
+  }
+}
+template <int D>
+int sel_br(const FwdParams& p, const KernelKey& k, hipStream_t s) {
+  return k.branches == 2 ? sel_pk<D, 2>(p, k, s) : sel_pk<D, 1>(p, k, s);
+}
+
+}  // namespace
+
+int launch_fwd_sparse(const FwdParams& p, const KernelKey& k, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  return k.d == 128 ? sel_br<128>(p, k, s) : sel_br<64>(p, k, s);
+}
+
+}  // namespace tda

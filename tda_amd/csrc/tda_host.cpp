@@ -16,6 +16,8 @@ namespace {
 
 thread_local int32_t g_last_hip_error = 0;
 
+constexpr int64_t kMaxSeqStride = int64_t(1) << 25;
+
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 int32_t check_tensor(const tda_tensor& t, int64_t elem_bytes) {
@@ -26,6 +28,8 @@ int32_t check_tensor(const tda_tensor& t, int64_t elem_bytes) {
     if (t.stride[k] < 0) return TDA_ERR_LAYOUT;
     if ((t.stride[k] * elem_bytes) % 16 != 0) return TDA_ERR_LAYOUT;
   }
+  // 32 rows of a tile span less than 2^31 bytes: the kernels address a tile with 32-bit offsets
+  if (t.stride[2] > kMaxSeqStride) return TDA_ERR_LAYOUT;
   return TDA_OK;
 }
 
@@ -51,6 +55,15 @@ int32_t check_common(const Common& c) {
   if (!c.beta) return TDA_ERR_NULL_POINTER;
   if (c.branches == 2 && !c.lambda_param) return TDA_ERR_NULL_POINTER;
   return TDA_OK;
+}
+
+int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Forward workspace: the bitmask scratch used when the caller asks for no occupancy output
+// (the bf16 forward always builds the bitmask: its second pass reads it).
+int64_t fwd_ws_bytes(int64_t bh, int64_t seq_len, int64_t branches) {
+  const int64_t nqt = ceil_div(seq_len, 32);
+  return round256(branches * bh * nqt * ceil_div(nqt, 32) * (int64_t)sizeof(uint32_t));
 }
 
 int pkind_of(float p) { return p == 2.0f ? 2 : (p == 1.0f ? 1 : 0); }
@@ -82,10 +95,12 @@ const char* tda_error_string(int32_t code) {
     case TDA_ERR_SHAPE: return "batch, heads or seq_len out of range";
     case TDA_ERR_HEAD_DIM: return "head_dim must be 64 or 128";
     case TDA_ERR_DTYPE: return "dtype must be float32 or bfloat16";
-    case TDA_ERR_LAYOUT: return "tensor layout unsupported: last-dim stride must be 1 and strides/pointers 16-byte aligned";
+    case TDA_ERR_LAYOUT:
+      return "tensor layout unsupported: last-dim stride must be 1, strides/pointers 16-byte aligned, "
+             "sequence stride at most 2^25 elements";
     case TDA_ERR_POWER: return "relu_power must be finite and >= 0";
     case TDA_ERR_BRANCHES: return "branches must be 1 or 2";
-    case TDA_ERR_WORKSPACE: return "backward workspace missing or too small";
+    case TDA_ERR_WORKSPACE: return "workspace missing, too small or not 16-byte aligned";
     case TDA_ERR_ABI: return "abi_version mismatch";
     case TDA_ERR_CAUSAL: return "only the causal form is implemented (causal must be 1)";
     case TDA_ERR_NORMS: return "normalize requires the norms buffer (forward: output, backward: the forward's output)";
@@ -105,6 +120,11 @@ size_t tda_norms_floats(int64_t batch, int64_t heads, int64_t seq_len, int32_t b
   return (size_t)(2 * branches * batch * heads * seq_len);
 }
 
+size_t tda_fwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches) {
+  if (batch < 1 || heads < 1 || seq_len < 1 || (branches != 1 && branches != 2)) return 0;
+  return (size_t)fwd_ws_bytes(batch * heads, seq_len, branches);
+}
+
 size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim) {
   (void)head_dim;
   if (batch < 1 || heads < 1 || seq_len < 1) return 0;
@@ -121,6 +141,10 @@ int32_t tda_validate_fwd(const tda_fwd_args* a) {
   for (int k = 0; k < n; ++k)
     if ((rc = check_tensor(*ts[k], eb))) return rc;
   if (a->normalize && !a->norms) return TDA_ERR_NORMS;
+  if (!a->workspace ||
+      a->workspace_bytes < tda_fwd_workspace_bytes(a->batch, a->heads, a->seq_len, a->branches))
+    return TDA_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0) return TDA_ERR_WORKSPACE;
   return TDA_OK;
 }
 
@@ -166,7 +190,7 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
   p.beta = a->beta;
   p.lam = a->lambda_param;
   p.norms = a->normalize ? a->norms : nullptr;
-  p.occ = a->occupancy;
+  p.occ = a->occupancy ? a->occupancy : static_cast<uint32_t*>(a->workspace);
   p.stats = a->stats;
   const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};
   const int e = tda::launch_fwd(p, key, stream);

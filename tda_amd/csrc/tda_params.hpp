@@ -25,7 +25,7 @@ struct FwdParams {
   const float* beta;
   const float* lam;
   float* norms;              // may be null
-  uint32_t* occ;             // may be null
+  uint32_t* occ;             // may be null (bf16: never, the host points it at workspace)
   unsigned long long* stats; // may be null
 };
 
@@ -56,7 +56,7 @@ struct KernelKey {
 };
 
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream);
-int launch_fwd_fast(const FwdParams& p, const KernelKey& k, void* stream);
+int launch_fwd_sparse(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_finish(const BwdParams& p, int branches, void* stream);

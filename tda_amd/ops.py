@@ -100,6 +100,9 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
     if normalize and norms is None:  # scratch: the kernels need the row norms either way
         norms = torch.empty(lib.tda_norms_floats(*q1.shape[:3], branches), dtype=torch.float32, device=q1.device)
     a.norms, a.occupancy, a.stats = _ptr(norms), _ptr(occupancy), _ptr(stats)
+    ws = torch.empty((lib.tda_fwd_workspace_bytes(*q1.shape[:3], branches) + 3) // 4, dtype=torch.float32,
+                     device=q1.device)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
     with torch.cuda.device(q1.device):
         _abi.check(lib.tda_fwd(ctypes.byref(a), _stream(q1.device)), "tda_fwd")
     return out

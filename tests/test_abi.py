@@ -91,6 +91,8 @@ def _fwd_args(shape=(2, 3, 100, 128), branches=2, dtype=_abi.DTYPE_BF16):
     a.beta = FAKE
     a.lambda_param = FAKE
     a.norms = FAKE
+    a.workspace = FAKE
+    a.workspace_bytes = _lib().tda_fwd_workspace_bytes(*shape[:3], branches)
     return a
 
 
@@ -136,6 +138,10 @@ def test_valid_args_pass():
     (lambda a: a.q1.stride.__setitem__(0, -128), _abi.ERR_LAYOUT),
     (lambda a: setattr(a.q1, "data", FAKE + 2), _abi.ERR_LAYOUT),
     (lambda a: setattr(a, "norms", None), _abi.ERR_NORMS),
+    (lambda a: a.k1.stride.__setitem__(2, (1 << 25) + 8), _abi.ERR_LAYOUT),
+    (lambda a: setattr(a, "workspace", None), _abi.ERR_WORKSPACE),
+    (lambda a: setattr(a, "workspace_bytes", a.workspace_bytes - 4), _abi.ERR_WORKSPACE),
+    (lambda a: setattr(a, "workspace", FAKE + 8), _abi.ERR_WORKSPACE),
 ])
 def test_fwd_validator_rejects(mutate, code):
     lib = _lib()
@@ -196,6 +202,10 @@ def test_buffer_sizes():
     assert lib.tda_norms_floats(4, 16, 4096, 2) == 4 * 64 * 4096
     assert lib.tda_norms_floats(1, 8, 128, 1) == 2 * 8 * 128
     assert lib.tda_bwd_workspace_bytes(4, 16, 4096, 128) == 64 * 128 * 2 * 4
+    # bitmask scratch, rounded up to 256 bytes
+    assert lib.tda_fwd_workspace_bytes(4, 16, 4096, 2) == 2 * 64 * 128 * 4 * 4
+    assert lib.tda_fwd_workspace_bytes(1, 1, 33, 1) == 256
+    assert lib.tda_fwd_workspace_bytes(1, 1, 33, 3) == 0
     assert lib.tda_occupancy_words(0, 1, 1, 1) == 0
 
 
