@@ -101,6 +101,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 1 GiB device copy 3 times (calibrates HBM byte counters)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); the op shards "
@@ -114,6 +116,15 @@ def main(argv=None) -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        # a copy kernel of known size: reads and writes 2^30 bytes per dispatch
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": 1 << 30, "copy_probe_bytes_written": 1 << 30, "dispatches": 3}))
+        return 0
     g = torch.Generator("cpu").manual_seed(2)
     xs = [torch.randn(SHAPE, generator=g).to(torch.bfloat16).to(dev) for _ in range(5)]
     do = torch.randn(SHAPE, generator=torch.Generator("cpu").manual_seed(3)).to(torch.bfloat16).to(dev)

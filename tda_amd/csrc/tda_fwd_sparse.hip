@@ -76,43 +76,61 @@ __device__ __forceinline__ WorkItem xcd_order(int bid, int nstreams, int nblocks
 }
 
 // ------------------------------------------------------------------ key_norms
-// Inverse L2 norms of the key rows of every branch.  One group of D/8 lanes per row (16 bytes
-// per lane), rows in order, so each load instruction covers whole rows.
+// Inverse L2 norms of the key rows of every branch.  A group of D/8 lanes reads one row (16
+// bytes per lane, whole rows per load instruction); each wave covers KN_ROWS consecutive rows
+// of one (branch, head) with all its loads issued before the first reduction.
+constexpr int KN_GROUPS = 4;  // row groups per wave
 template <int D>
 __global__ void __launch_bounds__(256) key_norms(FwdParams P, int BR) {
-  constexpr int LPR = D / 8;  // lanes per row
+  constexpr int LPR = D / 8;        // lanes per row
+  constexpr int RPG = 64 / LPR;     // rows per load instruction
+  constexpr int ROWS = RPG * KN_GROUPS;
+  const int l = lane_id(), sub = l % LPR;
   const int BH = P.B * P.H, N = P.N;
-  const int64_t rows = (int64_t)BH * N;
-  const int sub = threadIdx.x % LPR;
-  const int64_t gid = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPR;  // row id over branches
-  const int br = (int)(gid / rows);
-  const int64_t rid = gid - (int64_t)br * rows;
-  const bool ok = br < BR;
-  float ss = 0.f;
-  if (ok) {
-    const int slot = br ? F_K2 : F_K1;
-    const int bh = (int)(rid / N), t = (int)(rid % N);
-    const bf16* row = (const bf16*)P.in[slot] + (int64_t)(bh / P.H) * P.s[slot][0] +
-                      (int64_t)(bh % P.H) * P.s[slot][1] + (int64_t)t * P.s[slot][2];
-    ss = PolBF16::sumsq(*reinterpret_cast<const bf16x8*>(row + 8 * sub));
-  }
+  const int wpr = (N + ROWS - 1) / ROWS;  // waves per (branch, head)
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wid >= (int64_t)BR * BH * wpr) return;  // whole wave, no barriers
+  const int sidx = (int)(wid / wpr), br = sidx / BH, bh = sidx % BH;
+  const int t0 = (int)(wid % wpr) * ROWS + l / LPR;
+  const int slot = br ? F_K2 : F_K1;
+  const int64_t st = P.s[slot][2];
+  const bf16* head = (const bf16*)P.in[slot] + (int64_t)(bh / P.H) * P.s[slot][0] + (int64_t)(bh % P.H) * P.s[slot][1];
+  bf16x8 x[KN_GROUPS];
 #pragma unroll
-  for (int o = LPR / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-  if (ok && sub == 0) P.norms[(int64_t)(br ? N_K2 : N_K1) * rows + rid] = inv_norm(ss);
+  for (int u = 0; u < KN_GROUPS; ++u) {
+    const int t = min(t0 + RPG * u, N - 1);
+    x[u] = *reinterpret_cast<const bf16x8*>(head + (int64_t)t * st + 8 * sub);
+  }
+  float* out = P.norms + ((int64_t)(br ? N_K2 : N_K1) * BH + bh) * N;
+#pragma unroll
+  for (int u = 0; u < KN_GROUPS; ++u) {
+    float ss = PolBF16::sumsq(x[u]);
+#pragma unroll
+    for (int o = LPR / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    const int t = t0 + RPG * u;
+    if (sub == 0 && t < N) out[t] = inv_norm(ss);
+  }
 }
 
 // ------------------------------------------------------------------ fwd_screen
-// Workgroup = 4 waves x 64 query rows (two 32-row query tiles per wave) of one branch of one
-// head; grid = branches x heads x ceil(N / 256).  Key tiles stream through a 3-stage LDS ring
-// (buffer loads into VGPRs one tile ahead, LDS writes two tiles ahead of use, one barrier per
-// tile).  Score tiles are computed transposed, S^T = K Q^T, so each lane holds one query.
-template <int D, bool NORM>
-__global__ void __launch_bounds__(256, 2) fwd_screen(FwdParams P, int BR) {
-  constexpr int NT = D / 16;   // MFMA steps over d
-  constexpr int KS = D + 8;    // LDS row stride (elements): conflict-free 16-byte fragment reads
-  constexpr int TPR = D / 16;  // staging threads per row, two 16-byte chunks each
-  __shared__ __attribute__((aligned(16))) bf16 kst[3][32 * KS];
-  __shared__ __attribute__((aligned(16))) float krk[3][32];  // inverse key norms of the tile
+// Workgroup = 256 query rows of one branch of one head, QPW 32-row query tiles per wave
+// (8 / QPW waves); grid = branches x heads x ceil(N / 256).  Key tiles stream through LDS in
+// groups of TPB tiles ("super-stages", two of them in a ring): buffer loads into VGPRs one
+// iteration ahead, LDS writes of the next group while the current one is read, one barrier per
+// group.  Score tiles are computed transposed, S^T = K Q^T, so each lane holds one query.
+// Dispatch uses QPW = 2 (three waves per SIMD at 152 VGPRs) and TPB = 1: one query tile per
+// wave (twice the LDS fragment reads per MFMA) and larger groups (fewer waves) both measured
+// slower at the headline shape.
+template <int D, bool NORM, int QPW, int TPB>
+__global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) {
+  constexpr int NT = D / 16;                // MFMA steps over d
+  constexpr int KS = D + 8;                 // LDS row stride (elements): conflict-free fragment reads
+  constexpr int NTHR = 512 / QPW;           // threads per workgroup
+  constexpr int CPR = D / 8;                // 16-byte chunks per key row
+  constexpr int TPR = CPR < NTHR / 32 ? CPR : NTHR / 32;  // staging threads per row
+  constexpr int CPT = CPR / TPR;            // chunks per staging thread
+  __shared__ __attribute__((aligned(16))) bf16 kst[2 * TPB][32 * KS];
+  __shared__ __attribute__((aligned(16))) float krk[2 * TPB][32];  // inverse key norms of each tile
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5, tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -122,10 +140,13 @@ __global__ void __launch_bounds__(256, 2) fwd_screen(FwdParams P, int BR) {
   const int br = sidx / BH, bh = sidx % BH;
   const int b = bh / P.H, h = bh % P.H;
   const int qslot = br ? F_Q2 : F_Q1, kslot = br ? F_K2 : F_K1;
-  const int q0w = qb * 256 + 64 * wv;  // first row of this wave
-  const int qt0 = q0w >> 5;            // this wave's query tiles: qt0, qt0 + 1
+  const int q0w = qb * 256 + 32 * QPW * wv;  // first row of this wave
+  const int qt0 = q0w >> 5;                  // this wave's query tiles: qt0 .. qt0 + QPW - 1
   const int nkt = min(nqt, 8 * qb + 8);
-  const bool live0 = qt0 < nqt, live1 = qt0 + 1 < nqt;
+  const int nit = (nkt + TPB - 1) / TPB;
+  bool live[QPW];
+#pragma unroll
+  for (int s = 0; s < QPW; ++s) live[s] = qt0 + s < nqt;
 
   // ---- staging
   const bf16* khead = (const bf16*)P.in[kslot] + (int64_t)b * P.s[kslot][0] + (int64_t)h * P.s[kslot][1];
@@ -136,39 +157,51 @@ __global__ void __launch_bounds__(256, 2) fwd_screen(FwdParams P, int BR) {
   // key norms: threads 0..7 stage four rows each (rows past N read as 0, never used)
   const __amdgpu_buffer_rsrc_t rnorm =
       make_rsrc(NORM ? P.norms + ((int64_t)(br ? N_K2 : N_K1) * BH + bh) * N : nullptr, NORM ? (uint32_t)N * 4 : 0u);
-  u32x4 R0 = {}, R1 = {}, RN = {};
-  auto fetch = [&](int kt) {
-    if (stager) {
-      const __amdgpu_buffer_rsrc_t rs = tile_rsrc<D>(khead, sk, kt, N);
-      R0 = buf_load16(rs, soff);
-      R1 = buf_load16(rs, soff + 16 * TPR);
+  u32x4 R[TPB][CPT], RN[TPB];
+  auto fetch = [&](int it) {  // tiles of group it into registers
+#pragma unroll
+    for (int j = 0; j < TPB; ++j) {
+      const int kt = TPB * it + j;
+      if (kt >= nkt) break;
+      if (stager) {
+        const __amdgpu_buffer_rsrc_t rs = tile_rsrc<D>(khead, sk, kt, N);
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) R[j][c] = buf_load16(rs, soff + 16 * TPR * c);
+      }
+      if constexpr (NORM)
+        if (tid < 8) RN[j] = buf_load16(rnorm, (uint32_t)(32 * kt + 4 * tid) * 4);
     }
-    if constexpr (NORM)
-      if (tid < 8) RN = buf_load16(rnorm, (uint32_t)(32 * kt + 4 * tid) * 4);
   };
-  auto commit = [&](int s) {
-    if (stager) {
-      bf16* k = &kst[s][srow * KS + 8 * sch];
-      *reinterpret_cast<u32x4*>(k) = R0;
-      *reinterpret_cast<u32x4*>(k + 8 * TPR) = R1;
+  auto commit = [&](int it) {  // group it into its super-stage
+#pragma unroll
+    for (int j = 0; j < TPB; ++j) {
+      const int kt = TPB * it + j;
+      if (kt >= nkt) break;
+      const int st = TPB * (it & 1) + j;
+      if (stager) {
+        bf16* k = &kst[st][srow * KS + 8 * sch];
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) *reinterpret_cast<u32x4*>(k + 8 * TPR * c) = R[j][c];
+      }
+      if constexpr (NORM)
+        if (tid < 8) *reinterpret_cast<u32x4*>(&krk[st][4 * tid]) = RN[j];
     }
-    if constexpr (NORM)
-      if (tid < 8) *reinterpret_cast<u32x4*>(&krk[s][4 * tid]) = RN;
   };
 
   // ---- resident query fragments, inverse norms, thresholds
   const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
   const float beta = *P.beta;
-  bf16x8 Q[2][NT];
-  float rq[2] = {1.f, 1.f}, tau[2];
-  bool valid[2];
+  bf16x8 Q[QPW][NT];
+  float rq[QPW], tau[QPW];
+  bool valid[QPW];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
+  for (int s = 0; s < QPW; ++s) {
     const int iq = q0w + 32 * s + n32;
     valid[s] = iq < N;
     const bf16* row = qhead + (int64_t)min(iq, N - 1) * P.s[qslot][2];  // rows >= N: never vote
 #pragma unroll
     for (int t = 0; t < NT; ++t) Q[s][t] = *reinterpret_cast<const bf16x8*>(row + 16 * t + 8 * g);
+    rq[s] = 1.f;
     if constexpr (NORM) {
       rq[s] = inv_norm(row_sumsq<PolBF16, NT>(Q[s]));
       if (g == 0 && valid[s]) P.norms[((int64_t)(br ? N_Q2 : N_Q1) * BH + bh) * N + iq] = rq[s];
@@ -176,71 +209,82 @@ __global__ void __launch_bounds__(256, 2) fwd_screen(FwdParams P, int BR) {
     tau[s] = beta * tau_coeff(iq, P.inv_d);
   }
 
-  uint32_t* occ0 = P.occ + ((int64_t)sidx * nqt + qt0) * P.occ_w;  // bitmask rows of qt0, qt0 + 1
-  uint32_t word0 = 0u, word1 = 0u;
+  uint32_t* occ0 = P.occ + ((int64_t)sidx * nqt + qt0) * P.occ_w;  // bitmask row of qt0 (then qt0 + 1)
+  uint32_t word[QPW];
+#pragma unroll
+  for (int s = 0; s < QPW; ++s) word[s] = 0u;
   unsigned visited = 0;
   const int koff = n32 * KS + 8 * g;
 
+  // Threshold test of key tile kt (in stage st) against this wave's query tiles.
+  auto process = [&](int kt, int st) {
+    if (!(live[0] && kt <= qt0 + QPW - 1)) return;
+    const bf16* kp = &kst[st][koff];
+    bf16x8 fk[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) fk[t] = *reinterpret_cast<const bf16x8*>(kp + 16 * t);
+    __builtin_amdgcn_sched_barrier(0);  // all fragment reads in flight before the first MFMA
+    f32x16 S[QPW];
+#pragma unroll
+    for (int s = 0; s < QPW; ++s) S[s] = f32x16{};
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int s = 0; s < QPW; ++s) S[s] = PolBF16::mma(fk[t], Q[s][t], S[s]);
+    // largest s_ij rk_j per lane; x = fma(s rk, rq, -tau) is monotone in s rk (rq > 0), so
+    // "fma(max, rq, -tau) > 0" is exactly "some x_ij > 0" for the lane's keys
+    if constexpr (NORM) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f32x4 r4 = *reinterpret_cast<const f32x4*>(&krk[st][8 * u + 4 * g]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int s = 0; s < QPW; ++s) S[s][4 * u + e] *= r4[e];
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < QPW; ++s) {
+      const float bnd = __builtin_fmaf(max16(S[s]), rq[s], -tau[s]);
+      const bool in = kt <= qt0 + s;  // key tiles after the query tile hold no causal pair
+      const bool any = wave_ballot(in && valid[s] && bnd > 0.f) != 0ull;
+      word[s] |= (uint32_t)any << (kt & 31);
+      visited += (unsigned)(in && live[s]);
+    }
+  };
+  // bitmask words of this wave's rows: word kt/32 is complete after key tile kt
+  auto flush = [&](int kt) {
+    if (live[0] && ((kt & 31) == 31 || kt == nkt - 1)) {
+      if (l == 0) {
+#pragma unroll
+        for (int s = 0; s < QPW; ++s) {
+          if (!live[s]) continue;
+          uint32_t* row = occ0 + s * P.occ_w;
+          row[kt >> 5] = word[s];
+          if (kt == nkt - 1)  // words of key tiles this workgroup never reaches
+            for (int w = (kt >> 5) + 1; w < P.occ_w; ++w) row[w] = 0u;
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < QPW; ++s) word[s] = 0u;
+    }
+  };
+
   fetch(0);
   commit(0);
-  if (nkt > 1) {
-    fetch(1);
-    commit(1);
-  }
-  if (nkt > 2) fetch(2);
+  if (nit > 1) fetch(1);
   __syncthreads();
-
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int s = kt % 3;
-    if (live0 && kt <= qt0 + 1) {
-      const bf16* kp = &kst[s][koff];
-      bf16x8 fk[NT];
+  for (int it = 0; it < nit; ++it) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) fk[t] = *reinterpret_cast<const bf16x8*>(kp + 16 * t);
-      f32x16 S0 = {}, S1 = {};
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        S0 = PolBF16::mma(fk[t], Q[0][t], S0);
-        S1 = PolBF16::mma(fk[t], Q[1][t], S1);
-      }
-      // largest s_ij rk_j per lane; x = fma(s rk, rq, -tau) is monotone in s rk (rq > 0), so
-      // "fma(max, rq, -tau) > 0" is exactly "some x_ij > 0" for the lane's keys
-      if constexpr (NORM) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const f32x4 r4 = *reinterpret_cast<const f32x4*>(&krk[s][8 * u + 4 * g]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            S0[4 * u + e] *= r4[e];
-            S1[4 * u + e] *= r4[e];
-          }
-        }
-      }
-      const float b0 = __builtin_fmaf(max16(S0), rq[0], -tau[0]);
-      const float b1 = __builtin_fmaf(max16(S1), rq[1], -tau[1]);
-      const bool in0 = kt <= qt0;  // key tile qt0 + 1 lies wholly after query tile qt0
-      const bool a0 = wave_ballot(in0 && valid[0] && b0 > 0.f) != 0ull;
-      const bool a1 = wave_ballot(valid[1] && b1 > 0.f) != 0ull;
-      word0 |= (uint32_t)a0 << (kt & 31);
-      word1 |= (uint32_t)a1 << (kt & 31);
-      visited += (unsigned)in0 + (unsigned)live1;
+    for (int j = 0; j < TPB; ++j) {
+      const int kt = TPB * it + j;
+      if (kt >= nkt) break;
+      process(kt, TPB * (it & 1) + j);
+      flush(kt);
     }
-    // bitmask words of rows qt0 and qt0 + 1: word kt/32 is complete after key tile kt
-    if (live0 && ((kt & 31) == 31 || kt == nkt - 1)) {
-      if (l == 0) {
-        occ0[kt >> 5] = word0;
-        if (live1) occ0[P.occ_w + (kt >> 5)] = word1;
-        if (kt == nkt - 1) {  // words of key tiles this workgroup never reaches
-          for (int w = (kt >> 5) + 1; w < P.occ_w; ++w) {
-            occ0[w] = 0u;
-            if (live1) occ0[P.occ_w + w] = 0u;
-          }
-        }
-      }
-      word0 = word1 = 0u;
-    }
-    if (kt + 2 < nkt) commit((kt + 2) % 3);
-    if (kt + 3 < nkt) fetch(kt + 3);
+    // the other super-stage was last read before the previous barrier
+    if (it + 1 < nit) commit(it + 1);
+    if (it + 2 < nit) fetch(it + 2);
     __syncthreads();
   }
   if (P.stats && l == 0 && visited) atomicAdd(P.stats + 0, (unsigned long long)visited);
@@ -401,11 +445,13 @@ template <int D, int BR, int PK, bool NORM>
 int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   const int BH = p.B * p.H;
   if constexpr (NORM) {
-    const int64_t lanes = (int64_t)BR * BH * p.N * (D / 8);
-    hipLaunchKernelGGL(key_norms<D>, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, s, p, BR);
+    constexpr int rows = (64 / (D / 8)) * KN_GROUPS;  // rows per wave
+    const int64_t waves = (int64_t)BR * BH * ((p.N + rows - 1) / rows);
+    hipLaunchKernelGGL(key_norms<D>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, BR);
   }
   const unsigned nqb = (unsigned)((p.N + 255) / 256);
-  hipLaunchKernelGGL((fwd_screen<D, NORM>), dim3((unsigned)(BR * BH) * nqb), dim3(256), 0, s, p, BR);
+  constexpr int QPW = 2, TPB = 1;
+  hipLaunchKernelGGL((fwd_screen<D, NORM, QPW, TPB>), dim3((unsigned)(BR * BH) * nqb), dim3(512 / QPW), 0, s, p, BR);
   const unsigned nblk = (unsigned)((p.nqt + 3) / 4);
   hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)BH * nblk), dim3(256), 0, s, p);
   return (int)hipGetLastError();
