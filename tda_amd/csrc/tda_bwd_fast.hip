@@ -140,17 +140,21 @@ struct BwdWaveLds {
   float taus[32];  // tau coefficients of the query rows (dkv)
 };
 
+// Waves per workgroup of both passes.  The work per item varies with its number of non-zero
+// tiles; single-wave workgroups retire independently.
+constexpr int kBwdWaves = 1;
+
 // ------------------------------------------------------------------ query-major pass
 template <int D, int BR, int PK, bool NORM>
-__global__ void __launch_bounds__(256) bwd_dq_fast(BwdParams P) {
+__global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
   constexpr int NT = D / 16, ND = D / 32;
-  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> lds_all[4];
+  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> lds_all[kBwdWaves];
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   BwdWaveLds<D>& W = lds_all[wv];
   const int BH = P.B * P.H;
-  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+  const int64_t item = (int64_t)blockIdx.x * kBwdWaves + wv;
   if (item >= (int64_t)BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
   const int qt = P.nqt - 1 - (int)(item / BH);
   const int bh = (int)(item % BH);
@@ -272,15 +276,15 @@ __global__ void __launch_bounds__(256) bwd_dq_fast(BwdParams P) {
 
 // ------------------------------------------------------------------ key-major pass
 template <int D, int BR, int PK, bool NORM>
-__global__ void __launch_bounds__(256) bwd_dkv_fast(BwdParams P) {
+__global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
   constexpr int NT = D / 16, ND = D / 32;
-  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> lds_all[4];
+  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> lds_all[kBwdWaves];
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   BwdWaveLds<D>& W = lds_all[wv];
   const int BH = P.B * P.H;
-  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+  const int64_t item = (int64_t)blockIdx.x * kBwdWaves + wv;
   if (item >= (int64_t)BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
   const int kt = (int)(item / BH);
   const int bh = (int)(item % BH);
@@ -405,10 +409,10 @@ __global__ void __launch_bounds__(256) bwd_dkv_fast(BwdParams P) {
 template <int D, int BR, int PK, bool NORM>
 static int launch_t(const BwdParams& p, void* stream) {
   const int64_t items = (int64_t)p.B * p.H * p.nqt;
-  const unsigned grid = (unsigned)((items + 3) / 4);
+  const unsigned grid = (unsigned)((items + kBwdWaves - 1) / kBwdWaves);
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3(grid), dim3(256), 0, s, p);
-  hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3(grid), dim3(64 * kBwdWaves), 0, s, p);
+  hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3(grid), dim3(64 * kBwdWaves), 0, s, p);
   const int e = (int)hipGetLastError();
   return e ? e : launch_bwd_finish(p, BR, stream);
 }

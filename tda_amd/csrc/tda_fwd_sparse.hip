@@ -301,20 +301,23 @@ __device__ __forceinline__ bf16x8 tr_frag(const bf16* p) {
   return bf16x8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
 }
 
-// One wave per query tile (workgroup = 4 consecutive tiles of one head); no barriers.
+// One wave per query tile and one wave per workgroup: the work per query tile varies with its
+// number of non-zero tiles, and single-wave workgroups retire independently (a 4-wave
+// workgroup would hold its slot until its slowest wave ends).  No barriers.
+constexpr int kPvWaves = 1;  // waves per workgroup
 template <int D, int BR, int PK, bool NORM>
-__global__ void __launch_bounds__(256, 2) fwd_pv(FwdParams P) {
+__global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per_eu(2))) fwd_pv(FwdParams P) {
   constexpr int NT = D / 16, ND = D / 32;
   constexpr int VS = D + 32;     // LDS row stride of a V tile: conflict-free transpose reads
   constexpr int CPR = D / 8;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;  // rows per V load instruction
   constexpr int VL = 32 / RPI;   // V load instructions per tile
-  __shared__ __attribute__((aligned(16))) bf16 vst[4][32 * VS];
+  __shared__ __attribute__((aligned(16))) bf16 vst[kPvWaves][32 * VS];
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int BH = P.B * P.H, N = P.N, nqt = P.nqt;
-  const int nblk = (nqt + 3) / 4;
+  const int nblk = (nqt + kPvWaves - 1) / kPvWaves;
   int bh, blk;
   {
     const int bid = blockIdx.x;
@@ -327,7 +330,7 @@ __global__ void __launch_bounds__(256, 2) fwd_pv(FwdParams P) {
       blk = nblk - 1 - bid % nblk;
     }
   }
-  const int qt = 4 * blk + wv;
+  const int qt = kPvWaves * blk + wv;
   if (qt >= nqt) return;
   const int b = bh / P.H, h = bh % P.H;
   const int iq = 32 * qt + n32;
@@ -452,8 +455,8 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   const unsigned nqb = (unsigned)((p.N + 255) / 256);
   constexpr int QPW = 2, TPB = 1;
   hipLaunchKernelGGL((fwd_screen<D, NORM, QPW, TPB>), dim3((unsigned)(BR * BH) * nqb), dim3(512 / QPW), 0, s, p, BR);
-  const unsigned nblk = (unsigned)((p.nqt + 3) / 4);
-  hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)BH * nblk), dim3(256), 0, s, p);
+  const unsigned nblk = (unsigned)((p.nqt + kPvWaves - 1) / kPvWaves);
+  hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)BH * nblk), dim3(64 * kPvWaves), 0, s, p);
   return (int)hipGetLastError();
 }
 
