@@ -312,7 +312,9 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
   constexpr int CPR = D / 8;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;  // rows per V load instruction
   constexpr int VL = 32 / RPI;   // V load instructions per tile
+  constexpr int KS = D + 8;      // LDS row stride of a K tile: conflict-free row-fragment reads
   __shared__ __attribute__((aligned(16))) bf16 vst[kPvWaves][32 * VS];
+  __shared__ __attribute__((aligned(16))) bf16 kst[kPvWaves][32 * KS];
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -341,6 +343,7 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
   if constexpr (BR == 2) lam = clamp01(*P.lam);
 
   bf16* vt = vst[wv];
+  bf16* ktl = kst[wv];
   const int vrow = l / CPR, vch = l % CPR;
   const int bk = l >> 4, jj = l & 15;
   const int voff = (4 * (bk >> 1) + (jj >> 2)) * VS + 16 * (bk & 1) + 4 * (jj & 3);
@@ -380,10 +383,10 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
         // loads of the key tile (A operand rows), the V tile and the key norms
         const __amdgpu_buffer_rsrc_t rk = tile_rsrc<D>(khead, sk, kt, N);
         const __amdgpu_buffer_rsrc_t rv = tile_rsrc<D>(vhead, sv, kt, N);
-        bf16x8 fk[NT];
+        // whole rows per load instruction (coalesced), staged through LDS like V
+        u32x4 kr[VL];
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-          fk[t] = __builtin_bit_cast(bf16x8, buf_load16(rk, (uint32_t)((n32 * sk + 16 * t + 8 * g) * 2)));
+        for (int i = 0; i < VL; ++i) kr[i] = buf_load16(rk, (uint32_t)(((vrow + RPI * i) * sk + 8 * vch) * 2));
         u32x4 vr[VL];
 #pragma unroll
         for (int i = 0; i < VL; ++i) vr[i] = buf_load16(rv, (uint32_t)(((vrow + RPI * i) * sv + 8 * vch) * 2));
@@ -393,9 +396,13 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
           for (int u = 0; u < 4; ++u)
             rk4[u] = __builtin_bit_cast(f32x4, buf_load16(rn, (uint32_t)(32 * kt + 8 * u + 4 * g) * 4));
         }
-        f32x16 S = {};
 #pragma unroll
-        for (int t = 0; t < NT; ++t) S = PolBF16::mma(fk[t], Q[t], S);
+        for (int i = 0; i < VL; ++i) *reinterpret_cast<u32x4*>(ktl + (vrow + RPI * i) * KS + 8 * vch) = kr[i];
+        wave_lds_sync();
+        f32x16 S = {};
+        const bf16* kp = ktl + n32 * KS + 8 * g;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) S = PolBF16::mma(*reinterpret_cast<const bf16x8*>(kp + 16 * t), Q[t], S);
 #pragma unroll
         for (int i = 0; i < VL; ++i) *reinterpret_cast<u32x4*>(vt + (vrow + RPI * i) * VS + 8 * vch) = vr[i];
 
