@@ -373,10 +373,20 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
         const int kt = 32 * w + __builtin_ctz(bits);
         bits &= bits - 1u;
         if (!have_q) {
+          // query tile rows with whole-row loads, through the (still free) K tile buffer
           const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
-          const bf16* row = qhead + (int64_t)min(iq, N - 1) * P.s[qslot][2];
+          const __amdgpu_buffer_rsrc_t rq_ = tile_rsrc<D>(qhead, P.s[qslot][2], qt, N);
+          u32x4 qr[VL];
 #pragma unroll
-          for (int t = 0; t < NT; ++t) Q[t] = *reinterpret_cast<const bf16x8*>(row + 16 * t + 8 * g);
+          for (int i = 0; i < VL; ++i)
+            qr[i] = buf_load16(rq_, (uint32_t)(((vrow + RPI * i) * P.s[qslot][2] + 8 * vch) * 2));
+#pragma unroll
+          for (int i = 0; i < VL; ++i) *reinterpret_cast<u32x4*>(ktl + (vrow + RPI * i) * KS + 8 * vch) = qr[i];
+          wave_lds_sync();
+          const bf16* qp = ktl + n32 * KS + 8 * g;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) Q[t] = *reinterpret_cast<const bf16x8*>(qp + 16 * t);
+          wave_lds_sync();
           if constexpr (NORM) rq = P.norms[((int64_t)(br ? N_Q2 : N_Q1) * BH + bh) * N + min(iq, N - 1)];
           have_q = true;
         }
@@ -439,13 +449,24 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
     }
   }
 
-  if (valid) {
-    bf16* orow = (bf16*)P.out + (int64_t)b * P.s[F_OUT][0] + (int64_t)h * P.s[F_OUT][1] + (int64_t)iq * P.s[F_OUT][2];
+  // Output rows through LDS (the K tile buffer): lane (n, g) holds elements 32c + crow(r, g) of
+  // row n; stores then cover whole rows, 16 bytes per lane.
+  wave_lds_sync();
 #pragma unroll
-    for (int c = 0; c < ND; ++c)
+  for (int c = 0; c < ND; ++c)
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        store4(orow + 32 * c + 8 * u + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2], O[c][4 * u + 3]);
+    for (int u = 0; u < 4; ++u)
+      store4(ktl + n32 * KS + 32 * c + 8 * u + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2], O[c][4 * u + 3]);
+  wave_lds_sync();
+  {
+    bf16* ohead = (bf16*)P.out + (int64_t)b * P.s[F_OUT][0] + (int64_t)h * P.s[F_OUT][1];
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      const int r = vrow + RPI * i, row = 32 * qt + r;
+      if (row < N)
+        *reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch) =
+            *reinterpret_cast<const u32x4*>(ktl + r * KS + 8 * vch);
+    }
   }
   if (P.stats && l == 0 && computed) atomicAdd(P.stats + 1, (unsigned long long)computed);
 }
