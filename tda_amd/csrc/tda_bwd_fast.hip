@@ -92,11 +92,26 @@ __device__ __forceinline__ void crow_vals(const float* tab, float (&v)[16]) {
   }
 }
 
+// This lane's elements of an input row in the transposed C layout of a gradient tile
+// (elements 32c + 8u + 4g .. +3), for the F.normalize backward.
+template <int D>
+struct GradRow {
+  bf16x4 x[D / 32][4];
+};
+template <int D>
+__device__ __forceinline__ void load_grad_row(const bf16* xrow, GradRow<D>& r) {
+  const int g = lane_id() >> 5;
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) r.x[c][u] = *reinterpret_cast<const bf16x4*>(xrow + 32 * c + 8 * u + 4 * g);
+}
+
 // Apply the F.normalize backward to a gradient tile in the transposed C layout (lane = row,
 // value r of column block c = element 32c + crow(r, g)) and store it (see finish_rows in
-// tda_bwd.hip; same arithmetic).
+// tda_bwd.hip; same arithmetic).  xr: the input row (NORM only).
 template <int D, bool NORM>
-__device__ __forceinline__ void store_grad_rows(const f32x16 (&acc)[D / 32], const bf16* xrow, bf16* grow,
+__device__ __forceinline__ void store_grad_rows(const f32x16 (&acc)[D / 32], const GradRow<D>& xr, bf16* grow,
                                                 float rinv) {
   constexpr int ND = D / 32;
   const int g = lane_id() >> 5;
@@ -107,10 +122,9 @@ __device__ __forceinline__ void store_grad_rows(const f32x16 (&acc)[D / 32], con
     for (int c = 0; c < ND; ++c)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const f32x4 x = load4(xrow + 32 * c + 8 * u + 4 * g);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          xh[c][u][e] = x[e] * rinv;
+          xh[c][u][e] = (float)xr.x[c][u][e] * rinv;
           dot = __builtin_fmaf(xh[c][u][e], acc[c][4 * u + e], dot);
         }
       }
@@ -184,22 +198,33 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
   unsigned visited = 0, computed = 0;
   const int nw = (qt >> 5) + 1;  // bitmask words covering key tiles 0..qt
 
+  // Both branches' row operands, issued with dO so that one memory round trip covers them:
+  // query fragments, inverse query norms, bitmask words 0..63 (lane w holds word w).
+  bf16x8 QB[BR][NT];
+  float RQ[BR];
+  uint32_t LW[BR];
+#pragma unroll
+  for (int br = 0; br < BR; ++br) {
+    const int qslot = br == 0 ? B_Q1 : B_Q2;
+    const bf16* r = base(qslot) + (int64_t)ic * P.s[qslot][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) QB[br][t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+    RQ[br] = NORM ? P.norms[((int64_t)(br == 0 ? N_Q1 : N_Q2) * BH + bh) * N + ic] : 1.f;
+    const uint32_t* occrow = P.occ ? P.occ + (((int64_t)br * BH + bh) * P.nqt + qt) * P.occ_w : nullptr;
+    LW[br] = l < nw ? (occrow ? occrow[l] : 0xffffffffu) : 0u;
+  }
+
+#pragma unroll
   for (int br = 0; br < BR; ++br) {
     const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
     const bf16* kb = base(kslot);
     const int64_t sk = P.s[kslot][2];
-    bf16x8 Q[NT];
-    {
-      const bf16* r = base(qslot) + (int64_t)ic * P.s[qslot][2];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) Q[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
-    }
-    float rq = 1.f;
+    const bf16x8 (&Q)[NT] = QB[br];
+    GradRow<D> XR;  // the query row for the normalize backward, in flight during the tiles
+    if constexpr (NORM) load_grad_row<D>(base(qslot) + (int64_t)ic * P.s[qslot][2], XR);
+    const float rq = RQ[br];
     const float* nk = nullptr;
-    if constexpr (NORM) {
-      rq = P.norms[((int64_t)(br == 0 ? N_Q1 : N_Q2) * BH + bh) * N + ic];
-      nk = P.norms + ((int64_t)(br == 0 ? N_K1 : N_K2) * BH + bh) * N;
-    }
+    if constexpr (NORM) nk = P.norms + ((int64_t)(br == 0 ? N_K1 : N_K2) * BH + bh) * N;
     const float coef = br == 0 ? 1.f : -lam;
     f32x16 A[ND];
 #pragma unroll
@@ -207,7 +232,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
     const uint32_t* occrow = P.occ ? P.occ + (((int64_t)br * BH + bh) * P.nqt + qt) * P.occ_w : nullptr;
 
     for (int w0 = 0; w0 < nw; w0 += 64) {
-      const uint32_t lw = (w0 + l < nw) ? (occrow ? occrow[w0 + l] : 0xffffffffu) : 0u;
+      const uint32_t lw = w0 == 0 ? LW[br] : (w0 + l < nw) ? (occrow ? occrow[w0 + l] : 0xffffffffu) : 0u;
       for (int w = w0; w < min(nw, w0 + 64); ++w) {
         uint32_t bits = __builtin_amdgcn_readlane(lw, w - w0);
         if (w == (qt >> 5)) bits &= (qt & 31) == 31 ? 0xffffffffu : ((2u << (qt & 31)) - 1u);
@@ -254,11 +279,10 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
       }
     }
     if (qvalid) {
-      const bf16* qrow = base(qslot) + (int64_t)i * P.s[qslot][2];
       const int gslot = br == 0 ? B_DQ1 : B_DQ2;
       bf16* grow = (bf16*)P.grad[br == 0 ? 0 : 2] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
                    (int64_t)i * P.s[gslot][2];
-      store_grad_rows<D, NORM>(A, qrow, grow, rq);
+      store_grad_rows<D, NORM>(A, XR, grow, rq);
     }
   }
 
@@ -314,22 +338,35 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
   for (int c = 0; c < ND; ++c) AV[c] = f32x16{};
   unsigned visited = 0, computed = 0;
 
+  // Both branches' row operands, issued with V so that one memory round trip covers them: key
+  // fragments, inverse key norms, and the bitmask column bits of query tiles kt .. kt+63
+  // (lane q holds tile kt + q).
+  bf16x8 KB[BR][NT];
+  float RK[BR];
+  bool HAS[BR];
+#pragma unroll
+  for (int br = 0; br < BR; ++br) {
+    const int kslot = br == 0 ? B_K1 : B_K2;
+    const bf16* r = base(kslot) + (int64_t)jc * P.s[kslot][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) KB[br][t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+    RK[br] = NORM ? P.norms[((int64_t)(br == 0 ? N_K1 : N_K2) * BH + bh) * N + jc] : 1.f;
+    const uint32_t* occcol = P.occ ? P.occ + ((int64_t)br * BH + bh) * P.nqt * P.occ_w + (kt >> 5) : nullptr;
+    const int qtl = kt + l;
+    HAS[br] = qtl < P.nqt && (!occcol || ((occcol[(int64_t)qtl * P.occ_w] >> (kt & 31)) & 1u));
+  }
+
+#pragma unroll
   for (int br = 0; br < BR; ++br) {
     const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
     const bf16* qb = base(qslot);
     const int64_t sq = P.s[qslot][2];
-    bf16x8 K[NT];
-    {
-      const bf16* r = base(kslot) + (int64_t)jc * P.s[kslot][2];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) K[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
-    }
-    float rk = 1.f;
+    const bf16x8 (&K)[NT] = KB[br];
+    GradRow<D> XR;  // the key row for the normalize backward, in flight during the tiles
+    if constexpr (NORM) load_grad_row<D>(base(kslot) + (int64_t)jc * P.s[kslot][2], XR);
+    const float rk = RK[br];
     const float* nq = nullptr;
-    if constexpr (NORM) {
-      rk = P.norms[((int64_t)(br == 0 ? N_K1 : N_K2) * BH + bh) * N + jc];
-      nq = P.norms + ((int64_t)(br == 0 ? N_Q1 : N_Q2) * BH + bh) * N;
-    }
+    if constexpr (NORM) nq = P.norms + ((int64_t)(br == 0 ? N_Q1 : N_Q2) * BH + bh) * N;
     const float coef = br == 0 ? 1.f : -lam;
     f32x16 AK[ND];
 #pragma unroll
@@ -339,7 +376,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
 
     for (int q0c = kt; q0c < P.nqt; q0c += 64) {
       const int qtl = q0c + l;
-      const bool has = qtl < P.nqt && (!occcol || ((occcol[(int64_t)qtl * P.occ_w] >> (kt & 31)) & 1u));
+      const bool has = q0c == kt ? HAS[br] : qtl < P.nqt && (!occcol || ((occcol[(int64_t)qtl * P.occ_w] >> (kt & 31)) & 1u));
       uint64_t mask = wave_ballot(has);
       while (mask) {
         const int qt = q0c + __builtin_ctzll(mask);
@@ -388,16 +425,15 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
       }
     }
     if (kvalid) {
-      const bf16* krow = base(kslot) + (int64_t)j * P.s[kslot][2];
       const int gslot = br == 0 ? B_DK1 : B_DK2;
       bf16* grow = (bf16*)P.grad[br == 0 ? 1 : 3] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
                    (int64_t)j * P.s[gslot][2];
-      store_grad_rows<D, NORM>(AK, krow, grow, rk);
+      store_grad_rows<D, NORM>(AK, XR, grow, rk);
     }
   }
   if (kvalid) {
     bf16* vrow = (bf16*)P.grad[4] + (int64_t)b * P.s[B_DV][0] + (int64_t)h * P.s[B_DV][1] + (int64_t)j * P.s[B_DV][2];
-    store_grad_rows<D, false>(AV, nullptr, vrow, 1.f);
+    store_grad_rows<D, false>(AV, GradRow<D>{}, vrow, 1.f);
   }
   if (P.stats && l == 0) {
     atomicAdd(P.stats + 0, (unsigned long long)visited);

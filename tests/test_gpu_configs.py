@@ -123,36 +123,44 @@ def test_c4_long_context(p):
     assert computed / visited < 0.01  # ultra-sparse: almost every tile is skipped
 
 
-def test_occupancy_and_norms_match_oracle():
-    """The forward's side outputs (tile bitmask, inverse row norms) against the oracle on
-    two heads of the headline shape."""
+@pytest.mark.parametrize("shape,heads", [
+    ((4, 16, 4096, 128), (0, 63)),  # headline shape: the screen splits key ranges in 64-tile chunks
+    ((1, 3, 3100, 128), (0, 1, 2)),  # 32-tile chunks and a ragged last tile
+])
+def test_occupancy_and_norms_match_oracle(shape, heads):
+    """The forward's side outputs (tile bitmask, inverse row norms) against the oracle."""
     from tda_amd import ops
-    shape = (4, 16, 4096, 128)
     xs = make_inputs(shape, 2, 5, BF)
     q1, q2, k1, k2, v = xs
     beta = torch.full((), 1.0, device="cuda")
     lam = torch.full((), 0.5, device="cuda")
     norms, occ = ops.side_buffers(shape, 2, True, "cuda")
-    ops.forward(q1, k1, q2, k2, v, beta, lam, 2.0, True, 2, norms=norms, occupancy=occ)
-    BH, N = 64, 4096
+    out = ops.forward(q1, k1, q2, k2, v, beta, lam, 2.0, True, 2, norms=norms, occupancy=occ)
+    B, H, N, d = shape
+    bhs = [divmod(bh, H) for bh in heads]
+    ref = oracle_out(q1, q2, k1, k2, v, 1.0, 0.5, 2.0, True, 2, heads=bhs, dtype=torch.float32)
+    assert rel_err(heads_of(out, bhs), heads_of(ref, bhs)) <= 2e-2
+    BH, nqt = B * H, (N + 31) // 32
     nrm = norms.view(4, BH, N).cpu()
     for slot, x in enumerate((q1, k1, q2, k2)):
         want = 1.0 / x.float().norm(dim=-1).clamp_min(1e-12).reshape(BH, N).cpu()
         torch.testing.assert_close(nrm[slot], want, rtol=1e-5, atol=0)
-    nqt = N // 32
     words = occ.view(2, BH, nqt, -1).cpu()
-    bits = ((words.unsqueeze(-1).to(torch.int64) >> torch.arange(32)) & 1).reshape(2, BH, nqt, -1)[..., :nqt]
-    t = tau(N, 128, 1.0, dtype=torch.float32)[:, None]
+    nw = words.shape[-1]
+    bits = ((words.unsqueeze(-1).to(torch.int64) >> torch.arange(32)) & 1).reshape(2, BH, nqt, 32 * nw)
+    assert not bits[..., nqt:].any()  # words past the last key tile stay clear
+    t = tau(N, d, 1.0, dtype=torch.float32)[:, None]
     causal = torch.ones(N, N, dtype=torch.bool).tril()
     mism = 0
-    for bh in (0, 63):
-        b, h = divmod(bh, 16)
+    for bh in heads:
+        b, h = divmod(bh, H)
         for br, (q, k) in enumerate(((q1, k1), (q2, k2))):
             qf = torch.nn.functional.normalize(q[b, h].float().cpu(), dim=-1)
             kf = torch.nn.functional.normalize(k[b, h].float().cpu(), dim=-1)
-            nz = ((qf @ kf.T - t) > 0) & causal
+            nz = torch.zeros(32 * nqt, 32 * nqt, dtype=torch.bool)
+            nz[:N, :N] = ((qf @ kf.T - t) > 0) & causal
             tiles = nz.view(nqt, 32, nqt, 32).any(3).any(1)
-            mism += (tiles != bits[br, bh].bool()).sum().item()
+            mism += (tiles != bits[br, bh, :, :nqt].bool()).sum().item()
             assert 0.01 < tiles.float().sum().item() / (nqt * (nqt + 1) / 2) < 0.5
     assert mism <= 4, mism  # only threshold ties within rounding may differ
 
