@@ -418,18 +418,37 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
 }
 
 // Deterministic second stage: fixed-order fp64 sum of the per-wave partials.
-__global__ void __launch_bounds__(256) bwd_finish(const float* ws, int64_t items, const float* lam,
-                                                  float* dbeta, float* dlam, int branches) {
-  __shared__ double sb[256], sl[256];
+constexpr int kFinThreads = 1024;
+__global__ void __launch_bounds__(kFinThreads) bwd_finish(const float* ws, int64_t items, const float* lam,
+                                                          float* dbeta, float* dlam, int branches) {
+  // Each thread issues all its 16-byte loads (two (dbeta, dlambda) pairs each) before summing;
+  // the reduction order is fixed, so the result is bitwise reproducible.
+  __shared__ double sb[kFinThreads], sl[kFinThreads];
+  constexpr int U = 8;  // loads in flight per thread
+  const int64_t nq = items / 2;
+  const f32x4* w4 = reinterpret_cast<const f32x4*>(ws);
   double a = 0.0, c = 0.0;
-  for (int64_t k = threadIdx.x; k < items; k += 256) {
-    a += (double)ws[2 * k];
-    c += (double)ws[2 * k + 1];
+  for (int64_t k0 = 0; k0 < nq; k0 += (int64_t)U * kFinThreads) {
+    f32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k = k0 + (int64_t)u * kFinThreads + threadIdx.x;
+      v[u] = k < nq ? w4[k] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      a += (double)v[u][0] + (double)v[u][2];
+      c += (double)v[u][1] + (double)v[u][3];
+    }
+  }
+  if ((items & 1) && threadIdx.x == 0) {
+    a += (double)ws[2 * items - 2];
+    c += (double)ws[2 * items - 1];
   }
   sb[threadIdx.x] = a;
   sl[threadIdx.x] = c;
   __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
+  for (int o = kFinThreads / 2; o > 0; o >>= 1) {
     if ((int)threadIdx.x < o) {
       sb[threadIdx.x] += sb[threadIdx.x + o];
       sl[threadIdx.x] += sl[threadIdx.x + o];
@@ -481,7 +500,7 @@ static int bsel_d(const BwdParams& p, const KernelKey& k, void* s) {
 
 int launch_bwd_finish(const BwdParams& p, int branches, void* stream) {
   const int64_t items = (int64_t)p.B * p.H * p.nqt;
-  hipLaunchKernelGGL(bwd_finish, dim3(1), dim3(256), 0, (hipStream_t)stream, (const float*)p.ws, items, p.lam,
+  hipLaunchKernelGGL(bwd_finish, dim3(1), dim3(kFinThreads), 0, (hipStream_t)stream, (const float*)p.ws, items, p.lam,
                      p.dbeta, p.dlam, branches);
   return (int)hipGetLastError();
 }
