@@ -176,10 +176,10 @@ def main(argv=None) -> int:
     step_ms = s0.elapsed_time(s1) / args.steps
 
     # ---- skip statistics (untimed)
-    stats = torch.zeros(2, dtype=torch.int64, device=dev)
+    stats = torch.zeros(3, dtype=torch.int64, device=dev)
     with torch.no_grad():
         ops.forward(q1, k1, q2, k2, v, beta, lam, POWER, True, 2, stats=stats)
-    visited, computed = (int(x) for x in stats.tolist())
+    visited, computed, checked = (int(x) for x in stats.tolist())
 
     fwd_flop = units(SHAPE, FWD_UNITS)
     fb_flop = units(SHAPE, FWDBWD_UNITS)
@@ -205,7 +205,8 @@ def main(argv=None) -> int:
                    "parallelism": "single GPU"},
         "pct_peak": 100.0 * fb_tf / PEAK_BF16_TFLOPS,
         "fwd": {"ms": fwd_ms, "tflops": fwd_tf, "pct_peak": 100.0 * fwd_tf / PEAK_BF16_TFLOPS,
-                "counted_units": FWD_UNITS, "tiles_visited": visited, "tiles_pv_computed": computed,
+                "counted_units": FWD_UNITS, "tiles_visited": visited, "tiles_screen_kept": checked,
+                "tiles_pv_computed": computed,
                 "skipped_tile_fraction": 1.0 - computed / max(visited, 1)},
         "fwd_bwd": {"ms": max(step_ms, wall_ms), "event_ms": step_ms, "wall_ms": wall_ms, "tflops": fb_tf,
                     "pct_peak": 100.0 * fb_tf / PEAK_BF16_TFLOPS, "counted_units": FWDBWD_UNITS},

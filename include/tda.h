@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TDA_ABI_VERSION 2
+#define TDA_ABI_VERSION 3
 
 /* element types of q, k, v, out and gradients */
 #define TDA_DTYPE_F32  0
@@ -99,9 +99,11 @@ typedef struct tda_fwd_args {
                                out [branch][B*H][query tile][ceil(tiles/32)]: bit kt of
                                row (branch, bh, qt) is set when some A_ij of that branch is
                                non-zero in the 32x32 tile (query tile qt, key tile kt) */
-  unsigned long long* stats;/* [0] += (query tile, key tile, branch) triples on or below
-                               the diagonal, [1] += those with a non-zero weight tile
-                               (A.V issued); tiles are 32x32 */
+  unsigned long long* stats;/* 3 counters: [0] += (query tile, key tile, branch) triples
+                               on or below the diagonal, [1] += those with a non-zero
+                               weight tile (A.V issued), [2] += those whose exact weights
+                               were evaluated (bf16: the tiles the screen kept, a superset
+                               of [1]; f32 leaves [2] alone); tiles are 32x32 */
   void*  workspace;         /* device scratch of tda_fwd_workspace_bytes() bytes, 16-byte
                                aligned: holds the tile bitmask when occupancy is NULL */
   size_t workspace_bytes;

@@ -8,17 +8,19 @@
 //
 // Three launches, in stream order:
 //   key_norms   inverse L2 norms rk_j of the key rows, into the norms table (normalize only).
-//   fwd_screen  for every causal (query tile, key tile) pair of a branch, the score tile
-//               S = q k^T on the matrix cores and the tile's largest threshold argument
-//               x_ij = fma(s_ij rk_j, rq_i, -tau_i) (the weight is non-zero iff x_ij > 0).
-//               Tiles with some x_ij > 0 get their bit in the occupancy bitmask.  No V and no
-//               output accumulators: the kernel holds only Q fragments and two score tiles per
-//               wave, so MFMA results stay in ordinary VGPRs and several waves share a SIMD.
+//   fwd_screen  for every causal (query tile, key tile) pair of a branch, a score tile on the
+//               matrix cores and a test that keeps every tile holding a non-zero weight
+//               (x_ij = fma(s_ij rk_j, rq_i, -tau_i) > 0 for some pair).  Without normalisation
+//               the test is exact; with it, the queries enter pre-scaled by their inverse norms
+//               and the test carries a proven margin (kScreenMargin), so it may keep a few
+//               tiles whose weights are all zero.  No V and no output accumulators: the kernel
+//               holds only Q fragments and two score tiles per wave, so MFMA results stay in
+//               ordinary VGPRs and several waves share a SIMD.
 //   fwd_pv      one wave per query tile walks the set bits of both branches: recomputes the
 //               score tile with the same instruction sequence (so the same values), forms the
 //               exact weights ReLU(x)^p with the causal mask, and accumulates out += coef A V.
-//               Tiles whose weights are all zero after the mask lose their bit, so the bitmask
-//               ends exact.
+//               Tiles whose exact weights are all zero lose their bit, so the bitmask ends
+//               exact.
 // The screen tests every key of the tile, including keys after the query on the diagonal tile
 // and padding keys past N: it may keep a tile the mask empties, never drop a non-zero one.
 #include "tda_common.hpp"
@@ -54,6 +56,31 @@ __device__ __forceinline__ float max16(const f32x16& v) {
   const float c = fmaxf(fmaxf(v[8], v[9]), fmaxf(v[10], v[11]));
   const float d = fmaxf(fmaxf(v[12], v[13]), fmaxf(v[14], v[15]));
   return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// Largest of 16 values, NaN if any is NaN (v_maximum3_f32: no NaN canonicalisation of the
+// inputs, which the NaN-ignoring fmaxf needs in IEEE mode).
+__device__ __forceinline__ float maximum16(const f32x16& v) {
+  auto m3 = [](float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+  };
+  const float a = m3(v[0], v[1], v[2]), b = m3(v[3], v[4], v[5]), c = m3(v[6], v[7], v[8]);
+  const float d = m3(v[9], v[10], v[11]), e = m3(v[12], v[13], v[14]);
+  return m3(m3(a, b, c), m3(d, e, v[15]), v[15]);
+}
+
+// Margin of the normalised screen, in cosine units.  The screen's scores sh_ij = qh_i . k_j,
+// qh_i = bf16(q_i rq_i), differ from rq_i s_ij by at most (2^-9 + 2^-22) |k_j|: each element of
+// qh_i carries a relative rounding error of at most 2^-9 (bf16) + 2^-23 (the fp32 product),
+// summed against k_j by Cauchy-Schwarz with rq_i |q_i| <= 1 + 2^-16.  The fp32 accumulations of
+// the screen's and the exact path's MFMAs add at most 2^-17 |q||k| each (128 terms, unit
+// roundoff 2^-24), the fp32 products of the tests a few units of 2^-24.  Times rk_j
+// (rk_j |k_j| <= 1 + 2^-16) the total stays below 2^-9 + 2^-14; the margin doubles the part past
+// 2^-9.  tau_i, evaluated in fp32 with a few ulps of error, is monotone in i up to a relative
+// 2^-20; screen_tlo takes twice that off the smallest end value of the tile.
+constexpr float kScreenMargin = 0x1p-9f + 0x1p-13f;
+__device__ __forceinline__ float screen_tlo(float tmin) {
+  return tmin - fabsf(tmin) * 0x1p-19f - kScreenMargin;
 }
 
 // XCD-aware order of the (stream, block) work items of a grid: consecutive workgroup ids go to
@@ -117,10 +144,16 @@ __global__ void __launch_bounds__(256) key_norms(FwdParams P, int BR) {
 // (8 / QPW waves); grid = branches x heads x ceil(N / 256).  Key tiles stream through LDS in
 // groups of TPB tiles ("super-stages", two of them in a ring): buffer loads into VGPRs one
 // iteration ahead, LDS writes of the next group while the current one is read, one barrier per
-// group.  Score tiles are computed transposed, S^T = K Q^T, so each lane holds one query.
-// Dispatch uses QPW = 2 (three waves per SIMD at 152 VGPRs) and TPB = 1: one query tile per
-// wave (twice the LDS fragment reads per MFMA) and larger groups (fewer waves) both measured
-// slower at the headline shape.
+// group.
+// Without normalisation, score tiles are computed transposed, S^T = K Q^T: each lane holds one
+// query i and 16 of its keys, so "max_j s_ij > tau_i" is the exact test with one compare per
+// lane.  With normalisation the weight test is s_ij rk_j rq_i > tau_i; the queries enter
+// pre-scaled, qh_i = bf16(q_i rq_i), and the tile is computed as S = Qh K^T, so each lane holds
+// one key j (and 16 queries): the per-lane test "max_i sh_ij * rk_j > tlo" needs one multiply
+// per lane instead of one per score, with tlo = the tile's smallest tau minus screen_margin.
+// Dispatch uses QPW = 2 (three waves per SIMD) and TPB = 1: one query tile per wave (twice the
+// LDS fragment reads per MFMA) and larger groups (fewer waves) both measured slower at the
+// headline shape.
 template <int D, bool NORM, int QPW, int TPB>
 __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) {
   constexpr int NT = D / 16;                // MFMA steps over d
@@ -192,7 +225,7 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
   const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
   const float beta = *P.beta;
   bf16x8 Q[QPW][NT];
-  float rq[QPW], tau[QPW];
+  float tau[QPW];  // without normalisation tau_i of the lane's query; with it the tile's tlo
   bool valid[QPW];
 #pragma unroll
   for (int s = 0; s < QPW; ++s) {
@@ -201,19 +234,34 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     const bf16* row = qhead + (int64_t)min(iq, N - 1) * P.s[qslot][2];  // rows >= N: never vote
 #pragma unroll
     for (int t = 0; t < NT; ++t) Q[s][t] = *reinterpret_cast<const bf16x8*>(row + 16 * t + 8 * g);
-    rq[s] = 1.f;
     if constexpr (NORM) {
-      rq[s] = inv_norm(row_sumsq<PolBF16, NT>(Q[s]));
-      if (g == 0 && valid[s]) P.norms[((int64_t)(br ? N_Q2 : N_Q1) * BH + bh) * N + iq] = rq[s];
+      const float rq = inv_norm(row_sumsq<PolBF16, NT>(Q[s]));
+      if (g == 0 && valid[s]) P.norms[((int64_t)(br ? N_Q2 : N_Q1) * BH + bh) * N + iq] = rq;
+      // rows past N score 0; so do non-finite elements (NaN/Inf inputs), whose exact weights
+      // are 0 (x > 0 fails on NaN), so a NaN score can only come from a non-finite key row:
+      // it poisons the maximum of that key's lane alone, whose weights are 0 as well
+      const float sc = valid[s] ? rq : 0.f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float x = (float)Q[s][t][j] * sc;
+          Q[s][t][j] = (bf16)(__builtin_isfinite(x) ? x : 0.f);
+        }
+      // tau is monotone in i: its smallest value over the tile's rows is at one of the ends
+      const int i0 = q0w + 32 * s, i1 = max(i0, min(i0 + 31, N - 1));
+      tau[s] = screen_tlo(fminf(beta * tau_coeff(i0, P.inv_d), beta * tau_coeff(i1, P.inv_d)));
+    } else {
+      tau[s] = beta * tau_coeff(iq, P.inv_d);
     }
-    tau[s] = beta * tau_coeff(iq, P.inv_d);
   }
 
   uint32_t* occ0 = P.occ + ((int64_t)sidx * nqt + qt0) * P.occ_w;  // bitmask row of qt0 (then qt0 + 1)
-  uint32_t word[QPW];
+  // Per lane and query tile: bit kt % 32 set when the lane's test passed for key tile kt.  The
+  // wave ORs them when a 32-tile word is complete (cheaper than a ballot per tile).
+  uint32_t hb[QPW];
 #pragma unroll
-  for (int s = 0; s < QPW; ++s) word[s] = 0u;
-  unsigned visited = 0;
+  for (int s = 0; s < QPW; ++s) hb[s] = 0u;
   const int koff = n32 * KS + 8 * g;
 
   // Threshold test of key tile kt (in stage st) against this wave's query tiles.
@@ -222,51 +270,53 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     const bf16* kp = &kst[st][koff];
     bf16x8 fk[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) fk[t] = *reinterpret_cast<const bf16x8*>(kp + 16 * t);
+    for (int t = 0; t < NT; ++t) {  // in MFMA order: LDS returns in order, the chain waits per step
+      fk[t] = *reinterpret_cast<const bf16x8*>(kp + 16 * t);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    float rk = 1.f;
+    if constexpr (NORM) rk = krk[st][n32];  // the lane's key (0 past N)
     __builtin_amdgcn_sched_barrier(0);  // all fragment reads in flight before the first MFMA
     f32x16 S[QPW];
 #pragma unroll
     for (int s = 0; s < QPW; ++s) S[s] = f32x16{};
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int s = 0; s < QPW; ++s) S[s] = PolBF16::mma(fk[t], Q[s][t], S[s]);
-    // largest s_ij rk_j per lane; x = fma(s rk, rq, -tau) is monotone in s rk (rq > 0), so
-    // "fma(max, rq, -tau) > 0" is exactly "some x_ij > 0" for the lane's keys
-    if constexpr (NORM) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const f32x4 r4 = *reinterpret_cast<const f32x4*>(&krk[st][8 * u + 4 * g]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int s = 0; s < QPW; ++s) S[s][4 * u + e] *= r4[e];
-      }
-    }
+    // One query tile's chain at a time: dependent MFMAs back to back on the same accumulator
+    // take the accumulate fast path; alternating two VGPR accumulators measured ~20 % slower.
 #pragma unroll
     for (int s = 0; s < QPW; ++s) {
-      const float bnd = __builtin_fmaf(max16(S[s]), rq[s], -tau[s]);
-      const bool in = kt <= qt0 + s;  // key tiles after the query tile hold no causal pair
-      const bool any = wave_ballot(in && valid[s] && bnd > 0.f) != 0ull;
-      word[s] |= (uint32_t)any << (kt & 31);
-      visited += (unsigned)(in && live[s]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if constexpr (NORM) S[s] = PolBF16::mma(Q[s][t], fk[t], S[s]);  // S = Qh K^T
+        else S[s] = PolBF16::mma(fk[t], Q[s][t], S[s]);                 // S^T = K Q^T
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the chains apart
+    }
+    const uint32_t bit = 1u << (kt & 31);
+#pragma unroll
+    for (int s = 0; s < QPW; ++s) {
+      if (kt > qt0 + s) continue;  // key tiles after the query tile hold no causal pair
+      bool hit;
+      if constexpr (NORM) hit = maximum16(S[s]) * rk > tau[s];  // largest score of the lane's key
+      else hit = valid[s] && max16(S[s]) > tau[s];          // largest score of the lane's query
+      hb[s] |= hit ? bit : 0u;
     }
   };
   // bitmask words of this wave's rows: word kt/32 is complete after key tile kt
   auto flush = [&](int kt) {
     if (live[0] && ((kt & 31) == 31 || kt == nkt - 1)) {
-      if (l == 0) {
 #pragma unroll
-        for (int s = 0; s < QPW; ++s) {
-          if (!live[s]) continue;
+      for (int s = 0; s < QPW; ++s) {
+        uint32_t w = hb[s];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) w |= (uint32_t)__shfl_xor((int)w, o);
+        hb[s] = 0u;
+        if (l == 0 && live[s]) {
           uint32_t* row = occ0 + s * P.occ_w;
-          row[kt >> 5] = word[s];
+          row[kt >> 5] = w;
           if (kt == nkt - 1)  // words of key tiles this workgroup never reaches
-            for (int w = (kt >> 5) + 1; w < P.occ_w; ++w) row[w] = 0u;
+            for (int x = (kt >> 5) + 1; x < P.occ_w; ++x) row[x] = 0u;
         }
       }
-#pragma unroll
-      for (int s = 0; s < QPW; ++s) word[s] = 0u;
     }
   };
 
@@ -287,7 +337,13 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     if (it + 2 < nit) fetch(it + 2);
     __syncthreads();
   }
-  if (P.stats && l == 0 && visited) atomicAdd(P.stats + 0, (unsigned long long)visited);
+  if (P.stats && l == 0) {
+    // causal (query tile, key tile) pairs of this wave: key tiles 0 .. qt of each live query tile
+    unsigned visited = 0;
+#pragma unroll
+    for (int s = 0; s < QPW; ++s) visited += live[s] ? (unsigned)(qt0 + s + 1) : 0u;
+    if (visited) atomicAdd(P.stats + 0, (unsigned long long)visited);
+  }
 }
 
 // ------------------------------------------------------------------ fwd_pv
@@ -351,7 +407,7 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
   f32x16 O[ND];
 #pragma unroll
   for (int c = 0; c < ND; ++c) O[c] = f32x16{};
-  unsigned computed = 0;
+  unsigned computed = 0, checked = 0;
 
 #pragma unroll
   for (int br = 0; br < BR; ++br) {
@@ -372,6 +428,7 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
       while (bits) {
         const int kt = 32 * w + __builtin_ctz(bits);
         bits &= bits - 1u;
+        ++checked;
         if (!have_q) {
           // query tile rows with whole-row loads, through the (still free) K tile buffer
           const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
@@ -468,7 +525,10 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
             *reinterpret_cast<const u32x4*>(ktl + r * KS + 8 * vch);
     }
   }
-  if (P.stats && l == 0 && computed) atomicAdd(P.stats + 1, (unsigned long long)computed);
+  if (P.stats && l == 0 && checked) {
+    atomicAdd(P.stats + 1, (unsigned long long)computed);
+    atomicAdd(P.stats + 2, (unsigned long long)checked);
+  }
 }
 
 // ------------------------------------------------------------------ dispatch

@@ -99,6 +99,8 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
     a.lambda_param = _ptr(lam) if branches == 2 else None
     if normalize and norms is None:  # scratch: the kernels need the row norms either way
         norms = torch.empty(lib.tda_norms_floats(*q1.shape[:3], branches), dtype=torch.float32, device=q1.device)
+    if stats is not None and (stats.dtype != torch.int64 or stats.numel() < 3 or stats.device != q1.device):
+        raise ValueError("stats must be an int64 tensor of at least 3 elements on the inputs' device")
     a.norms, a.occupancy, a.stats = _ptr(norms), _ptr(occupancy), _ptr(stats)
     ws = torch.empty((lib.tda_fwd_workspace_bytes(*q1.shape[:3], branches) + 3) // 4, dtype=torch.float32,
                      device=q1.device)
