@@ -8,5 +8,7 @@ from .api import (  # noqa: F401
     differential_threshold_rela_triton,
     threshold_rela_triton,
 )
+from .layer import ThresholdDifferentialAttention  # noqa: F401
 
-__all__ = ["threshold_rela_triton", "differential_threshold_rela_triton", "ThresholdRelaFunction"]
+__all__ = ["threshold_rela_triton", "differential_threshold_rela_triton", "ThresholdRelaFunction",
+           "ThresholdDifferentialAttention"]

@@ -46,6 +46,16 @@ def _usable(t: torch.Tensor) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
+def _empty_like_layout(t: torch.Tensor) -> torch.Tensor:
+    """Uninitialised tensor of t's shape and dtype, in (B, N, H, d) memory order when t is a
+    view with heads inner to the sequence (e.g. of a fused projection output), else contiguous
+    (B, H, N, d).  The kernels take either through their strides."""
+    b, h, n, d = t.shape
+    if h > 1 and n > 1 and t.stride(1) < t.stride(2):
+        return torch.empty((b, n, h, d), dtype=t.dtype, device=t.device).transpose(1, 2)
+    return torch.empty(t.shape, dtype=t.dtype, device=t.device)
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -89,7 +99,7 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
     q1, k1, v = _usable(q1), _usable(k1), _usable(v)
     if branches == 2:
         q2, k2 = _usable(q2), _usable(k2)
-    out = torch.empty(q1.shape, dtype=q1.dtype, device=q1.device)
+    out = _empty_like_layout(q1)
     a = _abi.TdaFwdArgs()
     _common(a, q1, branches, normalize, relu_power)
     a.q1, a.k1, a.v, a.out = _tensor(q1), _tensor(k1), _tensor(v), _tensor(out)
@@ -119,10 +129,10 @@ def backward(q1, k1, q2, k2, v, dout, beta, lam, relu_power: float, normalize: b
     if branches == 2:
         q2, k2 = _usable(q2), _usable(k2)
     dev = q1.device
-    dq1, dk1, dv = (torch.empty(q1.shape, dtype=q1.dtype, device=dev) for _ in range(3))
+    dq1, dk1, dv = _empty_like_layout(q1), _empty_like_layout(k1), _empty_like_layout(v)
     dq2 = dk2 = dlam = None
     if branches == 2:
-        dq2, dk2 = (torch.empty(q1.shape, dtype=q1.dtype, device=dev) for _ in range(2))
+        dq2, dk2 = _empty_like_layout(q2), _empty_like_layout(k2)
         dlam = torch.empty((), dtype=torch.float32, device=dev)
     dbeta = torch.empty((), dtype=torch.float32, device=dev)
     b, h, n, d = q1.shape
