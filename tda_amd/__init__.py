@@ -9,6 +9,7 @@ from .api import (  # noqa: F401
     threshold_rela_triton,
 )
 from .layer import ThresholdDifferentialAttention  # noqa: F401
+from .stats import TileStats, tile_sparsity  # noqa: F401
 
 __all__ = ["threshold_rela_triton", "differential_threshold_rela_triton", "ThresholdRelaFunction",
-           "ThresholdDifferentialAttention"]
+           "ThresholdDifferentialAttention", "tile_sparsity", "TileStats"]
