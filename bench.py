@@ -99,12 +99,73 @@ def cpu_baseline(budget_s: float = 12.0):
     }
 
 
+def side_configs(steps: int, warmup: int):
+    """The BASELINE "report" configurations, timed like the headline forward (HIP events on
+    the launch stream around `steps` calls after `warmup`): configs[1] (TRA, bf16,
+    (4,16,2048,64), seed 1, beta 1, p 2, normalize) and configs[4] (TDA, bf16, (1,32,16384,128),
+    seed 4, beta 2, lambda 0.3, normalize) at p = 1 and p = 1.5, with the kernels' tile counters."""
+    import torch
+
+    from tda_amd import ops
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+
+    def timed(fn):
+        with torch.no_grad():
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(steps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    def tiles(call):
+        st = torch.zeros(3, dtype=torch.int64, device=dev)
+        with torch.no_grad():
+            call(st)
+        visited, nonzero, kept = (int(x) for x in st.tolist())
+        return {"tiles_visited": visited, "tiles_screen_kept": kept, "tiles_nonzero": nonzero,
+                "skipped_tile_fraction": 1.0 - nonzero / max(visited, 1)}
+
+    shape1 = (4, 16, 2048, 64)
+    g = torch.Generator("cpu").manual_seed(1)
+    q, k, v = (torch.randn(shape1, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+    beta = torch.tensor(1.0, device=dev)
+    ms = timed(lambda: ops.forward(q, k, None, None, v, beta, None, 2.0, True, 1))
+    res["configs[1]"] = {"workload": "TRA fwd bf16 (4,16,2048,64) seed 1, beta=1, p=2, normalize, causal",
+                         "ms": ms, "tflops": units(shape1, 2.0) / (ms * 1e-3) / 1e12,
+                         "pct_peak": 100.0 * units(shape1, 2.0) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                         "counted_units": 2.0,
+                         **tiles(lambda st: ops.forward(q, k, None, None, v, beta, None, 2.0, True, 1, stats=st))}
+    del q, k, v
+    shape4 = (1, 32, 16384, 128)
+    g = torch.Generator("cpu").manual_seed(4)
+    xs = [torch.randn(shape4, generator=g).to(torch.bfloat16).to(dev) for _ in range(5)]
+    q1, q2, k1, k2, v = xs
+    beta, lam = torch.tensor(2.0, device=dev), torch.tensor(0.3, device=dev)
+    for p in (1.0, 1.5):
+        ms = timed(lambda: ops.forward(q1, k1, q2, k2, v, beta, lam, p, True, 2))
+        res[f"configs[4] p={p}"] = {
+            "workload": f"TDA fwd bf16 (1,32,16384,128) seed 4, beta=2, lambda=0.3, p={p}, normalize, causal",
+            "ms": ms, "tflops": units(shape4, 3.0) / (ms * 1e-3) / 1e12,
+            "pct_peak": 100.0 * units(shape4, 3.0) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "counted_units": 3.0,
+            **tiles(lambda st: ops.forward(q1, k1, q2, k2, v, beta, lam, p, True, 2, stats=st))}
+    return res
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-side", action="store_true", help="skip the configs[1] / configs[4] report figures")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy 3 times (calibrates HBM byte counters)")
@@ -222,6 +283,8 @@ def main(argv=None) -> int:
                                      "compulsory 4.027e8",
                      "hbm_gbs_at_traffic": FWD_HBM_BYTES / (fwd_ms * 1e-3) / 1e9},
     }
+    if not args.no_side:
+        res["side_configs"] = side_configs(max(3, args.steps // 4), 2)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     print(json.dumps(res), flush=True)
