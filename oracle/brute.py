@@ -24,17 +24,19 @@ def _norm(row):
     return [x / n for x in row]
 
 
-def tra_rows(q, k, v, beta, p, normalize=False):
-    """q, k, v: lists of N rows (lists of d floats). Returns N rows."""
+def tra_rows(q, k, v, beta, p, normalize=False, q_offset=0):
+    """q: list of Nq rows, k, v: lists of Nk rows (lists of d floats); query row i sits at
+    position q_offset + i (0 and Nq = Nk in the reference).  Returns Nq rows."""
     n, d = len(q), len(q[0])
     if normalize:
         q = [_norm(r) for r in q]
         k = [_norm(r) for r in k]
     out = []
     for i in range(n):
-        t = beta * math.sqrt(2.0 * math.log(i + 1.0) / d)
+        pos = q_offset + i
+        t = beta * math.sqrt(2.0 * math.log(pos + 1.0) / d)
         acc = [0.0] * d
-        for j in range(i + 1):
+        for j in range(min(len(k), pos + 1)):
             s = 0.0
             for c in range(d):
                 s += q[i][c] * k[j][c]
@@ -47,8 +49,8 @@ def tra_rows(q, k, v, beta, p, normalize=False):
     return out
 
 
-def tda_rows(q1, q2, k1, k2, v, beta, lam, p, normalize=True):
-    o1 = tra_rows(q1, k1, v, beta, p, normalize)
-    o2 = tra_rows(q2, k2, v, beta, p, normalize)
+def tda_rows(q1, q2, k1, k2, v, beta, lam, p, normalize=True, q_offset=0):
+    o1 = tra_rows(q1, k1, v, beta, p, normalize, q_offset)
+    o2 = tra_rows(q2, k2, v, beta, p, normalize, q_offset)
     lc = min(max(lam, 0.0), 1.0)
     return [[a - lc * b for a, b in zip(r1, r2)] for r1, r2 in zip(o1, o2)]

@@ -23,6 +23,12 @@ cited as TTA:<line>):
   q2, k2 (TTA:505-509), two branches sharing v (TTA:512-513), then
   out1 - clamp(lambda, 0, 1) * out2 (TTA:516-517).
 
+Position offset (a superset of the reference, whose query index is always the
+absolute position, TTA:62): queries may be a block of q_offset.. q_offset+Nq-1
+against Nk keys (KV-cache decode, chunked prefill); query row i then uses
+tau(q_offset + i) and sees keys j <= q_offset + i.  q_offset = 0 with Nq = Nk
+is the reference's case.
+
 Gradients for q, k, v, beta and lambda come from torch autograd of these
 expressions (the reference returns None for beta, TTA:469; the build adds it).
 
@@ -41,11 +47,12 @@ import torch.nn.functional as F
 NORM_EPS = 1e-12  # torch.nn.functional.normalize default eps (TTA:506-509)
 
 
-def tau(n: int, d: int, beta, dtype=torch.float64, device="cpu") -> torch.Tensor:
-    """Per-row threshold tau_i = beta * sqrt(2 ln(i+1) / d), i = 0..n-1 (TTA:59-63).
+def tau(n: int, d: int, beta, dtype=torch.float64, device="cpu", offset: int = 0) -> torch.Tensor:
+    """Per-row threshold tau_i = beta * sqrt(2 ln(i+1) / d) for the absolute positions
+    i = offset .. offset+n-1 (TTA:59-63).
 
     ``beta`` may be a float or a 0-dim tensor (kept differentiable)."""
-    i = torch.arange(n, dtype=dtype, device=device)
+    i = torch.arange(offset, offset + n, dtype=dtype, device=device)
     c = torch.sqrt(2.0 * torch.log(i + 1.0) / d)
     return beta * c
 
@@ -74,22 +81,29 @@ def _normalize(x: torch.Tensor) -> torch.Tensor:
     return F.normalize(x, p=2.0, dim=-1, eps=NORM_EPS)
 
 
+def causal_mask(nq: int, nk: int, q_offset: int = 0, device="cpu") -> torch.Tensor:
+    """(nq, nk) bool: key j is visible to query row i when j <= q_offset + i (TTA:77-80)."""
+    i = torch.arange(nq, device=device).unsqueeze(1) + q_offset
+    return torch.arange(nk, device=device).unsqueeze(0) <= i
+
+
 def tra(q, k, v, beta, relu_power: float = 2.0, normalize: bool = False,
-        mask: str = "exclude") -> torch.Tensor:
+        mask: str = "exclude", q_offset: int = 0) -> torch.Tensor:
     """Threshold rectified attention, out = ReLU(mask(Q K^T) - tau)^p V.
 
     Follows TTA:19-115 (forward kernel) and TTA:472-486 (public wrapper); the
     ``normalize`` flag applies TTA:505-509 to q and k.  Computes in the dtype
     of the inputs (callers upcast bf16 inputs to float32/float64 first).
-    Shapes (B, H, N, d).  ``mask`` is "exclude" (j > i contributes nothing) or
-    "zero" (the reference's literal rule: S_ij := 0 for j > i, TTA:80)."""
+    Shapes q (B, H, Nq, d), k and v (B, H, Nk, d) (Nq = Nk and q_offset = 0 in the
+    reference).  ``mask`` is "exclude" (j > i contributes nothing) or "zero" (the
+    reference's literal rule: S_ij := 0 for j > i, TTA:80)."""
     if normalize:
         q = _normalize(q)
         k = _normalize(k)
     n, d = q.shape[-2], q.shape[-1]
     s = torch.matmul(q, k.transpose(-1, -2))
-    causal = torch.ones(n, n, dtype=torch.bool, device=q.device).tril()
-    t = tau(n, d, beta, dtype=q.dtype, device=q.device).unsqueeze(-1)
+    causal = causal_mask(n, k.shape[-2], q_offset, device=q.device)
+    t = tau(n, d, beta, dtype=q.dtype, device=q.device, offset=q_offset).unsqueeze(-1)
     if mask == "zero":
         s = torch.where(causal, s, torch.zeros_like(s))
         p = relu_pow(s - t, relu_power)
@@ -102,11 +116,11 @@ def tra(q, k, v, beta, relu_power: float = 2.0, normalize: bool = False,
 
 
 def tda(q1, q2, k1, k2, v, beta, lambda_param, relu_power: float = 2.0,
-        normalize: bool = True, mask: str = "exclude") -> torch.Tensor:
+        normalize: bool = True, mask: str = "exclude", q_offset: int = 0) -> torch.Tensor:
     """Threshold differential attention (TTA:489-519):
     TRA(n(q1), n(k1), v) - clamp(lambda, 0, 1) * TRA(n(q2), n(k2), v)."""
-    out1 = tra(q1, k1, v, beta, relu_power, normalize, mask)
-    out2 = tra(q2, k2, v, beta, relu_power, normalize, mask)
+    out1 = tra(q1, k1, v, beta, relu_power, normalize, mask, q_offset)
+    out2 = tra(q2, k2, v, beta, relu_power, normalize, mask, q_offset)
     if not isinstance(lambda_param, torch.Tensor):
         lambda_param = torch.tensor(float(lambda_param), dtype=out1.dtype)
     lam = torch.clamp(lambda_param, min=0.0, max=1.0)
@@ -121,26 +135,28 @@ def tda(q1, q2, k1, k2, v, beta, lambda_param, relu_power: float = 2.0,
 # ----------------------------------------------------------------------------
 
 @torch.no_grad()
-def tra_head_rows(q, k, v, beta: float, relu_power: float, r0: int, r1: int) -> torch.Tensor:
-    """Rows r0..r1-1 of TRA for one head; q, k, v are (N, d), already
-    normalised if required.  Keys beyond r1-1 are causally excluded."""
+def tra_head_rows(q, k, v, beta: float, relu_power: float, r0: int, r1: int,
+                  q_offset: int = 0) -> torch.Tensor:
+    """Query rows r0..r1-1 of TRA for one head; q is (Nq, d), k and v (Nk, d), already
+    normalised if required.  Keys after position q_offset + r1 - 1 are causally excluded."""
     d = q.shape[-1]
-    kk = k[:r1]
-    s = q[r0:r1] @ kk.T                                     # (r1-r0, r1)
-    i = torch.arange(r0, r1, dtype=q.dtype)
+    kn = min(k.shape[0], q_offset + r1)
+    kk = k[:kn]
+    s = q[r0:r1] @ kk.T                                     # (r1-r0, kn)
+    i = torch.arange(q_offset + r0, q_offset + r1, dtype=q.dtype)
     t = (beta * torch.sqrt(2.0 * torch.log(i + 1.0) / d)).unsqueeze(-1)
     x = s - t
-    j = torch.arange(r1)
-    causal = j.unsqueeze(0) <= torch.arange(r0, r1).unsqueeze(1)
+    j = torch.arange(kn)
+    causal = j.unsqueeze(0) <= torch.arange(q_offset + r0, q_offset + r1).unsqueeze(1)
     x = torch.where(causal, x, torch.full_like(x, -1.0))
     p = relu_pow(x, relu_power)
-    return p @ v[:r1]
+    return p @ v[:kn]
 
 
 @torch.no_grad()
 def tda_chunked(q1, q2, k1, k2, v, beta: float, lambda_param: float, relu_power: float,
                 normalize: bool, branches: int = 2, block: int = 1024,
-                heads=None, dtype=torch.float32) -> torch.Tensor:
+                heads=None, dtype=torch.float32, q_offset: int = 0) -> torch.Tensor:
     """No-grad evaluation of TRA (branches=1: q1, k1, v) or TDA (branches=2) on
     CPU, head by head and ``block`` query rows at a time.  Returns (B, H, N, d)
     in ``dtype`` (only the selected ``heads`` [(b, h), ...] are filled when
@@ -159,16 +175,16 @@ def tda_chunked(q1, q2, k1, k2, v, beta: float, lambda_param: float, relu_power:
             qb, kb = prep(q2), prep(k2)
         for r0 in range(0, n, block):
             r1 = min(n, r0 + block)
-            o = tra_head_rows(qa, ka, vv, beta, relu_power, r0, r1)
+            o = tra_head_rows(qa, ka, vv, beta, relu_power, r0, r1, q_offset)
             if branches == 2:
-                o = o - lam * tra_head_rows(qb, kb, vv, beta, relu_power, r0, r1)
+                o = o - lam * tra_head_rows(qb, kb, vv, beta, relu_power, r0, r1, q_offset)
             out[b, h, r0:r1] = o
     return out
 
 
 def tda_grads(q1, q2, k1, k2, v, dout, beta: float, lambda_param: float,
               relu_power: float, normalize: bool, branches: int = 2,
-              dtype=torch.float64):
+              dtype=torch.float64, q_offset: int = 0):
     """Autograd gradients of sum(out * dout) for TRA (branches=1) or TDA.
 
     Returns a dict with out, dq1, dk1, dv, dbeta and (branches=2) dq2, dk2,
@@ -182,11 +198,11 @@ def tda_grads(q1, q2, k1, k2, v, dout, beta: float, lambda_param: float,
     if branches == 2:
         tq2, tk2 = leaf(q2), leaf(k2)
         tl = torch.tensor(float(lambda_param), dtype=dtype, requires_grad=True)
-        out = tda(tq1, tq2, tk1, tk2, tv, tb, tl, relu_power, normalize)
+        out = tda(tq1, tq2, tk1, tk2, tv, tb, tl, relu_power, normalize, q_offset=q_offset)
         out.backward(go)
         res.update(dq2=tq2.grad, dk2=tk2.grad, dlambda=tl.grad)
     else:
-        out = tra(tq1, tk1, tv, tb, relu_power, normalize)
+        out = tra(tq1, tk1, tv, tb, relu_power, normalize, q_offset=q_offset)
         out.backward(go)
     res.update(out=out.detach(), dq1=tq1.grad, dk1=tk1.grad, dv=tv.grad, dbeta=tb.grad)
     return res

@@ -201,3 +201,48 @@ def test_rel_err_metric():
     assert rel_err(a, a) == 0.0
     assert rel_err(a + torch.tensor([0.0, 0.4, 0.0]), a) == pytest.approx(0.1)
     assert rel_err(torch.zeros(3), torch.zeros(3)) == 0.0
+
+
+# ---------------------------------------------------------------- position offset
+@pytest.mark.parametrize("nq,nk,off,normalize", [
+    (1, 9, 8, True),    # decode: the last position against the whole cache
+    (3, 9, 6, False),   # the last three positions
+    (4, 10, 2, True),   # a block in the middle: keys past position 5 are never visible
+    (6, 4, 1, True),    # queries past the key range see every key
+    (5, 5, 0, False),   # the reference's square case
+])
+def test_offset_matches_brute_force(nq, nk, off, normalize):
+    d = 4
+    q, k, v = _rand((nq, d), 90), _rand((nk, d), 91), _rand((nk, d), 92)
+    ref = torch.tensor(brute.tra_rows(_rows(q), _rows(k), _rows(v), 0.2, 2.0, normalize, off),
+                       dtype=torch.float64)
+    got = tra(q[None, None], k[None, None], v[None, None], 0.2, 2.0, normalize, q_offset=off)[0, 0]
+    torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
+    ch = tda_chunked(q[None, None], None, k[None, None], None, v[None, None], 0.2, 0.0, 2.0, normalize,
+                     branches=1, block=2, dtype=torch.float64, q_offset=off)[0, 0]
+    torch.testing.assert_close(ch, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_offset_block_equals_rows_of_full_sequence():
+    """Rows o..o+m-1 of a full causal pass equal the same query rows computed alone at
+    q_offset = o against all keys (the KV-cache identity); a wrong tau position or a mask
+    relative to the block instead of absolute fails it."""
+    n, d, o, m = 40, 8, 23, 9
+    q1, q2, k1, k2, v = (_rand((2, 3, n, d), s) for s in range(93, 98))
+    full = tda(q1, q2, k1, k2, v, 0.4, 0.6, 2.0, True)
+    blk = tda(q1[..., o:o + m, :], q2[..., o:o + m, :], k1, k2, v, 0.4, 0.6, 2.0, True, q_offset=o)
+    torch.testing.assert_close(blk, full[..., o:o + m, :], rtol=1e-12, atol=1e-12)
+    assert full[..., o:o + m, :].abs().max() > 0
+    # the keys after the block's last position never matter
+    blk2 = tda(q1[..., o:o + m, :], q2[..., o:o + m, :], k1[..., :o + m, :], k2[..., :o + m, :],
+               v[..., :o + m, :], 0.4, 0.6, 2.0, True, q_offset=o)
+    torch.testing.assert_close(blk2, blk, rtol=1e-12, atol=1e-12)
+
+
+def test_gradcheck_offset():
+    q = [_rand((1, 2, 3, 4), s).requires_grad_(True) for s in (100, 101)]
+    kv = [_rand((1, 2, 7, 4), s).requires_grad_(True) for s in (102, 103, 104)]
+    beta = torch.tensor(0.05, dtype=torch.float64, requires_grad=True)
+    lam = torch.tensor(0.4, dtype=torch.float64, requires_grad=True)
+    f = lambda q1, q2, k1, k2, v, b, l: tda(q1, q2, k1, k2, v, b, l, 2.0, True, q_offset=4)  # noqa: E731
+    assert torch.autograd.gradcheck(f, (*q, *kv, beta, lam), eps=1e-6, atol=1e-5)
