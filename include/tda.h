@@ -2,11 +2,12 @@
  * tda.h -- C ABI of the MI355X (gfx950) threshold-attention library libtda_hip.so.
  *
  * The library computes Threshold Rectified Attention (TRA, one branch) and
- * Threshold Differential Attention (TDA, two branches), causal, on tensors of
- * shape (B, H, N, d):
+ * Threshold Differential Attention (TDA, two branches), causal, on queries of
+ * shape (B, H, Nq, d) and keys/values of shape (B, H, Nk, d):
  *
- *   tau_i  = beta * sqrt(2 ln(i+1) / d)                 i = 0-based query index
- *   A_ij   = ReLU(s(q_i, k_j) - tau_i)^p  for j <= i    s = dot, or cosine when normalize
+ *   P_i    = q_offset + i                               absolute position of query row i
+ *   tau_i  = beta * sqrt(2 ln(P_i+1) / d)
+ *   A_ij   = ReLU(s(q_i, k_j) - tau_i)^p  for j <= P_i  s = dot, or cosine when normalize
  *   out    = A(q1,k1) V                                 branches == 1
  *   out    = (A(q1,k1) - clamp(lambda,0,1) A(q2,k2)) V  branches == 2
  *
@@ -24,6 +25,9 @@
  *               reference does not compute (it returns None, TTA:469).
  *   tda_validate_fwd / tda_validate_bwd <- the shape assert (TTA:348), extended
  *               to every argument; host-only, never touches a GPU.
+ *   seq_len_kv / q_offset: no counterpart (the reference's query index is always the
+ *               absolute position, TTA:62, with Nq = Nk); they serve KV-cache decode and
+ *               chunked prefill.  Zero for both is the reference's case.
  *
  * Conventions
  *   - Every pointer in the argument structs is a device pointer, except the
@@ -51,7 +55,7 @@
 extern "C" {
 #endif
 
-#define TDA_ABI_VERSION 3
+#define TDA_ABI_VERSION 4
 
 /* element types of q, k, v, out and gradients */
 #define TDA_DTYPE_F32  0
@@ -71,6 +75,8 @@ extern "C" {
 #define TDA_ERR_ABI           -9   /* abi_version != TDA_ABI_VERSION */
 #define TDA_ERR_CAUSAL       -10   /* causal != 1 (only the causal form exists) */
 #define TDA_ERR_NORMS        -11   /* normalize set but the norms buffer is missing */
+#define TDA_ERR_OFFSET       -12   /* q_offset negative, or seq_len_kv / q_offset + seq_len
+                                      beyond 2^30 - 64 */
 #define TDA_ERR_HIP         -100   /* a HIP launch failed; see tda_last_hip_error() */
 
 /* One (B, H, N, d) tensor: data pointer plus strides in elements. */
@@ -86,17 +92,19 @@ typedef struct tda_fwd_args {
   int32_t normalize;        /* 1 = cosine scores (F.normalize of q and k rows) */
   int32_t causal;           /* must be 1 */
   float   relu_power;       /* p >= 0; p == 1 and p == 2 take integer fast paths */
-  int64_t batch, heads, seq_len, head_dim;
-  tda_tensor q1, k1, q2, k2, v;   /* inputs (q2, k2 ignored when branches == 1) */
-  tda_tensor out;                 /* output, same dtype as the inputs */
+  int64_t batch, heads, seq_len, head_dim;  /* seq_len = Nq, the query rows */
+  tda_tensor q1, k1, q2, k2, v;   /* inputs (q2, k2 ignored when branches == 1): q rows Nq,
+                                     k and v rows Nk */
+  tda_tensor out;                 /* output (Nq rows), same dtype as the inputs */
   const float* beta;        /* device scalar */
   const float* lambda_param;/* device scalar, raw (clamped on device); branches == 2 */
-  float*    norms;          /* [2*branches][B*H][N] inverse row norms 1/max(|x|,1e-12)
-                               of q1, k1 (, q2, k2); required and written when
-                               normalize == 1 (the backward pass reads them), else unused */
+  float*    norms;          /* tda_norms_floats_kv() floats: inverse row norms
+                               1/max(|x|,1e-12) of q1 [B*H][Nq], k1 [B*H][Nk] (, q2
+                               [B*H][Nq], k2 [B*H][Nk]), back to back; required and written
+                               when normalize == 1 (the backward reads them), else unused */
   /* optional outputs (may be NULL): */
-  uint32_t* occupancy;      /* tile-occupancy bitmask, tda_occupancy_words() words laid
-                               out [branch][B*H][query tile][ceil(tiles/32)]: bit kt of
+  uint32_t* occupancy;      /* tile-occupancy bitmask, tda_occupancy_words_kv() words laid
+                               out [branch][B*H][query tile][ceil(key tiles/32)]: bit kt of
                                row (branch, bh, qt) is set when some A_ij of that branch is
                                non-zero in the 32x32 tile (query tile qt, key tile kt) */
   unsigned long long* stats;/* 3 counters: [0] += (query tile, key tile, branch) triples
@@ -104,9 +112,12 @@ typedef struct tda_fwd_args {
                                weight tile (A.V issued), [2] += those whose exact weights
                                were evaluated (bf16: the tiles the screen kept, a superset
                                of [1]; f32 leaves [2] alone); tiles are 32x32 */
-  void*  workspace;         /* device scratch of tda_fwd_workspace_bytes() bytes, 16-byte
-                               aligned: holds the tile bitmask when occupancy is NULL */
+  void*  workspace;         /* device scratch of tda_fwd_workspace_bytes_kv() bytes,
+                               16-byte aligned: holds the tile bitmask when occupancy is NULL */
   size_t workspace_bytes;
+  int64_t seq_len_kv;       /* Nk, the key/value rows; 0 means Nk = seq_len */
+  int64_t q_offset;         /* position of query row 0 (>= 0); 0 with Nk = Nq is the
+                               reference's causal case, Nk - Nq the KV-cache alignment */
 } tda_fwd_args;
 
 typedef struct tda_bwd_args {
@@ -129,6 +140,8 @@ typedef struct tda_bwd_args {
   void*  workspace;         /* device scratch of tda_bwd_workspace_bytes() bytes */
   size_t workspace_bytes;
   unsigned long long* stats;/* optional: [0] += tiles visited, [1] += tiles computed */
+  int64_t seq_len_kv;       /* as in tda_fwd_args (dq, dout: Nq rows; dk, dv: Nk rows) */
+  int64_t q_offset;
 } tda_bwd_args;
 
 int32_t     tda_abi_version(void);
@@ -140,10 +153,17 @@ int32_t     tda_last_hip_error(void);
 int32_t tda_validate_fwd(const tda_fwd_args* args);
 int32_t tda_validate_bwd(const tda_bwd_args* args);
 
-/* Buffer sizes for the optional forward outputs and the backward workspace. */
+/* Buffer sizes for the optional forward outputs and the backward workspace (0 for invalid
+   arguments).  The _kv forms take the key rows Nk; the others are the Nk = Nq case. */
 size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 size_t tda_norms_floats(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 size_t tda_fwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
+size_t tda_occupancy_words_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv,
+                              int32_t branches);
+size_t tda_norms_floats_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv,
+                           int32_t branches);
+size_t tda_fwd_workspace_bytes_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv,
+                                  int32_t branches);
 size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim);
 
 /* Enqueue the forward / backward pass on `stream` (a hipStream_t). */

@@ -13,7 +13,7 @@ import threading
 HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(HERE, "libtda_hip.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
@@ -29,6 +29,7 @@ ERR_WORKSPACE = -8
 ERR_ABI = -9
 ERR_CAUSAL = -10
 ERR_NORMS = -11
+ERR_OFFSET = -12
 ERR_HIP = -100
 
 
@@ -57,6 +58,7 @@ class TdaFwdArgs(ctypes.Structure):
         ("beta", ctypes.c_void_p), ("lambda_param", ctypes.c_void_p),
         ("norms", ctypes.c_void_p), ("occupancy", ctypes.c_void_p), ("stats", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("seq_len_kv", ctypes.c_int64), ("q_offset", ctypes.c_int64),
     ]
 
 
@@ -71,6 +73,7 @@ class TdaBwdArgs(ctypes.Structure):
         ("norms", ctypes.c_void_p), ("occupancy", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("stats", ctypes.c_void_p),
+        ("seq_len_kv", ctypes.c_int64), ("q_offset", ctypes.c_int64),
     ]
 
 
@@ -84,6 +87,9 @@ SIGNATURES = {
     "tda_occupancy_words": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
     "tda_norms_floats": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
     "tda_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
+    "tda_occupancy_words_kv": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int32]),
+    "tda_norms_floats_kv": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int32]),
+    "tda_fwd_workspace_bytes_kv": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int32]),
     "tda_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4),
     "tda_fwd": (ctypes.c_int32, [ctypes.POINTER(TdaFwdArgs), ctypes.c_void_p]),
     "tda_bwd": (ctypes.c_int32, [ctypes.POINTER(TdaBwdArgs), ctypes.c_void_p]),

@@ -14,7 +14,12 @@ Superset behaviour (all results identical where the reference is defined):
     receive a gradient (the reference returns None for beta, TTA:469);
   * all four (B, H, N, d) strides are honoured (the reference ignores the batch stride,
     TTA:49);
-  * errors raise ValueError with a message instead of an assert (TTA:348).
+  * errors raise ValueError with a message instead of an assert (TTA:348);
+  * keys and values may be longer or shorter than the queries (Nk != Nq), and the keyword
+    q_offset places query row i at absolute position q_offset + i: tau uses that position
+    and the row sees keys j <= q_offset + i (KV-cache decode, chunked prefill).  The default
+    q_offset is max(Nk - Nq, 0): the queries are the last Nq positions of the keys, and 0
+    when Nq = Nk, which is the reference's case.
 Only the causal form exists, as in the reference.  Supported head_dim: 64, 128.
 """
 from __future__ import annotations
@@ -43,9 +48,20 @@ def _power(relu_power) -> float:
     return p
 
 
-def _run(tensors, names, beta, lam, relu_power, normalize, branches):
-    ops._check_inputs(tensors, names)
+def _offset(q_offset, nq: int, nk: int) -> int:
+    if q_offset is None:
+        return max(nk - nq, 0)
+    off = int(q_offset)
+    if off < 0:
+        raise ValueError(f"q_offset must be >= 0, got {off}")
+    return off
+
+
+def _run(tensors, names, beta, lam, relu_power, normalize, branches, q_offset=None):
+    kv_from = 1 if branches == 1 else 2
+    ops._check_inputs(tensors, names, kv_from=kv_from)
     ref = tensors[0]
+    off = _offset(q_offset, ref.shape[2], tensors[kv_from].shape[2])
     if ref.shape[-1] not in (64, 128):
         raise ValueError(f"head_dim must be 64 or 128, got {ref.shape[-1]}")
     p = _power(relu_power)
@@ -55,7 +71,7 @@ def _run(tensors, names, beta, lam, relu_power, normalize, branches):
         raise ValueError(f"unsupported dtype {ref.dtype}")
     beta_t = _scalar(beta, dev, "beta")
     lam_t = _scalar(lam, dev, "lambda_param") if branches == 2 else None
-    if ref.shape[2] == 0 or ref.numel() == 0:
+    if any(t.numel() == 0 for t in tensors):  # no query rows, or no keys: the output is 0
         zero = sum(t.sum() for t in tensors) * 0.0 + beta_t * 0.0
         if lam_t is not None:
             zero = zero + lam_t * 0.0
@@ -65,27 +81,31 @@ def _run(tensors, names, beta, lam, relu_power, normalize, branches):
         q1, q2, k1, k2, v = xs
     else:
         (q1, k1, v), q2, k2 = xs, None, None
-    out = ops.TDAFunction.apply(q1, k1, q2, k2, v, beta_t, lam_t, p, bool(normalize), branches)
+    out = ops.TDAFunction.apply(q1, k1, q2, k2, v, beta_t, lam_t, p, bool(normalize), branches, off)
     return out if out.dtype == ref.dtype else out.to(ref.dtype)
 
 
-def threshold_rela_triton(q, k, v, beta, relu_power=2.0, normalize=False):
+def threshold_rela_triton(q, k, v, beta, relu_power=2.0, normalize=False, *, q_offset=None):
     """Threshold Rectified Attention: out = ReLU(Q K^T - tau)^p V, causal,
     tau_i = beta * sqrt(2 ln(i+1) / d)  (TTA:472-486).
 
-    q, k, v: (batch, heads, seq_len, head_dim) on the GPU, float32 or bfloat16 (float16 and
-    float64 are computed in float32).  beta: float or scalar tensor.  relu_power: float
-    (p == 1 and p == 2 take integer fast paths).  normalize: cosine scores."""
-    return _run((q, k, v), ("q", "k", "v"), beta, None, relu_power, normalize, 1)
+    q: (batch, heads, seq_len, head_dim), k, v: (batch, heads, seq_len_kv, head_dim) on the
+    GPU, float32 or bfloat16 (float16 and float64 are computed in float32).  beta: float or
+    scalar tensor.  relu_power: float (p == 1 and p == 2 take integer fast paths).
+    normalize: cosine scores.  q_offset: position of query row 0 (default
+    max(seq_len_kv - seq_len, 0))."""
+    return _run((q, k, v), ("q", "k", "v"), beta, None, relu_power, normalize, 1, q_offset)
 
 
 def differential_threshold_rela_triton(q1, q2, k1, k2, v, beta, lambda_param, relu_power=2.0,
-                                       normalize=True):
+                                       normalize=True, *, q_offset=None):
     """Threshold Differential Attention (TTA:489-519):
     TRA(n(q1), n(k1), v) - clamp(lambda_param, 0, 1) * TRA(n(q2), n(k2), v),
-    computed by one fused kernel; n() is the L2 row normalisation when normalize=True."""
+    computed by one fused kernel; n() is the L2 row normalisation when normalize=True.
+    q1, q2: (batch, heads, seq_len, head_dim); k1, k2, v: (..., seq_len_kv, head_dim);
+    q_offset as for threshold_rela_triton."""
     return _run((q1, q2, k1, k2, v), ("q1", "q2", "k1", "k2", "v"), beta, lambda_param,
-                relu_power, normalize, 2)
+                relu_power, normalize, 2, q_offset)
 
 
 class ThresholdRelaFunction:

@@ -19,6 +19,7 @@
 // score: A = 0 on a tile implies G = 0 there, so nothing else contributes.
 #include "tda_common.hpp"
 #include "tda_params.hpp"
+#include "tda_pos.hpp"
 
 namespace tda {
 
@@ -107,11 +108,13 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
   const int64_t item = (int64_t)blockIdx.x * 4 + wv;
   if (item >= (int64_t)BH * P.nqt) return;
   const int qt = P.nqt - 1 - (int)(item / BH);
+  const int ktl = kt_last(qt, P.qoff, P.nkt);  // last key tile the query tile sees
   const int bh = (int)(item % BH);
   const int b = bh / P.H, h = bh % P.H;
-  const int N = P.N;
+  const int Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
   const int i = qt * 32 + n32;
-  const bool qvalid = i < N;
+  const bool qvalid = i < Nq;
+  const int pq = qoff + i;  // the lane's query position
 
   const TRef<const T> q1{(const T*)P.in[0], P.s[B_Q1][0], P.s[B_Q1][1], P.s[B_Q1][2]};
   const TRef<const T> k1{(const T*)P.in[1], P.s[B_K1][0], P.s[B_K1][1], P.s[B_K1][2]};
@@ -137,12 +140,12 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
   float rq1 = 1.f, rq2 = 1.f;
   if constexpr (NORM) {
     if (qvalid) {
-      rq1 = P.norms[((int64_t)N_Q1 * BH + bh) * N + i];
-      if constexpr (BR == 2) rq2 = P.norms[((int64_t)N_Q2 * BH + bh) * N + i];
+      rq1 = P.norms[norm_base(P, N_Q1, bh) + i];
+      if constexpr (BR == 2) rq2 = P.norms[norm_base(P, N_Q2, bh) + i];
     }
   }
   const float pw = P.p;
-  const float ci = tau_coeff(i, P.inv_d);
+  const float ci = tau_coeff(pq, P.inv_d);
   const float tau = (*P.beta) * ci;
   float lam = 0.f;
   if constexpr (BR == 2) lam = clamp01(*P.lam);
@@ -158,10 +161,10 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
   unsigned visited = 0, computed = 0;
   const uint32_t* occrow = P.occ ? P.occ + ((int64_t)bh * P.nqt + qt) * P.occ_w : nullptr;
   const int64_t occ_br = (int64_t)BH * P.nqt * P.occ_w;  // branch-plane distance of the bitmask
-  const float* nk1 = NORM ? P.norms + ((int64_t)N_K1 * BH + bh) * N : nullptr;
-  const float* nk2 = NORM ? P.norms + ((int64_t)N_K2 * BH + bh) * N : nullptr;
+  const float* nk1 = NORM ? P.norms + norm_base(P, N_K1, bh) : nullptr;
+  const float* nk2 = NORM ? P.norms + norm_base(P, N_K2, bh) : nullptr;
 
-  for (int kt = 0; kt <= qt; ++kt) {
+  for (int kt = 0; kt <= ktl; ++kt) {
     if (occrow) {  // tile holds a non-zero score of either branch?
       uint32_t w = occrow[kt >> 5];
       if constexpr (BR == 2) w |= occrow[occ_br + (kt >> 5)];
@@ -172,17 +175,17 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
     const int j = k0 + n32;
     f32x16 S1 = f32x16{}, S2 = f32x16{}, Dp = f32x16{};
     {
-      const T* r = (j < N) ? k1.row(b, h, j) : nullptr;
+      const T* r = (j < Nk) ? k1.row(b, h, j) : nullptr;
 #pragma unroll
       for (int t = 0; t < NT; ++t) S1 = Pol::mma(Pol::load_row(r, t, g), Q1[t], S1);
     }
     if constexpr (BR == 2) {
-      const T* r = (j < N) ? k2.row(b, h, j) : nullptr;
+      const T* r = (j < Nk) ? k2.row(b, h, j) : nullptr;
 #pragma unroll
       for (int t = 0; t < NT; ++t) S2 = Pol::mma(Pol::load_row(r, t, g), Q2[t], S2);
     }
     {
-      const T* r = (j < N) ? vv.row(b, h, j) : nullptr;
+      const T* r = (j < Nk) ? vv.row(b, h, j) : nullptr;
 #pragma unroll
       for (int t = 0; t < NT; ++t) Dp = Pol::mma(Pol::load_row(r, t, g), DO[t], Dp);
     }
@@ -191,7 +194,7 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = k0 + crow(r, g);
-      const bool valid = qvalid && key <= i;  // key <= i < N
+      const bool valid = qvalid && key <= pq && key < Nk;
       float rk1 = 1.f, rk2 = 1.f;
       if constexpr (NORM) {
         rk1 = valid ? nk1[key] : 0.f;
@@ -215,7 +218,7 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
     }
     if (!occrow && wave_ballot(any) == 0ull) continue;
     ++computed;
-    prepare_tile<Pol, D>(kt_tile, k1, b, h, k0, N);
+    prepare_tile<Pol, D>(kt_tile, k1, b, h, k0, Nk);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const frag bp = Pol::pack_c(E1, s);
@@ -224,7 +227,7 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
     }
     release_tile<Pol>(kt_tile);
     if constexpr (BR == 2) {
-      prepare_tile<Pol, D>(kt_tile, k2, b, h, k0, N);
+      prepare_tile<Pol, D>(kt_tile, k2, b, h, k0, Nk);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const frag bp = Pol::pack_c(E2, s);
@@ -268,13 +271,13 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
   const int l = lane_id(), n32 = l & 31, g = l >> 5, wv = threadIdx.x >> 6;
   const int BH = P.B * P.H;
   const int64_t item = (int64_t)blockIdx.x * 4 + wv;
-  if (item >= (int64_t)BH * P.nqt) return;
+  if (item >= (int64_t)BH * P.nkt) return;
   const int kt = (int)(item / BH);
   const int bh = (int)(item % BH);
   const int b = bh / P.H, h = bh % P.H;
-  const int N = P.N;
+  const int Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
   const int j = kt * 32 + n32;
-  const bool kvalid = j < N;
+  const bool kvalid = j < Nk;
 
   const TRef<const T> q1{(const T*)P.in[0], P.s[B_Q1][0], P.s[B_Q1][1], P.s[B_Q1][2]};
   const TRef<const T> k1{(const T*)P.in[1], P.s[B_K1][0], P.s[B_K1][1], P.s[B_K1][2]};
@@ -301,16 +304,16 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
   float rk1 = 1.f, rk2 = 1.f;
   if constexpr (NORM) {
     if (kvalid) {
-      rk1 = P.norms[((int64_t)N_K1 * BH + bh) * N + j];
-      if constexpr (BR == 2) rk2 = P.norms[((int64_t)N_K2 * BH + bh) * N + j];
+      rk1 = P.norms[norm_base(P, N_K1, bh) + j];
+      if constexpr (BR == 2) rk2 = P.norms[norm_base(P, N_K2, bh) + j];
     }
   }
   const float pw = P.p;
   const float beta = *P.beta;
   float lam = 0.f;
   if constexpr (BR == 2) lam = clamp01(*P.lam);
-  const float* nq1 = NORM ? P.norms + ((int64_t)N_Q1 * BH + bh) * N : nullptr;
-  const float* nq2 = NORM ? P.norms + ((int64_t)N_Q2 * BH + bh) * N : nullptr;
+  const float* nq1 = NORM ? P.norms + norm_base(P, N_Q1, bh) : nullptr;
+  const float* nq2 = NORM ? P.norms + norm_base(P, N_Q2, bh) : nullptr;
 
   __shared__ __attribute__((aligned(16))) bf16 lds_all[(sizeof(T) == 2) ? 4 * TTileBF16<D>::ELEMS : 8];
   TT tile;
@@ -323,7 +326,7 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
   const uint32_t* occcol = P.occ ? P.occ + (int64_t)bh * P.nqt * P.occ_w + (kt >> 5) : nullptr;
   const int64_t occ_br = (int64_t)BH * P.nqt * P.occ_w;  // branch-plane distance of the bitmask
 
-  for (int qt = kt; qt < P.nqt; ++qt) {
+  for (int qt = qt_first(kt, qoff); qt < P.nqt; ++qt) {
     if (occcol) {  // tile holds a non-zero score of either branch?
       uint32_t w = occcol[(int64_t)qt * P.occ_w];
       if constexpr (BR == 2) w |= occcol[occ_br + (int64_t)qt * P.occ_w];
@@ -334,17 +337,17 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
     const int ia = q0 + n32;  // query row this lane loads for the A operand
     f32x16 S1 = f32x16{}, S2 = f32x16{}, Dp = f32x16{};
     {
-      const T* r = (ia < N) ? q1.row(b, h, ia) : nullptr;
+      const T* r = (ia < Nq) ? q1.row(b, h, ia) : nullptr;
 #pragma unroll
       for (int t = 0; t < NT; ++t) S1 = Pol::mma(Pol::load_row(r, t, g), K1[t], S1);
     }
     if constexpr (BR == 2) {
-      const T* r = (ia < N) ? q2.row(b, h, ia) : nullptr;
+      const T* r = (ia < Nq) ? q2.row(b, h, ia) : nullptr;
 #pragma unroll
       for (int t = 0; t < NT; ++t) S2 = Pol::mma(Pol::load_row(r, t, g), K2[t], S2);
     }
     {
-      const T* r = (ia < N) ? dO.row(b, h, ia) : nullptr;
+      const T* r = (ia < Nq) ? dO.row(b, h, ia) : nullptr;
 #pragma unroll
       for (int t = 0; t < NT; ++t) Dp = Pol::mma(Pol::load_row(r, t, g), V[t], Dp);
     }
@@ -353,13 +356,13 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int qi = q0 + crow(r, g);
-      const bool valid = kvalid && qi < N && j <= qi;
+      const bool valid = kvalid && qi < Nq && j <= qoff + qi;
       float rq1 = 1.f, rq2 = 1.f;
       if constexpr (NORM) {
         rq1 = valid ? nq1[qi] : 0.f;
         if constexpr (BR == 2) rq2 = valid ? nq2[qi] : 0.f;
       }
-      const float tau = beta * tau_coeff(qi, P.inv_d);
+      const float tau = beta * tau_coeff(qoff + qi, P.inv_d);
       const float x1 = __builtin_fmaf(NORM ? S1[r] * rk1 : S1[r], rq1, -tau);
       const bool p1 = valid && x1 > 0.f;
       float a = p1 ? pow_p<PK>(x1, pw) : 0.f;
@@ -379,7 +382,7 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
     }
     if (!occcol && wave_ballot(any) == 0ull) continue;
     ++computed;
-    prepare_tile<Pol, D>(tile, dO, b, h, q0, N);
+    prepare_tile<Pol, D>(tile, dO, b, h, q0, Nq);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const frag bp = Pol::pack_c(EV, s);
@@ -387,7 +390,7 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
       for (int c = 0; c < ND; ++c) AV[c] = Pol::mma(tile.frag(s, c), bp, AV[c]);
     }
     release_tile<Pol>(tile);
-    prepare_tile<Pol, D>(tile, q1, b, h, q0, N);
+    prepare_tile<Pol, D>(tile, q1, b, h, q0, Nq);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const frag bp = Pol::pack_c(E1, s);
@@ -396,7 +399,7 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
     }
     release_tile<Pol>(tile);
     if constexpr (BR == 2) {
-      prepare_tile<Pol, D>(tile, q2, b, h, q0, N);
+      prepare_tile<Pol, D>(tile, q2, b, h, q0, Nq);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const frag bp = Pol::pack_c(E2, s);
@@ -468,11 +471,10 @@ __global__ void __launch_bounds__(kFinThreads) bwd_finish(const float* ws, int64
 // ------------------------------------------------------------------ dispatch
 template <class Pol, int D, int BR, int PK, bool NORM>
 static int launch_bwd_t(const BwdParams& p, void* stream) {
-  const int64_t items = (int64_t)p.B * p.H * p.nqt;
-  const unsigned grid = (unsigned)((items + 3) / 4);
+  const int64_t qitems = (int64_t)p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL((bwd_dq<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, s, p);
-  hipLaunchKernelGGL((bwd_dkv<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((bwd_dq<Pol, D, BR, PK, NORM>), dim3((unsigned)((qitems + 3) / 4)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((bwd_dkv<Pol, D, BR, PK, NORM>), dim3((unsigned)((kitems + 3) / 4)), dim3(256), 0, s, p);
   const int e = (int)hipGetLastError();
   return e ? e : launch_bwd_finish(p, BR, stream);
 }

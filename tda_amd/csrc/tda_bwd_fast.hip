@@ -20,6 +20,7 @@
 // operands and accumulators are live at a time.
 #include "tda_common.hpp"
 #include "tda_params.hpp"
+#include "tda_pos.hpp"
 
 namespace tda {
 
@@ -173,10 +174,12 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
   const int qt = P.nqt - 1 - (int)(item / BH);
   const int bh = (int)(item % BH);
   const int b = bh / P.H, h = bh % P.H;
-  const int N = P.N;
+  const int Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
   const int i = qt * 32 + n32;
-  const bool qvalid = i < N;
-  const int ic = min(i, N - 1);
+  const bool qvalid = i < Nq;
+  const int ic = min(i, Nq - 1);
+  const int pq = qoff + i;                   // the lane's query position
+  const int ktl = kt_last(qt, qoff, P.nkt);  // last key tile the query tile sees
   auto base = [&](int slot) {
     return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
   };
@@ -187,7 +190,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) DO[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
   }
-  const float ci = tau_coeff(i, P.inv_d);
+  const float ci = tau_coeff(pq, P.inv_d);
   const float tau = (*P.beta) * ci;
   const float pw = P.p;
   float lam = 0.f;
@@ -196,7 +199,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
   const int64_t sv = P.s[B_V][2];
   float bsum = 0.f, lsum = 0.f;
   unsigned visited = 0, computed = 0;
-  const int nw = (qt >> 5) + 1;  // bitmask words covering key tiles 0..qt
+  const int nw = (ktl >> 5) + 1;  // bitmask words covering key tiles 0..ktl
 
   // Both branches' row operands, issued with dO so that one memory round trip covers them:
   // query fragments, inverse query norms, bitmask words 0..63 (lane w holds word w).
@@ -209,7 +212,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
     const bf16* r = base(qslot) + (int64_t)ic * P.s[qslot][2];
 #pragma unroll
     for (int t = 0; t < NT; ++t) QB[br][t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
-    RQ[br] = NORM ? P.norms[((int64_t)(br == 0 ? N_Q1 : N_Q2) * BH + bh) * N + ic] : 1.f;
+    RQ[br] = NORM ? P.norms[norm_base(P, br == 0 ? N_Q1 : N_Q2, bh) + ic] : 1.f;
     const uint32_t* occrow = P.occ ? P.occ + (((int64_t)br * BH + bh) * P.nqt + qt) * P.occ_w : nullptr;
     LW[br] = l < nw ? (occrow ? occrow[l] : 0xffffffffu) : 0u;
   }
@@ -224,7 +227,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
     if constexpr (NORM) load_grad_row<D>(base(qslot) + (int64_t)ic * P.s[qslot][2], XR);
     const float rq = RQ[br];
     const float* nk = nullptr;
-    if constexpr (NORM) nk = P.norms + ((int64_t)(br == 0 ? N_K1 : N_K2) * BH + bh) * N;
+    if constexpr (NORM) nk = P.norms + norm_base(P, br == 0 ? N_K1 : N_K2, bh);
     const float coef = br == 0 ? 1.f : -lam;
     f32x16 A[ND];
 #pragma unroll
@@ -235,15 +238,15 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
       const uint32_t lw = w0 == 0 ? LW[br] : (w0 + l < nw) ? (occrow ? occrow[w0 + l] : 0xffffffffu) : 0u;
       for (int w = w0; w < min(nw, w0 + 64); ++w) {
         uint32_t bits = __builtin_amdgcn_readlane(lw, w - w0);
-        if (w == (qt >> 5)) bits &= (qt & 31) == 31 ? 0xffffffffu : ((2u << (qt & 31)) - 1u);
+        if (w == (ktl >> 5)) bits &= (ktl & 31) == 31 ? 0xffffffffu : ((2u << (ktl & 31)) - 1u);
         while (bits) {
           const int kt = 32 * w + __builtin_ctz(bits);
           bits &= bits - 1u;
           ++visited;
           const int k0 = 32 * kt;
-          dma_tile<D>(kb, sk, k0, N, W.a);
-          dma_tile<D>(vb, sv, k0, N, W.b);
-          if constexpr (NORM) dma_row_vals(nk, k0, N, W.rows);
+          dma_tile<D>(kb, sk, k0, Nk, W.a);
+          dma_tile<D>(vb, sv, k0, Nk, W.b);
+          if constexpr (NORM) dma_row_vals(nk, k0, Nk, W.rows);
           wait_all_loads();
           f32x16 S = f32x16{}, Dp = f32x16{};
 #pragma unroll
@@ -257,7 +260,8 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
           bool any = false;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const bool valid = qvalid && (k0 + crow(r, g) <= i);
+            const int key = k0 + crow(r, g);
+            const bool valid = qvalid && key <= pq && key < Nk;  // rows past Nk are copies
             const float sr = NORM ? S[r] * rk[r] : S[r];
             const float x = __builtin_fmaf(sr, rq, -tau);
             const bool pos = valid && x > 0.f;
@@ -309,14 +313,15 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
   BwdWaveLds<D>& W = lds_all[wv];
   const int BH = P.B * P.H;
   const int64_t item = (int64_t)blockIdx.x * kBwdWaves + wv;
-  if (item >= (int64_t)BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
+  if (item >= (int64_t)BH * P.nkt) return;  // whole wave leaves; no workgroup barriers below
   const int kt = (int)(item / BH);
   const int bh = (int)(item % BH);
   const int b = bh / P.H, h = bh % P.H;
-  const int N = P.N;
+  const int Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
   const int j = kt * 32 + n32;
-  const bool kvalid = j < N;
-  const int jc = min(j, N - 1);
+  const bool kvalid = j < Nk;
+  const int jc = min(j, Nk - 1);
+  const int qtf = qt_first(kt, qoff);  // first query tile that sees the key tile
   auto base = [&](int slot) {
     return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
   };
@@ -339,8 +344,8 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
   unsigned visited = 0, computed = 0;
 
   // Both branches' row operands, issued with V so that one memory round trip covers them: key
-  // fragments, inverse key norms, and the bitmask column bits of query tiles kt .. kt+63
-  // (lane q holds tile kt + q).
+  // fragments, inverse key norms, and the bitmask column bits of query tiles qtf .. qtf+63
+  // (lane q holds tile qtf + q).
   bf16x8 KB[BR][NT];
   float RK[BR];
   bool HAS[BR];
@@ -350,9 +355,9 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
     const bf16* r = base(kslot) + (int64_t)jc * P.s[kslot][2];
 #pragma unroll
     for (int t = 0; t < NT; ++t) KB[br][t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
-    RK[br] = NORM ? P.norms[((int64_t)(br == 0 ? N_K1 : N_K2) * BH + bh) * N + jc] : 1.f;
+    RK[br] = NORM ? P.norms[norm_base(P, br == 0 ? N_K1 : N_K2, bh) + jc] : 1.f;
     const uint32_t* occcol = P.occ ? P.occ + ((int64_t)br * BH + bh) * P.nqt * P.occ_w + (kt >> 5) : nullptr;
-    const int qtl = kt + l;
+    const int qtl = qtf + l;
     HAS[br] = qtl < P.nqt && (!occcol || ((occcol[(int64_t)qtl * P.occ_w] >> (kt & 31)) & 1u));
   }
 
@@ -366,27 +371,27 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
     if constexpr (NORM) load_grad_row<D>(base(kslot) + (int64_t)jc * P.s[kslot][2], XR);
     const float rk = RK[br];
     const float* nq = nullptr;
-    if constexpr (NORM) nq = P.norms + ((int64_t)(br == 0 ? N_Q1 : N_Q2) * BH + bh) * N;
+    if constexpr (NORM) nq = P.norms + norm_base(P, br == 0 ? N_Q1 : N_Q2, bh);
     const float coef = br == 0 ? 1.f : -lam;
     f32x16 AK[ND];
 #pragma unroll
     for (int c = 0; c < ND; ++c) AK[c] = f32x16{};
-    // bitmask column: bit kt % 32 of word (br, bh, qt, kt / 32) for qt = kt .. nqt-1
+    // bitmask column: bit kt % 32 of word (br, bh, qt, kt / 32) for qt = qtf .. nqt-1
     const uint32_t* occcol = P.occ ? P.occ + ((int64_t)br * BH + bh) * P.nqt * P.occ_w + (kt >> 5) : nullptr;
 
-    for (int q0c = kt; q0c < P.nqt; q0c += 64) {
+    for (int q0c = qtf; q0c < P.nqt; q0c += 64) {
       const int qtl = q0c + l;
-      const bool has = q0c == kt ? HAS[br] : qtl < P.nqt && (!occcol || ((occcol[(int64_t)qtl * P.occ_w] >> (kt & 31)) & 1u));
+      const bool has = q0c == qtf ? HAS[br] : qtl < P.nqt && (!occcol || ((occcol[(int64_t)qtl * P.occ_w] >> (kt & 31)) & 1u));
       uint64_t mask = wave_ballot(has);
       while (mask) {
         const int qt = q0c + __builtin_ctzll(mask);
         mask &= mask - 1ull;
         ++visited;
         const int q0 = 32 * qt;
-        dma_tile<D>(qb, sq, q0, N, W.a);
-        dma_tile<D>(dob, sdo, q0, N, W.b);
-        if constexpr (NORM) dma_row_vals(nq, q0, N, W.rows);
-        if (l < 32) W.taus[l] = beta * tau_coeff(q0 + l, P.inv_d);
+        dma_tile<D>(qb, sq, q0, Nq, W.a);
+        dma_tile<D>(dob, sdo, q0, Nq, W.b);
+        if constexpr (NORM) dma_row_vals(nq, q0, Nq, W.rows);
+        if (l < 32) W.taus[l] = beta * tau_coeff(qoff + q0 + l, P.inv_d);
         wait_all_loads();
         f32x16 S = f32x16{}, Dp = f32x16{};
 #pragma unroll
@@ -402,7 +407,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int qi = q0 + crow(r, g);
-          const bool valid = kvalid && qi < N && j <= qi;
+          const bool valid = kvalid && qi < Nq && j <= qoff + qi;
           const float sr = NORM ? S[r] * rk : S[r];
           const float x = __builtin_fmaf(sr, NORM ? rq[r] : 1.f, -tq[r]);
           const bool pos = valid && x > 0.f;
@@ -444,11 +449,12 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
 // ------------------------------------------------------------------ dispatch
 template <int D, int BR, int PK, bool NORM>
 static int launch_t(const BwdParams& p, void* stream) {
-  const int64_t items = (int64_t)p.B * p.H * p.nqt;
-  const unsigned grid = (unsigned)((items + kBwdWaves - 1) / kBwdWaves);
+  const int64_t qitems = (int64_t)p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3(grid), dim3(64 * kBwdWaves), 0, s, p);
-  hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3(grid), dim3(64 * kBwdWaves), 0, s, p);
+  hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3((unsigned)((qitems + kBwdWaves - 1) / kBwdWaves)),
+                     dim3(64 * kBwdWaves), 0, s, p);
+  hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3((unsigned)((kitems + kBwdWaves - 1) / kBwdWaves)),
+                     dim3(64 * kBwdWaves), 0, s, p);
   const int e = (int)hipGetLastError();
   return e ? e : launch_bwd_finish(p, BR, stream);
 }

@@ -9,6 +9,7 @@
 // out = sum_j (A1_ij - clamp(lambda) A2_ij) v_j, so the differential combine is free.
 #include "tda_common.hpp"
 #include "tda_params.hpp"
+#include "tda_pos.hpp"
 
 namespace tda {
 
@@ -40,9 +41,11 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
   const int qt = P.nqt - 1 - (int)(item / BH);
   const int bh = (int)(item % BH);
   const int b = bh / P.H, h = bh % P.H;
-  const int N = P.N;
+  const int Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
   const int i = qt * 32 + n32;  // this lane's query row
-  const bool qvalid = i < N;
+  const bool qvalid = i < Nq;
+  const int pq = qoff + i;                   // its position
+  const int ktl = kt_last(qt, qoff, P.nkt);  // last key tile the query tile sees
 
   const TRef<const T> q1{(const T*)P.in[0], P.s[F_Q1][0], P.s[F_Q1][1], P.s[F_Q1][2]};
   const TRef<const T> k1{(const T*)P.in[1], P.s[F_K1][0], P.s[F_K1][1], P.s[F_K1][2]};
@@ -67,12 +70,12 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
     rq1 = inv_norm(row_sumsq<Pol, NT>(Q1));
     if constexpr (BR == 2) rq2 = inv_norm(row_sumsq<Pol, NT>(Q2));
     if (P.norms && qvalid && g == 0) {
-      P.norms[((int64_t)N_Q1 * BH + bh) * N + i] = rq1;
-      if constexpr (BR == 2) P.norms[((int64_t)N_Q2 * BH + bh) * N + i] = rq2;
+      P.norms[norm_base(P, N_Q1, bh) + i] = rq1;
+      if constexpr (BR == 2) P.norms[norm_base(P, N_Q2, bh) + i] = rq2;
     }
   }
   const float pw = P.p;
-  const float tau = (*P.beta) * tau_coeff(i, P.inv_d);
+  const float tau = (*P.beta) * tau_coeff(pq, P.inv_d);
   float lam = 0.f;
   if constexpr (BR == 2) lam = clamp01(*P.lam);
 
@@ -90,35 +93,36 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
   uint32_t word = 0, word2 = 0;
   unsigned visited = 0, computed = 0;
 
-  for (int kt = 0; kt <= qt; ++kt) {
+  for (int kt = 0; kt <= ktl; ++kt) {
     const int k0 = kt * 32;
     const int j = k0 + n32;  // key row this lane loads for the A operand
+    const bool kfirst = qt == qt_first(kt, qoff);  // the first query tile to see kt writes its norms
     f32x16 S1 = f32x16{}, S2 = f32x16{};
     float rk1r[16], rk2r[16];
     {
       frag K1[NT];
-      const T* r1 = (j < N) ? k1.row(b, h, j) : nullptr;
+      const T* r1 = (j < Nk) ? k1.row(b, h, j) : nullptr;
 #pragma unroll
       for (int t = 0; t < NT; ++t) K1[t] = Pol::load_row(r1, t, g);
 #pragma unroll
       for (int t = 0; t < NT; ++t) S1 = Pol::mma(K1[t], Q1[t], S1);
       if constexpr (NORM) {
         const float rk = inv_norm(row_sumsq<Pol, NT>(K1));
-        if (P.norms && kt == qt && g == 0 && j < N) P.norms[((int64_t)N_K1 * BH + bh) * N + j] = rk;
+        if (P.norms && kfirst && g == 0 && j < Nk) P.norms[norm_base(P, N_K1, bh) + j] = rk;
 #pragma unroll
         for (int r = 0; r < 16; ++r) rk1r[r] = __shfl(rk, crow(r, g));
       }
     }
     if constexpr (BR == 2) {
       frag K2[NT];
-      const T* r2 = (j < N) ? k2.row(b, h, j) : nullptr;
+      const T* r2 = (j < Nk) ? k2.row(b, h, j) : nullptr;
 #pragma unroll
       for (int t = 0; t < NT; ++t) K2[t] = Pol::load_row(r2, t, g);
 #pragma unroll
       for (int t = 0; t < NT; ++t) S2 = Pol::mma(K2[t], Q2[t], S2);
       if constexpr (NORM) {
         const float rk = inv_norm(row_sumsq<Pol, NT>(K2));
-        if (P.norms && kt == qt && g == 0 && j < N) P.norms[((int64_t)N_K2 * BH + bh) * N + j] = rk;
+        if (P.norms && kfirst && g == 0 && j < Nk) P.norms[norm_base(P, N_K2, bh) + j] = rk;
 #pragma unroll
         for (int r = 0; r < 16; ++r) rk2r[r] = __shfl(rk, crow(r, g));
       }
@@ -129,7 +133,8 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
     float m1 = -INFINITY, m2 = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const bool valid = qvalid && (k0 + crow(r, g) <= i);
+      const int key = k0 + crow(r, g);
+      const bool valid = qvalid && key <= pq && key < Nk;
       if constexpr (NORM) S1[r] *= rk1r[r];
       m1 = fmaxf(m1, valid ? S1[r] : -INFINITY);
       if constexpr (BR == 2) {
@@ -148,7 +153,8 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
       f32x16 C;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const bool valid = qvalid && (k0 + crow(r, g) <= i);
+        const int key = k0 + crow(r, g);
+        const bool valid = qvalid && key <= pq && key < Nk;
         const float x1 = __builtin_fmaf(S1[r], rq1, -tau);
         float a = (valid && x1 > 0.f) ? pow_p<PK>(x1, pw) : 0.f;
         if constexpr (BR == 2) {
@@ -159,10 +165,10 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
         C[r] = a;
       }
       if constexpr (sizeof(T) == 2) {
-        vt.stage(vv, b, h, k0, N);
+        vt.stage(vv, b, h, k0, Nk);
         wave_lds_sync();
       } else {
-        vt.set(vv, b, h, k0, N);
+        vt.set(vv, b, h, k0, Nk);
       }
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -172,7 +178,7 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
       }
       if constexpr (sizeof(T) == 2) wave_lds_sync();
     }
-    if (occrow && (((kt & 31) == 31) || kt == qt)) {
+    if (occrow && (((kt & 31) == 31) || kt == ktl)) {
       if (l == 0) {
         occrow[kt >> 5] = word;
         if constexpr (BR == 2) occrow[occ_br + (kt >> 5)] = word2;
@@ -181,9 +187,33 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
     }
   }
   if (occrow && l == 0) {
-    for (int w = (qt >> 5) + 1; w < P.occ_w; ++w) {
+    for (int w = (ktl >> 5) + 1; w < P.occ_w; ++w) {
       occrow[w] = 0u;
       if constexpr (BR == 2) occrow[occ_br + w] = 0u;
+    }
+  }
+
+  // Key tiles no query tile sees (keys past the last query position): their inverse norms
+  // still go to the table (the backward's normalize epilogue reads every key row's), written
+  // by the last query tile's wave.
+  if constexpr (NORM) {
+    if (P.norms && qt == P.nqt - 1) {
+      for (int kt = ktl + 1; kt < P.nkt; ++kt) {
+        const int j = 32 * kt + n32;
+        frag K[NT];
+        const T* r1 = (j < Nk) ? k1.row(b, h, j) : nullptr;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) K[t] = Pol::load_row(r1, t, g);
+        const float rka = inv_norm(row_sumsq<Pol, NT>(K));
+        if (g == 0 && j < Nk) P.norms[norm_base(P, N_K1, bh) + j] = rka;
+        if constexpr (BR == 2) {
+          const T* r2 = (j < Nk) ? k2.row(b, h, j) : nullptr;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) K[t] = Pol::load_row(r2, t, g);
+          const float rkb = inv_norm(row_sumsq<Pol, NT>(K));
+          if (g == 0 && j < Nk) P.norms[norm_base(P, N_K2, bh) + j] = rkb;
+        }
+      }
     }
   }
 

@@ -25,6 +25,7 @@
 // and padding keys past N: it may keep a tile the mask empties, never drop a non-zero one.
 #include "tda_common.hpp"
 #include "tda_params.hpp"
+#include "tda_pos.hpp"
 
 namespace tda {
 namespace {
@@ -113,7 +114,7 @@ __global__ void __launch_bounds__(256) key_norms(FwdParams P, int BR) {
   constexpr int RPG = 64 / LPR;     // rows per load instruction
   constexpr int ROWS = RPG * KN_GROUPS;
   const int l = lane_id(), sub = l % LPR;
-  const int BH = P.B * P.H, N = P.N;
+  const int BH = P.B * P.H, N = P.Nk;     // key rows
   const int wpr = (N + ROWS - 1) / ROWS;  // waves per (branch, head)
   const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (wid >= (int64_t)BR * BH * wpr) return;  // whole wave, no barriers
@@ -128,7 +129,7 @@ __global__ void __launch_bounds__(256) key_norms(FwdParams P, int BR) {
     const int t = min(t0 + RPG * u, N - 1);
     x[u] = *reinterpret_cast<const bf16x8*>(head + (int64_t)t * st + 8 * sub);
   }
-  float* out = P.norms + ((int64_t)(br ? N_K2 : N_K1) * BH + bh) * N;
+  float* out = P.norms + norm_base(P, br ? N_K2 : N_K1, bh);
 #pragma unroll
   for (int u = 0; u < KN_GROUPS; ++u) {
     float ss = PolBF16::sumsq(x[u]);
@@ -167,19 +168,23 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5, tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int BH = P.B * P.H, N = P.N, nqt = P.nqt;
-  const WorkItem wi = xcd_order(blockIdx.x, BR * BH, (N + 255) / 256);
+  const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
+  const WorkItem wi = xcd_order(blockIdx.x, BR * BH, (Nq + 255) / 256);
   const int sidx = wi.stream, qb = wi.block;
   const int br = sidx / BH, bh = sidx % BH;
   const int b = bh / P.H, h = bh % P.H;
   const int qslot = br ? F_Q2 : F_Q1, kslot = br ? F_K2 : F_K1;
   const int q0w = qb * 256 + 32 * QPW * wv;  // first row of this wave
   const int qt0 = q0w >> 5;                  // this wave's query tiles: qt0 .. qt0 + QPW - 1
-  const int nkt = min(nqt, 8 * qb + 8);
+  const int nkt = kt_last(min(8 * qb + 7, nqt - 1), qoff, P.nkt) + 1;  // key tiles of the workgroup
   const int nit = (nkt + TPB - 1) / TPB;
   bool live[QPW];
+  int ktl[QPW];  // last key tile each query tile sees
 #pragma unroll
-  for (int s = 0; s < QPW; ++s) live[s] = qt0 + s < nqt;
+  for (int s = 0; s < QPW; ++s) {
+    live[s] = qt0 + s < nqt;
+    ktl[s] = kt_last(qt0 + s, qoff, P.nkt);
+  }
 
   // ---- staging
   const bf16* khead = (const bf16*)P.in[kslot] + (int64_t)b * P.s[kslot][0] + (int64_t)h * P.s[kslot][1];
@@ -189,7 +194,7 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
   const uint32_t soff = (uint32_t)((srow * sk + 8 * sch) * 2);
   // key norms: threads 0..7 stage four rows each (rows past N read as 0, never used)
   const __amdgpu_buffer_rsrc_t rnorm =
-      make_rsrc(NORM ? P.norms + ((int64_t)(br ? N_K2 : N_K1) * BH + bh) * N : nullptr, NORM ? (uint32_t)N * 4 : 0u);
+      make_rsrc(NORM ? P.norms + norm_base(P, br ? N_K2 : N_K1, bh) : nullptr, NORM ? (uint32_t)Nk * 4 : 0u);
   u32x4 R[TPB][CPT], RN[TPB];
   auto fetch = [&](int it) {  // tiles of group it into registers
 #pragma unroll
@@ -197,7 +202,7 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
       const int kt = TPB * it + j;
       if (kt >= nkt) break;
       if (stager) {
-        const __amdgpu_buffer_rsrc_t rs = tile_rsrc<D>(khead, sk, kt, N);
+        const __amdgpu_buffer_rsrc_t rs = tile_rsrc<D>(khead, sk, kt, Nk);
 #pragma unroll
         for (int c = 0; c < CPT; ++c) R[j][c] = buf_load16(rs, soff + 16 * TPR * c);
       }
@@ -230,14 +235,14 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
 #pragma unroll
   for (int s = 0; s < QPW; ++s) {
     const int iq = q0w + 32 * s + n32;
-    valid[s] = iq < N;
-    const bf16* row = qhead + (int64_t)min(iq, N - 1) * P.s[qslot][2];  // rows >= N: never vote
+    valid[s] = iq < Nq;
+    const bf16* row = qhead + (int64_t)min(iq, Nq - 1) * P.s[qslot][2];  // rows >= Nq: never vote
 #pragma unroll
     for (int t = 0; t < NT; ++t) Q[s][t] = *reinterpret_cast<const bf16x8*>(row + 16 * t + 8 * g);
     if constexpr (NORM) {
       const float rq = inv_norm(row_sumsq<PolBF16, NT>(Q[s]));
-      if (g == 0 && valid[s]) P.norms[((int64_t)(br ? N_Q2 : N_Q1) * BH + bh) * N + iq] = rq;
-      // rows past N score 0; so do non-finite elements (NaN/Inf inputs), whose exact weights
+      if (g == 0 && valid[s]) P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + iq] = rq;
+      // rows past Nq score 0; so do non-finite elements (NaN/Inf inputs), whose exact weights
       // are 0 (x > 0 fails on NaN), so a NaN score can only come from a non-finite key row:
       // it poisons the maximum of that key's lane alone, whose weights are 0 as well
       const float sc = valid[s] ? rq : 0.f;
@@ -248,11 +253,12 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
           const float x = (float)Q[s][t][j] * sc;
           Q[s][t][j] = (bf16)(__builtin_isfinite(x) ? x : 0.f);
         }
-      // tau is monotone in i: its smallest value over the tile's rows is at one of the ends
-      const int i0 = q0w + 32 * s, i1 = max(i0, min(i0 + 31, N - 1));
-      tau[s] = screen_tlo(fminf(beta * tau_coeff(i0, P.inv_d), beta * tau_coeff(i1, P.inv_d)));
+      // tau is monotone in the position: its smallest value over the tile's rows is at one of
+      // the ends
+      const int i0 = q0w + 32 * s, i1 = max(i0, min(i0 + 31, Nq - 1));
+      tau[s] = screen_tlo(fminf(beta * tau_coeff(qoff + i0, P.inv_d), beta * tau_coeff(qoff + i1, P.inv_d)));
     } else {
-      tau[s] = beta * tau_coeff(iq, P.inv_d);
+      tau[s] = beta * tau_coeff(qoff + iq, P.inv_d);
     }
   }
 
@@ -266,7 +272,7 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
 
   // Threshold test of key tile kt (in stage st) against this wave's query tiles.
   auto process = [&](int kt, int st) {
-    if (!(live[0] && kt <= qt0 + QPW - 1)) return;
+    if (!(live[0] && kt <= ktl[QPW - 1])) return;
     const bf16* kp = &kst[st][koff];
     bf16x8 fk[NT];
 #pragma unroll
@@ -294,7 +300,7 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     const uint32_t bit = 1u << (kt & 31);
 #pragma unroll
     for (int s = 0; s < QPW; ++s) {
-      if (kt > qt0 + s) continue;  // key tiles after the query tile hold no causal pair
+      if (kt > ktl[s]) continue;  // key tiles after the query tile's last position hold no causal pair
       bool hit;
       if constexpr (NORM) hit = maximum16(S[s]) * rk > tau[s];  // largest score of the lane's key
       else hit = valid[s] && max16(S[s]) > tau[s];          // largest score of the lane's query
@@ -341,7 +347,7 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     // causal (query tile, key tile) pairs of this wave: key tiles 0 .. qt of each live query tile
     unsigned visited = 0;
 #pragma unroll
-    for (int s = 0; s < QPW; ++s) visited += live[s] ? (unsigned)(qt0 + s + 1) : 0u;
+    for (int s = 0; s < QPW; ++s) visited += live[s] ? (unsigned)(ktl[s] + 1) : 0u;
     if (visited) atomicAdd(P.stats + 0, (unsigned long long)visited);
   }
 }
@@ -374,7 +380,7 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int BH = P.B * P.H, N = P.N, nqt = P.nqt;
+  const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
   const int nblk = (nqt + kPvWaves - 1) / kPvWaves;
   int bh, blk;
   {
@@ -392,8 +398,10 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
   if (qt >= nqt) return;
   const int b = bh / P.H, h = bh % P.H;
   const int iq = 32 * qt + n32;
-  const bool valid = iq < N;
-  const float tau = *P.beta * tau_coeff(iq, P.inv_d);
+  const bool valid = iq < Nq;
+  const int pq = qoff + iq;                  // the lane's query position
+  const int klast = kt_last(qt, qoff, P.nkt);  // last key tile the query tile sees
+  const float tau = *P.beta * tau_coeff(pq, P.inv_d);
   const float pw = P.p;
   float lam = 0.f;
   if constexpr (BR == 2) lam = clamp01(*P.lam);
@@ -417,12 +425,12 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
     const bf16* vhead = (const bf16*)P.in[F_V] + (int64_t)b * P.s[F_V][0] + (int64_t)h * P.s[F_V][1];
     const int64_t sk = P.s[kslot][2], sv = P.s[F_V][2];
     const __amdgpu_buffer_rsrc_t rn =
-        make_rsrc(NORM ? P.norms + ((int64_t)(br ? N_K2 : N_K1) * BH + bh) * N : nullptr, NORM ? (uint32_t)N * 4 : 0u);
+        make_rsrc(NORM ? P.norms + norm_base(P, br ? N_K2 : N_K1, bh) : nullptr, NORM ? (uint32_t)Nk * 4 : 0u);
     const float coef = br == 0 ? 1.f : -lam;
     bool have_q = false;
     bf16x8 Q[NT];
     float rq = 1.f;
-    for (int w = 0; w <= (qt >> 5); ++w) {
+    for (int w = 0; w <= (klast >> 5); ++w) {
       const uint32_t bits0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)orow[w]);
       uint32_t bits = bits0, keep = bits0;
       while (bits) {
@@ -432,7 +440,7 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
         if (!have_q) {
           // query tile rows with whole-row loads, through the (still free) K tile buffer
           const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
-          const __amdgpu_buffer_rsrc_t rq_ = tile_rsrc<D>(qhead, P.s[qslot][2], qt, N);
+          const __amdgpu_buffer_rsrc_t rq_ = tile_rsrc<D>(qhead, P.s[qslot][2], qt, Nq);
           u32x4 qr[VL];
 #pragma unroll
           for (int i = 0; i < VL; ++i)
@@ -444,12 +452,12 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
 #pragma unroll
           for (int t = 0; t < NT; ++t) Q[t] = *reinterpret_cast<const bf16x8*>(qp + 16 * t);
           wave_lds_sync();
-          if constexpr (NORM) rq = P.norms[((int64_t)(br ? N_Q2 : N_Q1) * BH + bh) * N + min(iq, N - 1)];
+          if constexpr (NORM) rq = P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + min(iq, Nq - 1)];
           have_q = true;
         }
         // loads of the key tile (A operand rows), the V tile and the key norms
-        const __amdgpu_buffer_rsrc_t rk = tile_rsrc<D>(khead, sk, kt, N);
-        const __amdgpu_buffer_rsrc_t rv = tile_rsrc<D>(vhead, sv, kt, N);
+        const __amdgpu_buffer_rsrc_t rk = tile_rsrc<D>(khead, sk, kt, Nk);
+        const __amdgpu_buffer_rsrc_t rv = tile_rsrc<D>(vhead, sv, kt, Nk);
         // whole rows per load instruction (coalesced), staged through LDS like V
         u32x4 kr[VL];
 #pragma unroll
@@ -473,8 +481,9 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
 #pragma unroll
         for (int i = 0; i < VL; ++i) *reinterpret_cast<u32x4*>(vt + (vrow + RPI * i) * VS + 8 * vch) = vr[i];
 
-        // exact weights: keys after the query (diagonal tile only) are masked
-        const bool diag = kt == qt;
+        // exact weights: keys after the query's position and padding keys past Nk are masked
+        // (only tiles reaching past the position of the tile's first row, or past Nk, have any)
+        const bool edge = 32 * kt + 31 > min(qoff + 32 * qt, Nk - 1);
         f32x16 C;
         bool pos_any = false;
 #pragma unroll
@@ -483,7 +492,8 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * u + e;
             const float x = __builtin_fmaf(NORM ? S[r] * rk4[u][e] : S[r], rq, -tau);
-            const bool pos = (!diag || 32 * kt + crow(r, g) <= iq) && x > 0.f;
+            const int key = 32 * kt + crow(r, g);
+            const bool pos = (!edge || (key <= pq && key < Nk)) && x > 0.f;
             C[r] = pos ? coef * pow_p<PK>(x, pw) : 0.f;
             pos_any |= pos;
           }
@@ -520,7 +530,7 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
 #pragma unroll
     for (int i = 0; i < VL; ++i) {
       const int r = vrow + RPI * i, row = 32 * qt + r;
-      if (row < N)
+      if (row < Nq)
         *reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch) =
             *reinterpret_cast<const u32x4*>(ktl + r * KS + 8 * vch);
     }
@@ -537,10 +547,10 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   const int BH = p.B * p.H;
   if constexpr (NORM) {
     constexpr int rows = (64 / (D / 8)) * KN_GROUPS;  // rows per wave
-    const int64_t waves = (int64_t)BR * BH * ((p.N + rows - 1) / rows);
+    const int64_t waves = (int64_t)BR * BH * ((p.Nk + rows - 1) / rows);
     hipLaunchKernelGGL(key_norms<D>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, BR);
   }
-  const unsigned nqb = (unsigned)((p.N + 255) / 256);
+  const unsigned nqb = (unsigned)((p.Nq + 255) / 256);
   constexpr int QPW = 2, TPB = 1;
   hipLaunchKernelGGL((fwd_screen<D, NORM, QPW, TPB>), dim3((unsigned)(BR * BH) * nqb), dim3(512 / QPW), 0, s, p, BR);
   const unsigned nblk = (unsigned)((p.nqt + kPvWaves - 1) / kPvWaves);

@@ -39,7 +39,10 @@ struct Common {
   int64_t batch, heads, seq_len, head_dim;
   const float* beta;
   const float* lambda_param;
+  int64_t seq_len_kv, q_offset;  // seq_len_kv resolved (0 -> seq_len)
 };
+
+constexpr int64_t kMaxPos = (int64_t(1) << 30) - 64;  // positions and row counts stay in int32
 
 int32_t check_common(const Common& c) {
   if (c.abi_version != TDA_ABI_VERSION) return TDA_ERR_ABI;
@@ -51,6 +54,9 @@ int32_t check_common(const Common& c) {
   if (c.seq_len > (int64_t(1) << 30)) return TDA_ERR_SHAPE;
   if (c.batch * c.heads > (int64_t(1) << 24)) return TDA_ERR_SHAPE;
   if (c.batch * c.heads * ceil_div(c.seq_len, 32) > (int64_t(1) << 31) - 4) return TDA_ERR_SHAPE;
+  if (c.q_offset < 0 || c.seq_len_kv < 1 || c.seq_len_kv > kMaxPos || c.q_offset + c.seq_len > kMaxPos)
+    return TDA_ERR_OFFSET;
+  if (c.batch * c.heads * ceil_div(c.seq_len_kv, 32) > (int64_t(1) << 31) - 4) return TDA_ERR_SHAPE;
   if (!std::isfinite(c.relu_power) || c.relu_power < 0.f) return TDA_ERR_POWER;
   if (!c.beta) return TDA_ERR_NULL_POINTER;
   if (c.branches == 2 && !c.lambda_param) return TDA_ERR_NULL_POINTER;
@@ -61,9 +67,14 @@ int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
 
 // Forward workspace: the bitmask scratch used when the caller asks for no occupancy output
 // (the bf16 forward always builds the bitmask: its second pass reads it).
-int64_t fwd_ws_bytes(int64_t bh, int64_t seq_len, int64_t branches) {
-  const int64_t nqt = ceil_div(seq_len, 32);
-  return round256(branches * bh * nqt * ceil_div(nqt, 32) * (int64_t)sizeof(uint32_t));
+int64_t occ_words(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t branches) {
+  return branches * bh * ceil_div(seq_len, 32) * ceil_div(ceil_div(seq_len_kv, 32), 32);
+}
+int64_t fwd_ws_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t branches) {
+  return round256(occ_words(bh, seq_len, seq_len_kv, branches) * (int64_t)sizeof(uint32_t));
+}
+bool size_args_ok(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv, int32_t branches) {
+  return batch >= 1 && heads >= 1 && seq_len >= 1 && seq_len_kv >= 1 && (branches == 1 || branches == 2);
 }
 
 int pkind_of(float p) { return p == 2.0f ? 2 : (p == 1.0f ? 1 : 0); }
@@ -71,7 +82,8 @@ int pkind_of(float p) { return p == 2.0f ? 2 : (p == 1.0f ? 1 : 0); }
 template <class A>
 Common common_of(const A& a) {
   return Common{a.abi_version, a.dtype, a.branches, a.normalize, a.causal, a.relu_power,
-                a.batch, a.heads, a.seq_len, a.head_dim, a.beta, a.lambda_param};
+                a.batch, a.heads, a.seq_len, a.head_dim, a.beta, a.lambda_param,
+                a.seq_len_kv ? a.seq_len_kv : a.seq_len, a.q_offset};
 }
 
 void copy_strides(int64_t dst[3], const tda_tensor& t) {
@@ -104,25 +116,40 @@ const char* tda_error_string(int32_t code) {
     case TDA_ERR_ABI: return "abi_version mismatch";
     case TDA_ERR_CAUSAL: return "only the causal form is implemented (causal must be 1)";
     case TDA_ERR_NORMS: return "normalize requires the norms buffer (forward: output, backward: the forward's output)";
+    case TDA_ERR_OFFSET: return "q_offset must be >= 0, and seq_len_kv and q_offset + seq_len at most 2^30 - 64";
     case TDA_ERR_HIP: return "HIP kernel launch failed";
     default: return "unknown error";
   }
 }
 
+size_t tda_occupancy_words_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv,
+                              int32_t branches) {
+  if (!size_args_ok(batch, heads, seq_len, seq_len_kv, branches)) return 0;
+  return (size_t)occ_words(batch * heads, seq_len, seq_len_kv, branches);
+}
+
+size_t tda_norms_floats_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv,
+                           int32_t branches) {
+  if (!size_args_ok(batch, heads, seq_len, seq_len_kv, branches)) return 0;
+  return (size_t)(branches * batch * heads * (seq_len + seq_len_kv));
+}
+
+size_t tda_fwd_workspace_bytes_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv,
+                                  int32_t branches) {
+  if (!size_args_ok(batch, heads, seq_len, seq_len_kv, branches)) return 0;
+  return (size_t)fwd_ws_bytes(batch * heads, seq_len, seq_len_kv, branches);
+}
+
 size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches) {
-  if (batch < 1 || heads < 1 || seq_len < 1 || (branches != 1 && branches != 2)) return 0;
-  const int64_t nqt = ceil_div(seq_len, 32);
-  return (size_t)(branches * batch * heads * nqt * ceil_div(nqt, 32));
+  return tda_occupancy_words_kv(batch, heads, seq_len, seq_len, branches);
 }
 
 size_t tda_norms_floats(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches) {
-  if (batch < 1 || heads < 1 || seq_len < 1 || (branches != 1 && branches != 2)) return 0;
-  return (size_t)(2 * branches * batch * heads * seq_len);
+  return tda_norms_floats_kv(batch, heads, seq_len, seq_len, branches);
 }
 
 size_t tda_fwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches) {
-  if (batch < 1 || heads < 1 || seq_len < 1 || (branches != 1 && branches != 2)) return 0;
-  return (size_t)fwd_ws_bytes(batch * heads, seq_len, branches);
+  return tda_fwd_workspace_bytes_kv(batch, heads, seq_len, seq_len, branches);
 }
 
 size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim) {
@@ -141,8 +168,9 @@ int32_t tda_validate_fwd(const tda_fwd_args* a) {
   for (int k = 0; k < n; ++k)
     if ((rc = check_tensor(*ts[k], eb))) return rc;
   if (a->normalize && !a->norms) return TDA_ERR_NORMS;
+  const Common c = common_of(*a);
   if (!a->workspace ||
-      a->workspace_bytes < tda_fwd_workspace_bytes(a->batch, a->heads, a->seq_len, a->branches))
+      a->workspace_bytes < tda_fwd_workspace_bytes_kv(a->batch, a->heads, a->seq_len, c.seq_len_kv, a->branches))
     return TDA_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0) return TDA_ERR_WORKSPACE;
   return TDA_OK;
@@ -180,11 +208,15 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
   }
   p.out = a->out.data;
   copy_strides(p.s[tda::F_OUT], a->out);
+  const Common c = common_of(*a);
   p.B = (int)a->batch;
   p.H = (int)a->heads;
-  p.N = (int)a->seq_len;
+  p.Nq = (int)a->seq_len;
+  p.Nk = (int)c.seq_len_kv;
+  p.qoff = (int)c.q_offset;
   p.nqt = (int)ceil_div(a->seq_len, 32);
-  p.occ_w = (int)ceil_div(p.nqt, 32);
+  p.nkt = (int)ceil_div(c.seq_len_kv, 32);
+  p.occ_w = (int)ceil_div(p.nkt, 32);
   p.p = a->relu_power;
   p.inv_d = 1.0f / (float)a->head_dim;
   p.beta = a->beta;
@@ -221,11 +253,15 @@ int32_t tda_bwd(const tda_bwd_args* a, void* stream) {
     p.grad[k] = t.data;
     copy_strides(p.s[tda::B_DQ1 + k], t);
   }
+  const Common c = common_of(*a);
   p.B = (int)a->batch;
   p.H = (int)a->heads;
-  p.N = (int)a->seq_len;
+  p.Nq = (int)a->seq_len;
+  p.Nk = (int)c.seq_len_kv;
+  p.qoff = (int)c.q_offset;
   p.nqt = (int)ceil_div(a->seq_len, 32);
-  p.occ_w = (int)ceil_div(p.nqt, 32);
+  p.nkt = (int)ceil_div(c.seq_len_kv, 32);
+  p.occ_w = (int)ceil_div(p.nkt, 32);
   p.p = a->relu_power;
   p.inv_d = 1.0f / (float)a->head_dim;
   p.beta = a->beta;

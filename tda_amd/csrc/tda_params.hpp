@@ -10,16 +10,21 @@ namespace tda {
 enum FwdSlot { F_Q1 = 0, F_K1, F_Q2, F_K2, F_V, F_OUT, F_NSLOT };
 enum BwdSlot { B_Q1 = 0, B_K1, B_Q2, B_K2, B_V, B_DO, B_DQ1, B_DK1, B_DQ2, B_DK2, B_DV, B_NSLOT };
 
-// Row-norm table layout: [slot][B*H][N] with slot 0 = q1, 1 = k1, 2 = q2, 3 = k2.
+// Row-norm table: slots q1, k1, q2, k2 back to back, each [B*H][rows] with rows = Nq for the
+// query slots and Nk for the key slots (norm_base).
 enum NormSlot { N_Q1 = 0, N_K1 = 1, N_Q2 = 2, N_K2 = 3 };
+
+// Positions: query row i of a head sits at absolute position qoff + i and sees the keys
+// j <= qoff + i of the Nk key rows (qoff = 0 and Nq = Nk is the plain causal case).  Tiles are
+// 32 rows: nqt = ceil(Nq / 32) query tiles, nkt = ceil(Nk / 32) key tiles.
 
 struct FwdParams {
   const void* in[5];         // q1, k1, q2, k2, v
   void* out;
   int64_t s[F_NSLOT][3];     // batch, head, sequence strides in elements
-  int B, H, N;
-  int nqt;                   // ceil(N / 32): query tiles == key tiles
-  int occ_w;                 // bitmask words per query tile: ceil(nqt / 32)
+  int B, H, Nq, Nk, qoff;
+  int nqt, nkt;              // query tiles, key tiles
+  int occ_w;                 // bitmask words per query tile: ceil(nkt / 32)
   float p;                   // relu_power
   float inv_d;               // 1 / head_dim
   const float* beta;
@@ -33,8 +38,8 @@ struct BwdParams {
   const void* in[6];         // q1, k1, q2, k2, v, dout
   void* grad[5];             // dq1, dk1, dq2, dk2, dv
   int64_t s[B_NSLOT][3];
-  int B, H, N;
-  int nqt, occ_w;
+  int B, H, Nq, Nk, qoff;
+  int nqt, nkt, occ_w;
   float p, inv_d;
   const float* beta;
   const float* lam;

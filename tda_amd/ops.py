@@ -60,15 +60,27 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _check_inputs(tensors, names):
+def _check_inputs(tensors, names, kv_from: int | None = None):
+    """Every tensor 4-D with the first one's shape, dtype and device; with kv_from, tensors
+    from that index on (keys and values) may differ from it in the sequence length only."""
     ref = tensors[0]
+    if not isinstance(ref, torch.Tensor):
+        raise TypeError(f"{names[0]} must be a torch.Tensor")
     if ref.dim() != 4:
         raise ValueError(f"{names[0]} must have shape (batch, heads, seq_len, head_dim), got {tuple(ref.shape)}")
-    for t, n in zip(tensors, names):
+    kv_ref = tensors[kv_from] if kv_from is not None else None
+    for idx, (t, n) in enumerate(zip(tensors, names)):
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{n} must be a torch.Tensor")
-        if t.shape != ref.shape:
-            raise ValueError(f"shape mismatch: {names[0]} {tuple(ref.shape)} vs {n} {tuple(t.shape)}")
+        want = ref.shape
+        if kv_from is not None and idx >= kv_from:
+            if t.dim() != 4 or t.shape[:2] != ref.shape[:2] or t.shape[3] != ref.shape[3]:
+                raise ValueError(f"shape mismatch: {names[0]} {tuple(ref.shape)} vs {n} {tuple(t.shape)} "
+                                 "(keys and values may differ from the queries in seq_len only)")
+            want = kv_ref.shape
+        if t.shape != want:
+            raise ValueError(f"shape mismatch: {names[kv_from if kv_from is not None and idx >= kv_from else 0]} "
+                             f"{tuple(want)} vs {n} {tuple(t.shape)}")
         if t.dtype != ref.dtype:
             raise ValueError(f"dtype mismatch: {names[0]} {ref.dtype} vs {n} {t.dtype}")
         if t.device != ref.device:
@@ -79,8 +91,11 @@ def _check_inputs(tensors, names):
         raise ValueError(f"floating-point inputs required, got {ref.dtype}")
 
 
-def _common(args, t: torch.Tensor, branches: int, normalize: bool, relu_power: float):
+def _common(args, t: torch.Tensor, branches: int, normalize: bool, relu_power: float,
+            n_kv: int | None = None, q_offset: int = 0):
     b, h, n, d = t.shape
+    args.seq_len_kv = n if n_kv is None else n_kv
+    args.q_offset = q_offset
     args.abi_version = _abi.ABI_VERSION
     args.dtype = _NATIVE[t.dtype]
     args.branches = branches
@@ -91,29 +106,32 @@ def _common(args, t: torch.Tensor, branches: int, normalize: bool, relu_power: f
 
 
 def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, branches: int,
-            norms=None, occupancy=None, stats=None) -> torch.Tensor:
+            norms=None, occupancy=None, stats=None, q_offset: int = 0) -> torch.Tensor:
     """One forward launch.  Tensors must already be in a native dtype (float32 / bfloat16)
-    on one device; beta (and lam) are 0-dim float32 tensors on that device.  The optional
-    norms / occupancy / stats buffers receive the side outputs described in include/tda.h."""
+    on one device; beta (and lam) are 0-dim float32 tensors on that device.  q1 (q2) have Nq
+    rows at positions q_offset.., k1 (k2) and v have Nk rows.  The optional norms /
+    occupancy / stats buffers receive the side outputs described in include/tda.h."""
     lib = _abi.load()
     q1, k1, v = _usable(q1), _usable(k1), _usable(v)
     if branches == 2:
         q2, k2 = _usable(q2), _usable(k2)
     out = _empty_like_layout(q1)
     a = _abi.TdaFwdArgs()
-    _common(a, q1, branches, normalize, relu_power)
+    nk = k1.shape[2]
+    _common(a, q1, branches, normalize, relu_power, nk, q_offset)
     a.q1, a.k1, a.v, a.out = _tensor(q1), _tensor(k1), _tensor(v), _tensor(out)
     if branches == 2:
         a.q2, a.k2 = _tensor(q2), _tensor(k2)
     a.beta = _ptr(beta)
     a.lambda_param = _ptr(lam) if branches == 2 else None
     if normalize and norms is None:  # scratch: the kernels need the row norms either way
-        norms = torch.empty(lib.tda_norms_floats(*q1.shape[:3], branches), dtype=torch.float32, device=q1.device)
+        norms = torch.empty(lib.tda_norms_floats_kv(*q1.shape[:3], nk, branches), dtype=torch.float32,
+                            device=q1.device)
     if stats is not None and (stats.dtype != torch.int64 or stats.numel() < 3 or stats.device != q1.device):
         raise ValueError("stats must be an int64 tensor of at least 3 elements on the inputs' device")
     a.norms, a.occupancy, a.stats = _ptr(norms), _ptr(occupancy), _ptr(stats)
-    ws = torch.empty((lib.tda_fwd_workspace_bytes(*q1.shape[:3], branches) + 3) // 4, dtype=torch.float32,
-                     device=q1.device)
+    ws = torch.empty((lib.tda_fwd_workspace_bytes_kv(*q1.shape[:3], nk, branches) + 3) // 4,
+                     dtype=torch.float32, device=q1.device)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
     with torch.cuda.device(q1.device):
         _abi.check(lib.tda_fwd(ctypes.byref(a), _stream(q1.device)), "tda_fwd")
@@ -121,7 +139,7 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
 
 
 def backward(q1, k1, q2, k2, v, dout, beta, lam, relu_power: float, normalize: bool,
-             branches: int, norms=None, occupancy=None, stats=None):
+             branches: int, norms=None, occupancy=None, stats=None, q_offset: int = 0):
     """One backward launch: returns (dq1, dk1, dq2, dk2, dv, dbeta, dlambda); the branch-2
     entries and dlambda are None when branches == 1."""
     lib = _abi.load()
@@ -139,7 +157,7 @@ def backward(q1, k1, q2, k2, v, dout, beta, lam, relu_power: float, normalize: b
     ws_bytes = lib.tda_bwd_workspace_bytes(b, h, n, d)
     ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev)
     a = _abi.TdaBwdArgs()
-    _common(a, q1, branches, normalize, relu_power)
+    _common(a, q1, branches, normalize, relu_power, k1.shape[2], q_offset)
     a.q1, a.k1, a.v, a.dout = _tensor(q1), _tensor(k1), _tensor(v), _tensor(dout)
     a.dq1, a.dk1, a.dv = _tensor(dq1), _tensor(dk1), _tensor(dv)
     if branches == 2:
@@ -155,13 +173,14 @@ def backward(q1, k1, q2, k2, v, dout, beta, lam, relu_power: float, normalize: b
     return dq1, dk1, dq2, dk2, dv, dbeta, dlam
 
 
-def side_buffers(shape, branches: int, normalize: bool, device):
+def side_buffers(shape, branches: int, normalize: bool, device, n_kv: int | None = None):
     """Allocate the forward's norms and occupancy outputs (uninitialised: the forward writes
-    every element)."""
+    every element); shape is the queries' (B, H, Nq, d), n_kv the key rows (default Nq)."""
     lib = _abi.load()
     b, h, n, _ = shape
-    occ = torch.empty(lib.tda_occupancy_words(b, h, n, branches), dtype=torch.int32, device=device)
-    norms = (torch.empty(lib.tda_norms_floats(b, h, n, branches), dtype=torch.float32, device=device)
+    nk = n if n_kv is None else n_kv
+    occ = torch.empty(lib.tda_occupancy_words_kv(b, h, n, nk, branches), dtype=torch.int32, device=device)
+    norms = (torch.empty(lib.tda_norms_floats_kv(b, h, n, nk, branches), dtype=torch.float32, device=device)
              if normalize else None)
     return norms, occ
 
@@ -173,25 +192,27 @@ class TDAFunction(torch.autograd.Function):
     q2, k2, lam are None when branches == 1; beta / lam are 0-dim float32 device tensors."""
 
     @staticmethod
-    def forward(ctx, q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches):
+    def forward(ctx, q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches, q_offset=0):
         need = any(ctx.needs_input_grad[:7])
         norms = occ = None
         if need:
-            norms, occ = side_buffers(q1.shape, branches, normalize, q1.device)
-        out = forward(q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches, norms, occ)
+            norms, occ = side_buffers(q1.shape, branches, normalize, q1.device, k1.shape[2])
+        out = forward(q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches, norms, occ,
+                      q_offset=q_offset)
         ctx.save_for_backward(q1, k1, q2, k2, v, beta, lam, norms, occ)
-        ctx.cfg = (float(relu_power), bool(normalize), int(branches))
+        ctx.cfg = (float(relu_power), bool(normalize), int(branches), int(q_offset))
         return out
 
     @staticmethod
     def backward(ctx, dout):
         q1, k1, q2, k2, v, beta, lam, norms, occ = ctx.saved_tensors
-        relu_power, normalize, branches = ctx.cfg
+        relu_power, normalize, branches, q_offset = ctx.cfg
         dout = dout.to(q1.dtype)
         dq1, dk1, dq2, dk2, dv, dbeta, dlam = backward(
-            q1, k1, q2, k2, v, dout, beta, lam, relu_power, normalize, branches, norms, occ)
+            q1, k1, q2, k2, v, dout, beta, lam, relu_power, normalize, branches, norms, occ,
+            q_offset=q_offset)
         ng = ctx.needs_input_grad
         return (dq1 if ng[0] else None, dk1 if ng[1] else None,
                 dq2 if ng[2] else None, dk2 if ng[3] else None,
                 dv if ng[4] else None, dbeta if ng[5] else None,
-                dlam if (branches == 2 and ng[6]) else None, None, None, None)
+                dlam if (branches == 2 and ng[6]) else None, None, None, None, None)

@@ -142,6 +142,12 @@ def test_valid_args_pass():
     (lambda a: setattr(a, "workspace", None), _abi.ERR_WORKSPACE),
     (lambda a: setattr(a, "workspace_bytes", a.workspace_bytes - 4), _abi.ERR_WORKSPACE),
     (lambda a: setattr(a, "workspace", FAKE + 8), _abi.ERR_WORKSPACE),
+    (lambda a: setattr(a, "q_offset", -1), _abi.ERR_OFFSET),
+    (lambda a: setattr(a, "q_offset", (1 << 30) - 64), _abi.ERR_OFFSET),  # position past 2^30 - 64
+    (lambda a: setattr(a, "seq_len_kv", 1 << 30), _abi.ERR_OFFSET),
+    (lambda a: setattr(a, "seq_len_kv", -5), _abi.ERR_OFFSET),
+    # more key rows need a wider bitmask than the workspace holds
+    (lambda a: setattr(a, "seq_len_kv", 5000), _abi.ERR_WORKSPACE),
 ])
 def test_fwd_validator_rejects(mutate, code):
     lib = _lib()
@@ -149,6 +155,23 @@ def test_fwd_validator_rejects(mutate, code):
     mutate(a)
     assert lib.tda_validate_fwd(ctypes.byref(a)) == code
     assert lib.tda_fwd(ctypes.byref(a), None) == code  # rejected before any launch
+
+
+def test_offset_args_pass():
+    """seq_len_kv = 0 means Nk = Nq; a KV-cache shape with its workspace validates."""
+    lib = _lib()
+    a = _fwd_args()
+    a.seq_len_kv, a.q_offset = 0, 0
+    assert lib.tda_validate_fwd(ctypes.byref(a)) == _abi.OK
+    a.seq_len, a.seq_len_kv, a.q_offset = 1, 900, 899
+    a.workspace_bytes = lib.tda_fwd_workspace_bytes_kv(2, 3, 1, 900, 2)
+    assert lib.tda_validate_fwd(ctypes.byref(a)) == _abi.OK
+    b = _bwd_args()
+    b.seq_len, b.seq_len_kv, b.q_offset = 7, 300, 100
+    b.workspace_bytes = lib.tda_bwd_workspace_bytes(2, 3, 7, 128)
+    assert lib.tda_validate_bwd(ctypes.byref(b)) == _abi.OK
+    b.q_offset = -3
+    assert lib.tda_validate_bwd(ctypes.byref(b)) == _abi.ERR_OFFSET
 
 
 def test_single_branch_ignores_second_branch_pointers():
@@ -198,6 +221,14 @@ def test_buffer_sizes():
     assert lib.tda_occupancy_words(4, 16, 4096, 1) == 64 * 128 * 4
     assert lib.tda_occupancy_words(1, 1, 1, 1) == 1
     assert lib.tda_occupancy_words(1, 1, 33, 2) == 4
+    # rectangular: query tiles x ceil(key tiles / 32) words per row
+    assert lib.tda_occupancy_words_kv(1, 1, 33, 100, 2) == 2 * 2 * 1
+    assert lib.tda_occupancy_words_kv(1, 1, 1, 5000, 1) == 1 * ((5000 + 31) // 32 + 31) // 32
+    assert lib.tda_occupancy_words_kv(2, 3, 64, 64, 2) == lib.tda_occupancy_words(2, 3, 64, 2)
+    assert lib.tda_norms_floats_kv(2, 3, 10, 20, 2) == 2 * 6 * 30
+    assert lib.tda_norms_floats_kv(2, 3, 10, 10, 1) == lib.tda_norms_floats(2, 3, 10, 1)
+    assert lib.tda_fwd_workspace_bytes_kv(1, 1, 1, 5000, 1) == 256
+    assert lib.tda_occupancy_words_kv(1, 1, 33, 0, 2) == 0
     assert lib.tda_occupancy_words(1, 1, 33, 3) == 0
     assert lib.tda_norms_floats(4, 16, 4096, 2) == 4 * 64 * 4096
     assert lib.tda_norms_floats(1, 8, 128, 1) == 2 * 8 * 128
