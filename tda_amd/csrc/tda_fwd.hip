@@ -261,9 +261,11 @@ static int sel_d(const FwdParams& p, const KernelKey& k, void* s) {
   return k.d == 128 ? sel_br<Pol, 128>(p, k, s) : sel_br<Pol, 64>(p, k, s);
 }
 
-// bf16 runs the screen + sparse A.V kernels (tda_fwd_sparse.hip); fp32 runs fwd_wave.
+// bf16 runs the screen + sparse A.V kernels (tda_fwd_sparse.hip), or with a single query tile
+// the split-key decode kernels (tda_fwd_decode.hip); fp32 runs fwd_wave.
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream) {
-  return k.dtype == 1 ? launch_fwd_sparse(p, k, stream) : sel_d<PolF32>(p, k, stream);
+  if (k.dtype == 1) return p.nqt == 1 && p.part ? launch_fwd_decode(p, k, p.part, stream) : launch_fwd_sparse(p, k, stream);
+  return sel_d<PolF32>(p, k, stream);
 }
 
 }  // namespace tda

@@ -32,6 +32,7 @@ struct FwdParams {
   float* norms;              // may be null
   uint32_t* occ;             // may be null (bf16: never, the host points it at workspace)
   unsigned long long* stats; // may be null
+  float* part;               // bf16 with one query tile: per-chunk partial outputs (workspace)
 };
 
 struct BwdParams {
@@ -62,6 +63,7 @@ struct KernelKey {
 
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_fwd_sparse(const FwdParams& p, const KernelKey& k, void* stream);
+int launch_fwd_decode(const FwdParams& p, const KernelKey& k, float* part, void* stream);
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_finish(const BwdParams& p, int branches, void* stream);

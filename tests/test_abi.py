@@ -227,7 +227,9 @@ def test_buffer_sizes():
     assert lib.tda_occupancy_words_kv(2, 3, 64, 64, 2) == lib.tda_occupancy_words(2, 3, 64, 2)
     assert lib.tda_norms_floats_kv(2, 3, 10, 20, 2) == 2 * 6 * 30
     assert lib.tda_norms_floats_kv(2, 3, 10, 10, 1) == lib.tda_norms_floats(2, 3, 10, 1)
-    assert lib.tda_fwd_workspace_bytes_kv(1, 1, 1, 5000, 1) == 256
+    # one query tile: + the decode partials, [B*H][ceil(key tiles / 32)][Nq][128] floats
+    assert lib.tda_fwd_workspace_bytes_kv(1, 1, 1, 5000, 1) == 256 + 5 * 1 * 128 * 4
+    assert lib.tda_fwd_workspace_bytes_kv(1, 1, 33, 5000, 1) == 256 * ((2 * 5 * 4 + 255) // 256)
     assert lib.tda_occupancy_words_kv(1, 1, 33, 0, 2) == 0
     assert lib.tda_occupancy_words(1, 1, 33, 3) == 0
     assert lib.tda_norms_floats(4, 16, 4096, 2) == 4 * 64 * 4096
