@@ -103,7 +103,8 @@ def side_configs(steps: int, warmup: int):
     """The BASELINE "report" configurations, timed like the headline forward (HIP events on
     the launch stream around `steps` calls after `warmup`): configs[1] (TRA, bf16,
     (4,16,2048,64), seed 1, beta 1, p 2, normalize) and configs[4] (TDA, bf16, (1,32,16384,128),
-    seed 4, beta 2, lambda 0.3, normalize) at p = 1 and p = 1.5, with the kernels' tile counters."""
+    seed 4, beta 2, lambda 0.3, normalize) at p = 1 and p = 1.5, with the kernels' tile counters;
+    plus a KV-cache decode step (one query against 16384 keys)."""
     import torch
 
     from tda_amd import ops
@@ -156,6 +157,23 @@ def side_configs(steps: int, warmup: int):
             "ms": ms, "tflops": units(shape4, 3.0) / (ms * 1e-3) / 1e12,
             "pct_peak": 100.0 * units(shape4, 3.0) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, "counted_units": 3.0,
             **tiles(lambda st: ops.forward(q1, k1, q2, k2, v, beta, lam, p, True, 2, stats=st))}
+    # KV-cache decode (no BASELINE config; the position-offset extension): one query at the last
+    # position of a 16384-key cache.  HBM-bound: the keys of both branches are read once, V
+    # only for non-zero tiles; roofline = key bytes / time against 8 TB/s.
+    B, H, NK, D = 4, 16, 16384, 128
+    g = torch.Generator("cpu").manual_seed(5)
+    qd1, qd2 = (torch.randn(B, H, 1, D, generator=g).to(torch.bfloat16).to(dev) for _ in range(2))
+    del q1, q2, k1, k2, v, xs
+    kd1, kd2, vd = (torch.randn(B, H, NK, D, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+    beta, lam = torch.tensor(1.0, device=dev), torch.tensor(0.5, device=dev)
+    ms = timed(lambda: ops.forward(qd1, kd1, qd2, kd2, vd, beta, lam, 2.0, True, 2, q_offset=NK - 1))
+    kbytes = 2 * B * H * NK * D * 2
+    res["decode"] = {"workload": f"TDA fwd bf16, one query at position {NK - 1} against ({B},{H},{NK},{D}) keys, "
+                                 "beta=1, lambda=0.5, p=2, normalize (seed 5)",
+                     "ms": ms, "bound": "hbm", "key_bytes": kbytes, "achieved_gbs": kbytes / (ms * 1e-3) / 1e9,
+                     "frac_of_8tbs": kbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                     **tiles(lambda st: ops.forward(qd1, kd1, qd2, kd2, vd, beta, lam, 2.0, True, 2, stats=st,
+                                                    q_offset=NK - 1))}
     return res
 
 
