@@ -113,7 +113,9 @@ typedef struct tda_fwd_args {
                                were evaluated (bf16: the tiles the screen kept, a superset
                                of [1]; f32 leaves [2] alone); tiles are 32x32 */
   void*  workspace;         /* device scratch of tda_fwd_workspace_bytes_kv() bytes,
-                               16-byte aligned: holds the tile bitmask when occupancy is NULL */
+                               16-byte aligned: holds the tile bitmask when occupancy is NULL
+                               and, when seq_len <= 32, the fp32 per-chunk partial outputs of
+                               the single-query-tile (decode) kernels */
   size_t workspace_bytes;
   int64_t seq_len_kv;       /* Nk, the key/value rows; 0 means Nk = seq_len */
   int64_t q_offset;         /* position of query row 0 (>= 0); 0 with Nk = Nq is the
