@@ -298,13 +298,19 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
       __builtin_amdgcn_sched_barrier(0);  // keep the chains apart
     }
     const uint32_t bit = 1u << (kt & 31);
+    // Both tests run on every path, masked by selects: the MFMA results are read only in
+    // straight-line code after the chains, where the compiler counts the wait states the
+    // hardware needs between an MFMA writing a register and a VALU reading it.  (With a branch
+    // skipping the first test, the compiler placed the second test's reads too early on the
+    // branch path: 7 wait states where 12 are needed, so the test could read scores that were
+    // not yet written.)
 #pragma unroll
     for (int s = 0; s < QPW; ++s) {
-      if (kt > ktl[s]) continue;  // key tiles after the query tile's last position hold no causal pair
       bool hit;
       if constexpr (NORM) hit = maximum16(S[s]) * rk > tau[s];  // largest score of the lane's key
       else hit = valid[s] && max16(S[s]) > tau[s];          // largest score of the lane's query
-      hb[s] |= hit ? bit : 0u;
+      // key tiles after the query tile's last position hold no causal pair
+      hb[s] |= hit && kt <= ktl[s] ? bit : 0u;
     }
   };
   // bitmask words of this wave's rows: word kt/32 is complete after key tile kt
