@@ -55,7 +55,7 @@
 extern "C" {
 #endif
 
-#define TDA_ABI_VERSION 4
+#define TDA_ABI_VERSION 5
 
 /* element types of q, k, v, out and gradients */
 #define TDA_DTYPE_F32  0
@@ -120,6 +120,11 @@ typedef struct tda_fwd_args {
   int64_t seq_len_kv;       /* Nk, the key/value rows; 0 means Nk = seq_len */
   int64_t q_offset;         /* position of query row 0 (>= 0); 0 with Nk = Nq is the
                                reference's causal case, Nk - Nq the KV-cache alignment */
+  uint32_t* pairs;          /* optional output (may be NULL), tda_pair_words() words, 16-byte
+                               aligned: for each (branch, head, query tile) the list of its
+                               non-zero weights (key index, row, exact threshold margin), which
+                               lets the backward read only the rows they name; bf16 only (the
+                               f32 forward leaves it alone) */
 } tda_fwd_args;
 
 typedef struct tda_bwd_args {
@@ -144,6 +149,8 @@ typedef struct tda_bwd_args {
   unsigned long long* stats;/* optional: [0] += tiles visited, [1] += tiles computed */
   int64_t seq_len_kv;       /* as in tda_fwd_args (dq, dout: Nq rows; dk, dv: Nk rows) */
   int64_t q_offset;
+  const uint32_t* pairs;    /* the forward's pair lists, or NULL; used only with occupancy
+                               (bf16): lists that did not fit fall back to the bitmask tiles */
 } tda_bwd_args;
 
 int32_t     tda_abi_version(void);
@@ -167,6 +174,8 @@ size_t tda_norms_floats_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_
 size_t tda_fwd_workspace_bytes_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv,
                                   int32_t branches);
 size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim);
+/* Words of the pair-list output (queries seq_len; no dependence on the key rows). */
+size_t tda_pair_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 
 /* Enqueue the forward / backward pass on `stream` (a hipStream_t). */
 int32_t tda_fwd(const tda_fwd_args* args, void* stream);

@@ -13,7 +13,7 @@ import threading
 HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(HERE, "libtda_hip.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
@@ -59,6 +59,7 @@ class TdaFwdArgs(ctypes.Structure):
         ("norms", ctypes.c_void_p), ("occupancy", ctypes.c_void_p), ("stats", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("seq_len_kv", ctypes.c_int64), ("q_offset", ctypes.c_int64),
+        ("pairs", ctypes.c_void_p),
     ]
 
 
@@ -74,6 +75,7 @@ class TdaBwdArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("stats", ctypes.c_void_p),
         ("seq_len_kv", ctypes.c_int64), ("q_offset", ctypes.c_int64),
+        ("pairs", ctypes.c_void_p),
     ]
 
 
@@ -91,6 +93,7 @@ SIGNATURES = {
     "tda_norms_floats_kv": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int32]),
     "tda_fwd_workspace_bytes_kv": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int32]),
     "tda_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4),
+    "tda_pair_words": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
     "tda_fwd": (ctypes.c_int32, [ctypes.POINTER(TdaFwdArgs), ctypes.c_void_p]),
     "tda_bwd": (ctypes.c_int32, [ctypes.POINTER(TdaBwdArgs), ctypes.c_void_p]),
 }

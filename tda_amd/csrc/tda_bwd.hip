@@ -476,7 +476,7 @@ static int launch_bwd_t(const BwdParams& p, void* stream) {
   hipLaunchKernelGGL((bwd_dq<Pol, D, BR, PK, NORM>), dim3((unsigned)((qitems + 3) / 4)), dim3(256), 0, s, p);
   hipLaunchKernelGGL((bwd_dkv<Pol, D, BR, PK, NORM>), dim3((unsigned)((kitems + 3) / 4)), dim3(256), 0, s, p);
   const int e = (int)hipGetLastError();
-  return e ? e : launch_bwd_finish(p, BR, stream);
+  return e ? e : launch_bwd_finish(p, BR, (int64_t)p.B * p.H * p.nqt, stream);
 }
 
 template <class Pol, int D, int BR, int PK>
@@ -500,8 +500,7 @@ static int bsel_d(const BwdParams& p, const KernelKey& k, void* s) {
   return k.d == 128 ? bsel_br<Pol, 128>(p, k, s) : bsel_br<Pol, 64>(p, k, s);
 }
 
-int launch_bwd_finish(const BwdParams& p, int branches, void* stream) {
-  const int64_t items = (int64_t)p.B * p.H * p.nqt;
+int launch_bwd_finish(const BwdParams& p, int branches, int64_t items, void* stream) {
   hipLaunchKernelGGL(bwd_finish, dim3(1), dim3(kFinThreads), 0, (hipStream_t)stream, (const float*)p.ws, items, p.lam,
                      p.dbeta, p.dlam, branches);
   return (int)hipGetLastError();

@@ -26,6 +26,7 @@ namespace tda {
 
 #define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte chunk swizzle of a row-major 32-row tile (D/8 chunks per row).  Conflict-free for the
 // row-fragment reads (32 rows, one chunk each) and for the transpose reads (4 rows x 2 chunks
@@ -57,6 +58,66 @@ __device__ __forceinline__ void dma_row_vals(const float* vals, int r0, int n, f
   if (l < 32) __builtin_amdgcn_global_load_lds((const void*)(vals + min(r0 + l, n - 1)), LDS_PTR(void, dst), 4, 0, 0);
 }
 __device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0); }
+
+// The same loads through a buffer descriptor per tile: the tile sets the descriptor's base and
+// size, the lanes add 32-bit offsets within the tile; rows past n read as zeros (the
+// descriptor's range check).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+template <int D>
+__device__ __forceinline__ void dma_tile_b(const bf16* rows, int64_t st, int r0, int n, bf16* tile) {
+  constexpr int CH = D / 8, RPI = 64 / CH;
+  const int l = lane_id();
+  const int nr = min(32, n - r0);
+  const __amdgpu_buffer_rsrc_t rs = rows_rsrc(rows + (int64_t)r0 * st, (uint32_t)(((int64_t)(nr - 1) * st + D) * 2));
+  const uint32_t st2 = (uint32_t)(2 * st);  // row stride in bytes (at most 2^26)
+#pragma unroll
+  for (int u = 0; u < 32 / RPI; ++u) {
+    const int r = u * RPI + l / CH;
+    const uint32_t off = (uint32_t)r * st2 + 16u * (uint32_t)((l % CH) ^ bswz<D>(r));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(void, tile + u * RPI * D), 16, off, 0, 0, 0);
+  }
+}
+// One row j of a (n, D) row set into row j % 32 of a swizzled tile (D/8 lanes, 16 bytes each).
+template <int D>
+__device__ __forceinline__ void dma_row(const bf16* rows, int64_t st, int j, bf16* tile) {
+  constexpr int CH = D / 8;
+  const int l = lane_id(), jl = j & 31;
+  const __amdgpu_buffer_rsrc_t rs = rows_rsrc(rows + (int64_t)j * st, (uint32_t)(D * 2));
+  if (l < CH)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(void, tile + jl * D), 16, 16u * (uint32_t)(l ^ bswz<D>(jl)), 0,
+                                             0, 0);
+}
+// Zero a 32 x D tile (the pair paths load only the rows their pairs name; the other rows meet
+// zero weights, and must hold finite values).
+template <int D>
+__device__ __forceinline__ void zero_tile(bf16* tile) {
+  const int l = lane_id();
+#pragma unroll
+  for (int u = 0; u < 32 * D / 8 / 64; ++u) *reinterpret_cast<u32x4*>(tile + 8 * (64 * u + l)) = u32x4{0u, 0u, 0u, 0u};
+}
+// Value index r of the 32x32 C layout holding tile row `row` for lane group g = (row >> 2) & 1.
+__device__ __forceinline__ int crow_index(int row) { return 4 * (row >> 3) + (row & 3); }
+// Lane-distributed pair list: lane e < n holds entry e (key, query row in the tile, x).
+struct PairLanes {
+  int key, row;
+  float x;
+};
+__device__ __forceinline__ PairLanes load_pairs(const uint32_t* ent, uint32_t n) {
+  const int l = lane_id();
+  u32x4 e = u32x4{0u, 0u, 0u, 0u};
+  if ((uint32_t)l < n) e = *reinterpret_cast<const u32x4*>(ent + 4 * l);
+  // x through a bit cast of the whole vector: hipcc compiled __builtin_bit_cast(float, e[2])
+  // to element 0 (the key index)
+  const f32x4 ef = __builtin_bit_cast(f32x4, e);
+  return PairLanes{(int)e[0], (int)e[1], ef[2]};
+}
+
+__device__ __forceinline__ void dma_row_vals_b(const float* vals, int r0, int n, float* dst) {
+  const __amdgpu_buffer_rsrc_t rs = rows_rsrc(vals + r0, (uint32_t)(min(32, n - r0) * 4));
+  if (lane_id() < 32) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(void, dst), 4, 4 * lane_id(), 0, 0, 0);
+}
 
 // Row fragment t of a swizzled tile: lane (m, g) gets elements 16t + 8g .. +7 of row m.
 template <int D>
@@ -160,8 +221,10 @@ struct BwdWaveLds {
 constexpr int kBwdWaves = 1;
 
 // ------------------------------------------------------------------ query-major pass
+// One wave per (branch, query tile): a branch's resident operands (its query fragments, dO,
+// one dq accumulator) are half of both branches', which lets two waves share a SIMD.
 template <int D, int BR, int PK, bool NORM>
-__global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
+__global__ void __launch_bounds__(64 * kBwdWaves) __attribute__((amdgpu_waves_per_eu(2))) bwd_dq_fast(BwdParams P) {
   constexpr int NT = D / 16, ND = D / 32;
   __shared__ __attribute__((aligned(16))) BwdWaveLds<D> lds_all[kBwdWaves];
 
@@ -169,10 +232,13 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   BwdWaveLds<D>& W = lds_all[wv];
   const int BH = P.B * P.H;
-  const int64_t item = (int64_t)blockIdx.x * kBwdWaves + wv;
-  if (item >= (int64_t)BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
-  const int qt = P.nqt - 1 - (int)(item / BH);
-  const int bh = (int)(item % BH);
+  const int64_t item = (int64_t)blockIdx.x * kBwdWaves + wv;  // (query tile, head, branch)
+  if (item >= (int64_t)BR * BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
+  // longest first (query tiles from the last); the two branches of a (head, query tile) adjacent
+  const int br = BR == 2 ? (int)(item & 1) : 0;
+  const int64_t rest = BR == 2 ? item >> 1 : item;
+  const int qt = P.nqt - 1 - (int)(rest / BH);
+  const int bh = (int)(rest % BH);
   const int b = bh / P.H, h = bh % P.H;
   const int Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
   const int i = qt * 32 + n32;
@@ -183,111 +249,164 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dq_fast(BwdParams P) {
   auto base = [&](int slot) {
     return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
   };
+  const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
 
-  bf16x8 DO[NT];
+  // row operands, all issued before the first wait: dO and query fragments, the inverse query
+  // norm, bitmask words 0..63 of the branch's row (lane w holds word w)
+  const int nw = (ktl >> 5) + 1;  // bitmask words covering key tiles 0..ktl
+  // the forward's pair list of (branch, head, query tile), when it fit (else the tile path)
+  const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
+  const uint32_t npairs = P.pairs ? P.pairs[pair_lists(BR, BH, P.nqt) * 4 * kPairCap + lidx] : kPairOverflow;
+  const bool pair_path = npairs <= (uint32_t)kPairCap;
+  PairLanes PL{0, 0, 0.f};
+  bool row_used = !pair_path;  // the lane's query row meets a non-zero weight (pair path: some pair names it)
+  if (pair_path) {
+    PL = load_pairs(P.pairs + lidx * (4 * kPairCap), npairs);
+    for (uint32_t e = 0; e < npairs; ++e) row_used |= __builtin_amdgcn_readlane(PL.row, (int)e) == n32;
+  }
+  bf16x8 DO[NT], Q[NT];
   {
+    // dO rows only where a pair needs them (the pair path's dP is read at pair positions only)
     const bf16* r = base(B_DO) + (int64_t)ic * P.s[B_DO][2];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) DO[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+    for (int t = 0; t < NT; ++t) DO[t] = row_used ? *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g) : bf16x8{};
+    if (!pair_path) {  // the tile path recomputes the scores
+      const bf16* rq_ = base(qslot) + (int64_t)ic * P.s[qslot][2];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Q[t] = *reinterpret_cast<const bf16x8*>(rq_ + 16 * t + 8 * g);
+    }
   }
+  const float rq = NORM ? P.norms[norm_base(P, br == 0 ? N_Q1 : N_Q2, bh) + ic] : 1.f;
+  const uint32_t* occrow = P.occ ? P.occ + (((int64_t)br * BH + bh) * P.nqt + qt) * P.occ_w : nullptr;
+  const uint32_t lw0 = l < nw ? (occrow ? occrow[l] : 0xffffffffu) : 0u;
   const float ci = tau_coeff(pq, P.inv_d);
   const float tau = (*P.beta) * ci;
   const float pw = P.p;
-  float lam = 0.f;
-  if constexpr (BR == 2) lam = clamp01(*P.lam);
+  float coef = 1.f;
+  if constexpr (BR == 2) coef = br == 0 ? 1.f : -clamp01(*P.lam);
+  const bool want_l = BR == 2 && br == 1;  // dlambda comes from branch 2 alone
   const bf16* vb = base(B_V);
   const int64_t sv = P.s[B_V][2];
+  const bf16* kb = base(kslot);
+  const int64_t sk = P.s[kslot][2];
+  const float* nk = nullptr;
+  if constexpr (NORM) nk = P.norms + norm_base(P, br == 0 ? N_K1 : N_K2, bh);
   float bsum = 0.f, lsum = 0.f;
   unsigned visited = 0, computed = 0;
-  const int nw = (ktl >> 5) + 1;  // bitmask words covering key tiles 0..ktl
 
-  // Both branches' row operands, issued with dO so that one memory round trip covers them:
-  // query fragments, inverse query norms, bitmask words 0..63 (lane w holds word w).
-  bf16x8 QB[BR][NT];
-  float RQ[BR];
-  uint32_t LW[BR];
+  f32x16 A[ND];
 #pragma unroll
-  for (int br = 0; br < BR; ++br) {
-    const int qslot = br == 0 ? B_Q1 : B_Q2;
-    const bf16* r = base(qslot) + (int64_t)ic * P.s[qslot][2];
+  for (int c = 0; c < ND; ++c) A[c] = f32x16{};
+
+  if (pair_path) {
+    // Pairs of one key tile are consecutive in the list.  Per key tile: the key and value rows
+    // the pairs name (into the zeroed tiles), dP = dO V^T on the matrix cores, dS at the pair
+    // positions from the forward's x, then dq += dS K.
+    zero_tile<D>(W.a);
+    __builtin_amdgcn_s_waitcnt(0);
+    uint32_t e0 = 0;
+    while (e0 < npairs) {
+      const int kt = __builtin_amdgcn_readlane(PL.key, (int)e0) >> 5;
+      const uint64_t grp = wave_ballot((uint32_t)l >= e0 && (uint32_t)l < npairs && (PL.key >> 5) == kt);
+      const uint32_t e1 = e0 + (uint32_t)__builtin_popcountll(grp);
+      ++visited;
+      ++computed;
+      for (uint32_t e = e0; e < e1; ++e) {
+        const int j = __builtin_amdgcn_readlane(PL.key, (int)e);
+        dma_row<D>(kb, sk, j, W.a);
+        dma_row<D>(vb, sv, j, W.b);
+      }
+      wait_all_loads();
+      f32x16 Dp = f32x16{};
 #pragma unroll
-    for (int t = 0; t < NT; ++t) QB[br][t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
-    RQ[br] = NORM ? P.norms[norm_base(P, br == 0 ? N_Q1 : N_Q2, bh) + ic] : 1.f;
-    const uint32_t* occrow = P.occ ? P.occ + (((int64_t)br * BH + bh) * P.nqt + qt) * P.occ_w : nullptr;
-    LW[br] = l < nw ? (occrow ? occrow[l] : 0xffffffffu) : 0u;
+      for (int t = 0; t < NT; ++t) Dp = PolBF16::mma(tile_row_frag<D>(W.b, t), DO[t], Dp);
+      f32x16 E = f32x16{};
+      for (uint32_t e = e0; e < e1; ++e) {
+        const int j = __builtin_amdgcn_readlane(PL.key, (int)e), jl = j & 31;
+        const int il = __builtin_amdgcn_readlane(PL.row, (int)e);
+        const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, PL.x), (int)e));
+        const float rk = NORM ? nk[j] : 1.f;
+        const int rr = crow_index(jl);
+        const bool mine = n32 == il && g == ((jl >> 2) & 1);  // the lane holding (query il, key jl)
+        float dp = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dp = r == rr ? Dp[r] : dp;
+        const float ds = coef * dpow_p<PK>(x, pw) * dp;
+        bsum += mine ? ds : 0.f;
+        lsum = __builtin_fmaf(mine && want_l ? pow_p<PK>(x, pw) : 0.f, dp, lsum);
+        const float ev = NORM ? ds * rk : ds;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) E[r] = mine && r == rr ? ev : E[r];
+      }
+      const bf16x8 E0 = PolBF16::pack_c(E, 0), E1 = PolBF16::pack_c(E, 1);
+#pragma unroll
+      for (int c = 0; c < ND; ++c) {
+        A[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 0, c), E0, A[c]);
+        A[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 1, c), E1, A[c]);
+      }
+      e0 = e1;
+    }
   }
 
+  for (int w0 = 0; w0 < (pair_path ? 0 : nw); w0 += 64) {
+    const uint32_t lw = w0 == 0 ? lw0 : (w0 + l < nw) ? (occrow ? occrow[w0 + l] : 0xffffffffu) : 0u;
+    for (int w = w0; w < min(nw, w0 + 64); ++w) {
+      uint32_t bits = __builtin_amdgcn_readlane(lw, w - w0);
+      if (w == (ktl >> 5)) bits &= (ktl & 31) == 31 ? 0xffffffffu : ((2u << (ktl & 31)) - 1u);
+      while (bits) {
+        const int kt = 32 * w + __builtin_ctz(bits);
+        bits &= bits - 1u;
+        ++visited;
+        const int k0 = 32 * kt;
+        dma_tile_b<D>(kb, sk, k0, Nk, W.a);
+        dma_tile_b<D>(vb, sv, k0, Nk, W.b);
+        if constexpr (NORM) dma_row_vals_b(nk, k0, Nk, W.rows);
+        wait_all_loads();
+        f32x16 S = f32x16{}, Dp = f32x16{};
 #pragma unroll
-  for (int br = 0; br < BR; ++br) {
-    const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
-    const bf16* kb = base(kslot);
-    const int64_t sk = P.s[kslot][2];
-    const bf16x8 (&Q)[NT] = QB[br];
-    GradRow<D> XR;  // the query row for the normalize backward, in flight during the tiles
-    if constexpr (NORM) load_grad_row<D>(base(qslot) + (int64_t)ic * P.s[qslot][2], XR);
-    const float rq = RQ[br];
-    const float* nk = nullptr;
-    if constexpr (NORM) nk = P.norms + norm_base(P, br == 0 ? N_K1 : N_K2, bh);
-    const float coef = br == 0 ? 1.f : -lam;
-    f32x16 A[ND];
+        for (int t = 0; t < NT; ++t) {
+          S = PolBF16::mma(tile_row_frag<D>(W.a, t), Q[t], S);
+          Dp = PolBF16::mma(tile_row_frag<D>(W.b, t), DO[t], Dp);
+        }
+        float rk[16];
+        if constexpr (NORM) crow_vals(W.rows, rk);
+        f32x16 E;
+        bool any = false;
 #pragma unroll
-    for (int c = 0; c < ND; ++c) A[c] = f32x16{};
-    const uint32_t* occrow = P.occ ? P.occ + (((int64_t)br * BH + bh) * P.nqt + qt) * P.occ_w : nullptr;
-
-    for (int w0 = 0; w0 < nw; w0 += 64) {
-      const uint32_t lw = w0 == 0 ? LW[br] : (w0 + l < nw) ? (occrow ? occrow[w0 + l] : 0xffffffffu) : 0u;
-      for (int w = w0; w < min(nw, w0 + 64); ++w) {
-        uint32_t bits = __builtin_amdgcn_readlane(lw, w - w0);
-        if (w == (ktl >> 5)) bits &= (ktl & 31) == 31 ? 0xffffffffu : ((2u << (ktl & 31)) - 1u);
-        while (bits) {
-          const int kt = 32 * w + __builtin_ctz(bits);
-          bits &= bits - 1u;
-          ++visited;
-          const int k0 = 32 * kt;
-          dma_tile<D>(kb, sk, k0, Nk, W.a);
-          dma_tile<D>(vb, sv, k0, Nk, W.b);
-          if constexpr (NORM) dma_row_vals(nk, k0, Nk, W.rows);
-          wait_all_loads();
-          f32x16 S = f32x16{}, Dp = f32x16{};
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + crow(r, g);
+          const bool valid = qvalid && key <= pq && key < Nk;  // rows past Nk read as zeros
+          const float sr = NORM ? S[r] * rk[r] : S[r];
+          const float x = __builtin_fmaf(sr, rq, -tau);
+          const bool pos = valid && x > 0.f;
+          const float ds = pos ? coef * dpow_p<PK>(x, pw) * Dp[r] : 0.f;
+          bsum += ds;
+          lsum = __builtin_fmaf(pos && want_l ? pow_p<PK>(x, pw) : 0.f, Dp[r], lsum);
+          any = any || pos;
+          E[r] = NORM ? ds * rk[r] : ds;
+        }
+        if (!occrow && wave_ballot(any) == 0ull) continue;
+        ++computed;
+        const bf16x8 E0 = PolBF16::pack_c(E, 0), E1 = PolBF16::pack_c(E, 1);
 #pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            S = PolBF16::mma(tile_row_frag<D>(W.a, t), Q[t], S);
-            Dp = PolBF16::mma(tile_row_frag<D>(W.b, t), DO[t], Dp);
-          }
-          float rk[16];
-          if constexpr (NORM) crow_vals(W.rows, rk);
-          f32x16 E;
-          bool any = false;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + crow(r, g);
-            const bool valid = qvalid && key <= pq && key < Nk;  // rows past Nk are copies
-            const float sr = NORM ? S[r] * rk[r] : S[r];
-            const float x = __builtin_fmaf(sr, rq, -tau);
-            const bool pos = valid && x > 0.f;
-            const float ds = pos ? coef * dpow_p<PK>(x, pw) * Dp[r] : 0.f;
-            bsum += ds;
-            if (br == 1) lsum = __builtin_fmaf(pos ? pow_p<PK>(x, pw) : 0.f, Dp[r], lsum);
-            any = any || pos;
-            E[r] = NORM ? ds * rk[r] : ds;
-          }
-          if (!occrow && wave_ballot(any) == 0ull) continue;
-          ++computed;
-          const bf16x8 E0 = PolBF16::pack_c(E, 0), E1 = PolBF16::pack_c(E, 1);
-#pragma unroll
-          for (int c = 0; c < ND; ++c) {
-            A[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 0, c), E0, A[c]);
-            A[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 1, c), E1, A[c]);
-          }
+        for (int c = 0; c < ND; ++c) {
+          A[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 0, c), E0, A[c]);
+          A[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 1, c), E1, A[c]);
         }
       }
     }
-    if (qvalid) {
-      const int gslot = br == 0 ? B_DQ1 : B_DQ2;
-      bf16* grow = (bf16*)P.grad[br == 0 ? 0 : 2] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
-                   (int64_t)i * P.s[gslot][2];
-      store_grad_rows<D, NORM>(A, XR, grow, rq);
-    }
+  }
+  if (qvalid) {
+    // the query row for the normalize backward, loaded after the tiles (held during them, it
+    // would push the wave past the register budget of two waves per SIMD); rows no weight
+    // meets have a zero gradient, and zeros for their input row keep it zero
+    GradRow<D> XR = {};
+    if constexpr (NORM)
+      if (row_used) load_grad_row<D>(base(qslot) + (int64_t)ic * P.s[qslot][2], XR);
+    const int gslot = br == 0 ? B_DQ1 : B_DQ2;
+    bf16* grow = (bf16*)P.grad[br == 0 ? 0 : 2] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
+                 (int64_t)i * P.s[gslot][2];
+    store_grad_rows<D, NORM>(A, XR, grow, rq);
   }
 
   const float pb = wave_sum(-ci * bsum);
@@ -342,19 +461,19 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
 #pragma unroll
   for (int c = 0; c < ND; ++c) AV[c] = f32x16{};
   unsigned visited = 0, computed = 0;
+  if (P.pairs) {  // the pair path loads single rows: the others must be finite
+    zero_tile<D>(W.a);
+    zero_tile<D>(W.b);
+    __builtin_amdgcn_s_waitcnt(0);
+  }
 
-  // Both branches' row operands, issued with V so that one memory round trip covers them: key
-  // fragments, inverse key norms, and the bitmask column bits of query tiles qtf .. qtf+63
-  // (lane q holds tile qtf + q).
-  bf16x8 KB[BR][NT];
+  // Both branches' row operands, issued with V so that one memory round trip covers them:
+  // inverse key norms, and the bitmask column bits of query tiles qtf .. qtf+63 (lane q holds
+  // tile qtf + q).  The key fragments are loaded by the tile path, which alone needs them.
   float RK[BR];
   bool HAS[BR];
 #pragma unroll
   for (int br = 0; br < BR; ++br) {
-    const int kslot = br == 0 ? B_K1 : B_K2;
-    const bf16* r = base(kslot) + (int64_t)jc * P.s[kslot][2];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) KB[br][t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
     RK[br] = NORM ? P.norms[norm_base(P, br == 0 ? N_K1 : N_K2, bh) + jc] : 1.f;
     const uint32_t* occcol = P.occ ? P.occ + ((int64_t)br * BH + bh) * P.nqt * P.occ_w + (kt >> 5) : nullptr;
     const int qtl = qtf + l;
@@ -366,9 +485,8 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
     const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
     const bf16* qb = base(qslot);
     const int64_t sq = P.s[qslot][2];
-    const bf16x8 (&K)[NT] = KB[br];
-    GradRow<D> XR;  // the key row for the normalize backward, in flight during the tiles
-    if constexpr (NORM) load_grad_row<D>(base(kslot) + (int64_t)jc * P.s[kslot][2], XR);
+    const bf16* krow = base(kslot) + (int64_t)jc * P.s[kslot][2];
+    bool row_used = false;  // the lane's key row met a non-zero weight (or the tile path ran)
     const float rk = RK[br];
     const float* nq = nullptr;
     if constexpr (NORM) nq = P.norms + norm_base(P, br == 0 ? N_Q1 : N_Q2, bh);
@@ -388,6 +506,61 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
         mask &= mask - 1ull;
         ++visited;
         const int q0 = 32 * qt;
+        const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
+        const uint32_t npairs =
+            P.pairs ? P.pairs[pair_lists(BR, BH, P.nqt) * 4 * kPairCap + lidx] : kPairOverflow;
+        if (npairs <= (uint32_t)kPairCap) {
+          // the query tile's pairs with a key in this tile: their query and dO rows (into the
+          // zeroed tiles), dP = dO V^T on the matrix cores, the weights and dS at the pair
+          // positions from the forward's x, then dv += A^T dO and dk += dS^T Q
+          const PairLanes PL = load_pairs(P.pairs + lidx * (4 * kPairCap), npairs);
+          uint64_t sel = wave_ballot((uint32_t)l < npairs && (PL.key >> 5) == kt);
+          for (uint64_t m = sel; m; m &= m - 1ull) {
+            const int i = q0 + __builtin_amdgcn_readlane(PL.row, __builtin_ctzll(m));
+            dma_row<D>(qb, sq, i, W.a);
+            dma_row<D>(dob, sdo, i, W.b);
+          }
+          wait_all_loads();
+          f32x16 Dp = f32x16{};
+#pragma unroll
+          for (int t = 0; t < NT; ++t) Dp = PolBF16::mma(tile_row_frag<D>(W.b, t), V[t], Dp);
+          f32x16 EV = f32x16{}, EK = f32x16{};
+          for (uint64_t m = sel; m; m &= m - 1ull) {
+            const int e = __builtin_ctzll(m);
+            const int jl = __builtin_amdgcn_readlane(PL.key, e) & 31, il = __builtin_amdgcn_readlane(PL.row, e);
+            const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, PL.x), e));
+            const float rqi = NORM ? nq[q0 + il] : 1.f;
+            const int rr = crow_index(il);
+            const bool mine = n32 == jl && g == ((il >> 2) & 1);  // the lane holding (key jl, query il)
+            row_used |= n32 == jl;
+            float dp = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dp = r == rr ? Dp[r] : dp;
+            const float ev = coef * pow_p<PK>(x, pw);
+            const float ds = coef * dpow_p<PK>(x, pw) * dp;
+            const float ek = NORM ? ds * rqi : ds;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              EV[r] = mine && r == rr ? ev : EV[r];
+              EK[r] = mine && r == rr ? ek : EK[r];
+            }
+          }
+          ++computed;
+          const bf16x8 V0 = PolBF16::pack_c(EV, 0), V1 = PolBF16::pack_c(EV, 1);
+          const bf16x8 K0 = PolBF16::pack_c(EK, 0), K1 = PolBF16::pack_c(EK, 1);
+#pragma unroll
+          for (int c = 0; c < ND; ++c) {
+            AV[c] = PolBF16::mma(tile_tr_frag<D>(W.b, 0, c), V0, AV[c]);
+            AV[c] = PolBF16::mma(tile_tr_frag<D>(W.b, 1, c), V1, AV[c]);
+            AK[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 0, c), K0, AK[c]);
+            AK[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 1, c), K1, AK[c]);
+          }
+          continue;
+        }
+        row_used = true;
+        bf16x8 K[NT];  // the key fragments, for the score recompute
+#pragma unroll
+        for (int t = 0; t < NT; ++t) K[t] = *reinterpret_cast<const bf16x8*>(krow + 16 * t + 8 * g);
         dma_tile<D>(qb, sq, q0, Nq, W.a);
         dma_tile<D>(dob, sdo, q0, Nq, W.b);
         if constexpr (NORM) dma_row_vals(nq, q0, Nq, W.rows);
@@ -430,6 +603,11 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
       }
     }
     if (kvalid) {
+      // the key row for the normalize backward; rows no weight meets have a zero gradient,
+      // and zeros for their input row keep it zero
+      GradRow<D> XR = {};
+      if constexpr (NORM)
+        if (row_used) load_grad_row<D>(krow, XR);
       const int gslot = br == 0 ? B_DK1 : B_DK2;
       bf16* grow = (bf16*)P.grad[br == 0 ? 1 : 3] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
                    (int64_t)j * P.s[gslot][2];
@@ -449,14 +627,14 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
 // ------------------------------------------------------------------ dispatch
 template <int D, int BR, int PK, bool NORM>
 static int launch_t(const BwdParams& p, void* stream) {
-  const int64_t qitems = (int64_t)p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
+  const int64_t qitems = (int64_t)BR * p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3((unsigned)((qitems + kBwdWaves - 1) / kBwdWaves)),
                      dim3(64 * kBwdWaves), 0, s, p);
   hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3((unsigned)((kitems + kBwdWaves - 1) / kBwdWaves)),
                      dim3(64 * kBwdWaves), 0, s, p);
   const int e = (int)hipGetLastError();
-  return e ? e : launch_bwd_finish(p, BR, stream);
+  return e ? e : launch_bwd_finish(p, BR, qitems, stream);
 }
 template <int D, int BR, int PK>
 static int sel_norm(const BwdParams& p, const KernelKey& k, void* s) {

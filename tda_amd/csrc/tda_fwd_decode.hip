@@ -161,6 +161,8 @@ __global__ void __launch_bounds__(64 * kDecWaves, 2) fwd_decode(FwdParams P, flo
     const int n = e / D, d = e % D;
     dst[e] = red[d][n];
   }
+  if (P.pairs && chunk == 0 && threadIdx.x < BR)  // no pair lists here: the backward uses the bitmask
+    P.pairs[pair_lists(BR, BH, 1) * 4 * kPairCap + (int64_t)threadIdx.x * BH + bh] = kPairOverflow;
   if (threadIdx.x < BR && P.occ) {
     const int br = threadIdx.x;
     uint32_t w = 0u;

@@ -436,6 +436,10 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
     bool have_q = false;
     bf16x8 Q[NT];
     float rq = 1.f;
+    // pair list of (branch, head, query tile): npairs entries written so far (may pass the cap)
+    const int64_t lidx = ((int64_t)br * BH + bh) * nqt + qt;
+    uint32_t* pent = P.pairs ? P.pairs + lidx * (4 * kPairCap) : nullptr;
+    uint32_t npairs = 0;
     for (int w = 0; w <= (klast >> 5); ++w) {
       const uint32_t bits0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)orow[w]);
       uint32_t bits = bits0, keep = bits0;
@@ -502,6 +506,16 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
             const bool pos = (!edge || (key <= pq && key < Nk)) && x > 0.f;
             C[r] = pos ? coef * pow_p<PK>(x, pw) : 0.f;
             pos_any |= pos;
+            if (pent) {
+              // list entry of each non-zero weight, in the order (value r, lane)
+              const bool hit = valid && pos;
+              const uint64_t bal = wave_ballot(hit);
+              const uint32_t slot = npairs + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+              if (hit && slot < (uint32_t)kPairCap)
+                *reinterpret_cast<u32x4*>(pent + 4 * slot) = u32x4{(uint32_t)key, (uint32_t)n32, __builtin_bit_cast(uint32_t, x), 0u};
+              npairs += (uint32_t)__builtin_popcountll(bal);
+            }
           }
         if (wave_ballot(valid && pos_any) == 0ull) {
           keep &= ~(1u << (kt & 31));
@@ -520,6 +534,7 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
       }
       if (keep != bits0 && l == 0) orow[w] = keep;
     }
+    if (pent && l == 0) P.pairs[pair_lists(P.nbr, BH, nqt) * 4 * kPairCap + lidx] = npairs;
   }
 
   // Output rows through LDS (the K tile buffer): lane (n, g) holds elements 32c + crow(r, g) of

@@ -151,6 +151,11 @@ size_t tda_fwd_workspace_bytes_kv(int64_t batch, int64_t heads, int64_t seq_len,
   return (size_t)fwd_ws_bytes(batch * heads, seq_len, seq_len_kv, branches);
 }
 
+size_t tda_pair_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches) {
+  if (!size_args_ok(batch, heads, seq_len, seq_len, branches)) return 0;
+  return (size_t)tda::pair_words(branches, batch * heads, ceil_div(seq_len, 32));
+}
+
 size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches) {
   return tda_occupancy_words_kv(batch, heads, seq_len, seq_len, branches);
 }
@@ -166,7 +171,8 @@ size_t tda_fwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, in
 size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim) {
   (void)head_dim;
   if (batch < 1 || heads < 1 || seq_len < 1) return 0;
-  return (size_t)(batch * heads * ceil_div(seq_len, 32)) * 2 * sizeof(float);
+  // one (dbeta, dlambda) partial pair per (branch, head, query tile), for two branches
+  return (size_t)(2 * batch * heads * ceil_div(seq_len, 32)) * 2 * sizeof(float);
 }
 
 int32_t tda_validate_fwd(const tda_fwd_args* a) {
@@ -184,6 +190,7 @@ int32_t tda_validate_fwd(const tda_fwd_args* a) {
       a->workspace_bytes < tda_fwd_workspace_bytes_kv(a->batch, a->heads, a->seq_len, c.seq_len_kv, a->branches))
     return TDA_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0) return TDA_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(a->pairs) % 16 != 0) return TDA_ERR_LAYOUT;
   return TDA_OK;
 }
 
@@ -202,6 +209,7 @@ int32_t tda_validate_bwd(const tda_bwd_args* a) {
       a->workspace_bytes < tda_bwd_workspace_bytes(a->batch, a->heads, a->seq_len, a->head_dim))
     return TDA_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0) return TDA_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(a->pairs) % 16 != 0) return TDA_ERR_LAYOUT;
   return TDA_OK;
 }
 
@@ -238,6 +246,8 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
     p.part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) +
                                       fwd_occ_bytes(a->batch * a->heads, a->seq_len, c.seq_len_kv, a->branches));
   p.stats = a->stats;
+  p.pairs = a->pairs;
+  p.nbr = a->branches;
   const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};
   const int e = tda::launch_fwd(p, key, stream);
   if (e != 0) {
@@ -286,6 +296,7 @@ int32_t tda_bwd(const tda_bwd_args* a, void* stream) {
   p.occ = a->occupancy;
   p.ws = static_cast<float*>(a->workspace);
   p.stats = a->stats;
+  p.pairs = a->occupancy ? a->pairs : nullptr;  // the key-major pass finds the lists through the bitmask
   const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};
   const int e = tda::launch_bwd(p, key, stream);
   if (e != 0) {

@@ -14,6 +14,20 @@ enum BwdSlot { B_Q1 = 0, B_K1, B_Q2, B_K2, B_V, B_DO, B_DQ1, B_DK1, B_DQ2, B_DK2
 // query slots and Nk for the key slots (norm_base).
 enum NormSlot { N_Q1 = 0, N_K1 = 1, N_Q2 = 2, N_K2 = 3 };
 
+// Pair lists (bf16): for each (branch, head, query tile) the non-zero weights of the tile's
+// rows, written by the forward's exact pass and read by the backward, which then touches only
+// the rows they name.  Layout: the entries, kPairCap per list (list = (branch * B*H + bh) * nqt
+// + qt), each 4 u32 {key index j, query row within the tile, bits of x_ij = fma(s rk, rq, -tau),
+// 0}, in the order the exact pass met them (key tiles ascending); then the counts, u32 per list.
+// A count above kPairCap marks a list that did not fit: the backward then runs its tile path
+// for that query tile.
+constexpr int kPairCap = 32;
+constexpr int64_t pair_lists(int64_t branches, int64_t bh, int64_t nqt) { return branches * bh * nqt; }
+constexpr int64_t pair_words(int64_t branches, int64_t bh, int64_t nqt) {
+  return pair_lists(branches, bh, nqt) * (1 + 4 * kPairCap);
+}
+constexpr uint32_t kPairOverflow = 0xffffffffu;  // count of a list the forward did not write
+
 // Positions: query row i of a head sits at absolute position qoff + i and sees the keys
 // j <= qoff + i of the Nk key rows (qoff = 0 and Nq = Nk is the plain causal case).  Tiles are
 // 32 rows: nqt = ceil(Nq / 32) query tiles, nkt = ceil(Nk / 32) key tiles.
@@ -33,6 +47,8 @@ struct FwdParams {
   uint32_t* occ;             // may be null (bf16: never, the host points it at workspace)
   unsigned long long* stats; // may be null
   float* part;               // bf16 with one query tile: per-chunk partial outputs (workspace)
+  uint32_t* pairs;           // may be null: pair lists (bf16)
+  int nbr;                   // branches
 };
 
 struct BwdParams {
@@ -48,8 +64,9 @@ struct BwdParams {
   float* dlam;
   const float* norms;
   const uint32_t* occ;       // may be null: every causal tile is tested
-  float* ws;                 // [BH * nqt][2] dbeta / dlambda partials of the dQ pass
+  float* ws;                 // [branches * BH * nqt][2] dbeta / dlambda partials of the dQ pass
   unsigned long long* stats;
+  const uint32_t* pairs;     // may be null: the forward's pair lists (used with occ)
 };
 
 // Kernel-family launchers (return a hipError_t value).  Template selection happens inside.
@@ -66,6 +83,7 @@ int launch_fwd_sparse(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_fwd_decode(const FwdParams& p, const KernelKey& k, float* part, void* stream);
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream);
-int launch_bwd_finish(const BwdParams& p, int branches, void* stream);
+// Sum the (dbeta, dlambda) partial pairs ws[2 * item], item < items, in a fixed order.
+int launch_bwd_finish(const BwdParams& p, int branches, int64_t items, void* stream);
 
 }  // namespace tda

@@ -106,11 +106,11 @@ def _common(args, t: torch.Tensor, branches: int, normalize: bool, relu_power: f
 
 
 def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, branches: int,
-            norms=None, occupancy=None, stats=None, q_offset: int = 0) -> torch.Tensor:
+            norms=None, occupancy=None, stats=None, q_offset: int = 0, pairs=None) -> torch.Tensor:
     """One forward launch.  Tensors must already be in a native dtype (float32 / bfloat16)
     on one device; beta (and lam) are 0-dim float32 tensors on that device.  q1 (q2) have Nq
     rows at positions q_offset.., k1 (k2) and v have Nk rows.  The optional norms /
-    occupancy / stats buffers receive the side outputs described in include/tda.h."""
+    occupancy / stats / pairs buffers receive the side outputs described in include/tda.h."""
     lib = _abi.load()
     q1, k1, v = _usable(q1), _usable(k1), _usable(v)
     if branches == 2:
@@ -129,7 +129,7 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
                             device=q1.device)
     if stats is not None and (stats.dtype != torch.int64 or stats.numel() < 3 or stats.device != q1.device):
         raise ValueError("stats must be an int64 tensor of at least 3 elements on the inputs' device")
-    a.norms, a.occupancy, a.stats = _ptr(norms), _ptr(occupancy), _ptr(stats)
+    a.norms, a.occupancy, a.stats, a.pairs = _ptr(norms), _ptr(occupancy), _ptr(stats), _ptr(pairs)
     ws = torch.empty((lib.tda_fwd_workspace_bytes_kv(*q1.shape[:3], nk, branches) + 3) // 4,
                      dtype=torch.float32, device=q1.device)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
@@ -139,9 +139,10 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
 
 
 def backward(q1, k1, q2, k2, v, dout, beta, lam, relu_power: float, normalize: bool,
-             branches: int, norms=None, occupancy=None, stats=None, q_offset: int = 0):
+             branches: int, norms=None, occupancy=None, stats=None, q_offset: int = 0, pairs=None):
     """One backward launch: returns (dq1, dk1, dq2, dk2, dv, dbeta, dlambda); the branch-2
-    entries and dlambda are None when branches == 1."""
+    entries and dlambda are None when branches == 1.  pairs: the forward's pair lists (bf16,
+    with occupancy), or None for the bitmask tiles alone."""
     lib = _abi.load()
     q1, k1, v, dout = _usable(q1), _usable(k1), _usable(v), _usable(dout)
     if branches == 2:
@@ -165,7 +166,7 @@ def backward(q1, k1, q2, k2, v, dout, beta, lam, relu_power: float, normalize: b
     a.beta = _ptr(beta)
     a.lambda_param = _ptr(lam) if branches == 2 else None
     a.dbeta, a.dlambda = _ptr(dbeta), _ptr(dlam)
-    a.norms, a.occupancy = _ptr(norms), _ptr(occupancy)
+    a.norms, a.occupancy, a.pairs = _ptr(norms), _ptr(occupancy), _ptr(pairs)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
     a.stats = _ptr(stats)
     with torch.cuda.device(dev):
@@ -185,6 +186,13 @@ def side_buffers(shape, branches: int, normalize: bool, device, n_kv: int | None
     return norms, occ
 
 
+def pair_buffer(shape, branches: int, device):
+    """Allocate the forward's pair-list output (bf16 forwards write it; uninitialised: the
+    forward writes every count it sets a list by)."""
+    b, h, n, _ = shape
+    return torch.empty(_abi.load().tda_pair_words(b, h, n, branches), dtype=torch.int32, device=device)
+
+
 class TDAFunction(torch.autograd.Function):
     """Autograd node for TRA (branches == 1) and fused TDA (branches == 2).
 
@@ -194,23 +202,25 @@ class TDAFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches, q_offset=0):
         need = any(ctx.needs_input_grad[:7])
-        norms = occ = None
+        norms = occ = pairs = None
         if need:
             norms, occ = side_buffers(q1.shape, branches, normalize, q1.device, k1.shape[2])
+            if q1.dtype == torch.bfloat16:
+                pairs = pair_buffer(q1.shape, branches, q1.device)
         out = forward(q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches, norms, occ,
-                      q_offset=q_offset)
-        ctx.save_for_backward(q1, k1, q2, k2, v, beta, lam, norms, occ)
+                      q_offset=q_offset, pairs=pairs)
+        ctx.save_for_backward(q1, k1, q2, k2, v, beta, lam, norms, occ, pairs)
         ctx.cfg = (float(relu_power), bool(normalize), int(branches), int(q_offset))
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q1, k1, q2, k2, v, beta, lam, norms, occ = ctx.saved_tensors
+        q1, k1, q2, k2, v, beta, lam, norms, occ, pairs = ctx.saved_tensors
         relu_power, normalize, branches, q_offset = ctx.cfg
         dout = dout.to(q1.dtype)
         dq1, dk1, dq2, dk2, dv, dbeta, dlam = backward(
             q1, k1, q2, k2, v, dout, beta, lam, relu_power, normalize, branches, norms, occ,
-            q_offset=q_offset)
+            q_offset=q_offset, pairs=pairs)
         ng = ctx.needs_input_grad
         return (dq1 if ng[0] else None, dk1 if ng[1] else None,
                 dq2 if ng[2] else None, dk2 if ng[3] else None,
