@@ -6,18 +6,22 @@
 // follow torch autograd of TTA:505-517; dbeta is new (the reference returns None, TTA:469).
 // The formulas are listed at the top of tda_bwd.hip.
 //
-// Layout of the work:
-//   * query-major pass (bwd_dq_fast): one wave per 32-row query tile; for each branch it walks
-//     the set bits of that branch's bitmask row, so only key tiles with a non-zero score are
-//     touched.  dq_br is finished (F.normalize backward) at the end of the branch; the dbeta /
-//     dlambda partials accumulate over both branches.
-//   * key-major pass (bwd_dkv_fast): one wave per 32-row key tile; for each branch it walks
-//     the set bits of the bitmask column.  dv accumulates over both branches (A1 - lam A2);
-//     dk_br is finished at the end of each branch.
-// Each visited tile is fetched by the wave itself with direct global->LDS loads into a
-// wave-private, chunk-swizzled row-major tile that serves both as row fragments (ds_read_b128)
-// and, through the LDS transpose read, as transposed fragments.  Only one branch's resident
-// operands and accumulators are live at a time.
+// Layout of the work.  With the forward's pair lists (the non-zero weights of each (branch,
+// query tile), see tda_params.hpp) the backward touches only the rows those weights name:
+//   * bwd_dq_pairs: one wave per (branch, query tile) whose list fit; whole-row vector work per
+//     pair, the tile's other gradient rows stored as zeros.
+//   * bwd_dkv_pairs: one wave per key tile whose bitmask column has only lists that fit; the
+//     column's pairs gathered into 32-row "pair tiles" for the matrix cores.
+// The tile passes take the rest (lists past the cap, or no lists at all), driven by the bitmask:
+//   * bwd_dq_fast: one wave per (branch, query tile); walks the set bits of the bitmask row, so
+//     only key tiles with a non-zero score are touched; dq_br is finished (F.normalize backward)
+//     at the end.
+//   * bwd_dkv_fast: one wave per key tile; walks the set bits of the bitmask column of each
+//     branch; dv accumulates over both branches (A1 - lam A2), dk_br is finished per branch.
+// The tile passes fetch each visited tile with direct global->LDS loads into a wave-private,
+// chunk-swizzled row-major tile that serves both as row fragments (ds_read_b128) and, through
+// the LDS transpose read, as transposed fragments.  dbeta / dlambda partials: one pair per
+// (branch, query tile), summed in a fixed order by bwd_finish.
 #include "tda_common.hpp"
 #include "tda_params.hpp"
 #include "tda_pos.hpp"
@@ -78,16 +82,6 @@ __device__ __forceinline__ void dma_tile_b(const bf16* rows, int64_t st, int r0,
     const uint32_t off = (uint32_t)r * st2 + 16u * (uint32_t)((l % CH) ^ bswz<D>(r));
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(void, tile + u * RPI * D), 16, off, 0, 0, 0);
   }
-}
-// One row j of a (n, D) row set into row j % 32 of a swizzled tile (D/8 lanes, 16 bytes each).
-template <int D>
-__device__ __forceinline__ void dma_row(const bf16* rows, int64_t st, int j, bf16* tile) {
-  constexpr int CH = D / 8;
-  const int l = lane_id(), jl = j & 31;
-  const __amdgpu_buffer_rsrc_t rs = rows_rsrc(rows + (int64_t)j * st, (uint32_t)(D * 2));
-  if (l < CH)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(void, tile + jl * D), 16, 16u * (uint32_t)(l ^ bswz<D>(jl)), 0,
-                                             0, 0);
 }
 // Zero a 32 x D tile (the pair paths load only the rows their pairs name; the other rows meet
 // zero weights, and must hold finite values).
@@ -220,9 +214,11 @@ struct BwdWaveLds {
 // tiles; single-wave workgroups retire independently.
 constexpr int kBwdWaves = 1;
 
-// ------------------------------------------------------------------ query-major pass
-// One wave per (branch, query tile): a branch's resident operands (its query fragments, dO,
-// one dq accumulator) are half of both branches', which lets two waves share a SIMD.
+// ------------------------------------------------------------------ query-major pass, tiles
+// One wave per (branch, query tile) whose pair list did not fit (or with no lists at all): it
+// walks the set bits of the branch's bitmask row.  A branch's resident operands (its query
+// fragments, dO, one dq accumulator) are half of both branches', which lets two waves share a
+// SIMD.
 template <int D, int BR, int PK, bool NORM>
 __global__ void __launch_bounds__(64 * kBwdWaves) __attribute__((amdgpu_waves_per_eu(2))) bwd_dq_fast(BwdParams P) {
   constexpr int NT = D / 16, ND = D / 32;
@@ -257,23 +253,15 @@ __global__ void __launch_bounds__(64 * kBwdWaves) __attribute__((amdgpu_waves_pe
   // the forward's pair list of (branch, head, query tile), when it fit (else the tile path)
   const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
   const uint32_t npairs = P.pairs ? P.pairs[pair_lists(BR, BH, P.nqt) * 4 * kPairCap + lidx] : kPairOverflow;
-  const bool pair_path = npairs <= (uint32_t)kPairCap;
-  PairLanes PL{0, 0, 0.f};
-  bool row_used = !pair_path;  // the lane's query row meets a non-zero weight (pair path: some pair names it)
-  if (pair_path) {
-    PL = load_pairs(P.pairs + lidx * (4 * kPairCap), npairs);
-    for (uint32_t e = 0; e < npairs; ++e) row_used |= __builtin_amdgcn_readlane(PL.row, (int)e) == n32;
-  }
+  if (npairs <= (uint32_t)kPairCap) return;  // bwd_dq_pairs handles the lists that fit
   bf16x8 DO[NT], Q[NT];
   {
-    // dO rows only where a pair needs them (the pair path's dP is read at pair positions only)
     const bf16* r = base(B_DO) + (int64_t)ic * P.s[B_DO][2];
+    const bf16* rq_ = base(qslot) + (int64_t)ic * P.s[qslot][2];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) DO[t] = row_used ? *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g) : bf16x8{};
-    if (!pair_path) {  // the tile path recomputes the scores
-      const bf16* rq_ = base(qslot) + (int64_t)ic * P.s[qslot][2];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) Q[t] = *reinterpret_cast<const bf16x8*>(rq_ + 16 * t + 8 * g);
+    for (int t = 0; t < NT; ++t) {
+      DO[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+      Q[t] = *reinterpret_cast<const bf16x8*>(rq_ + 16 * t + 8 * g);
     }
   }
   const float rq = NORM ? P.norms[norm_base(P, br == 0 ? N_Q1 : N_Q2, bh) + ic] : 1.f;
@@ -298,57 +286,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) __attribute__((amdgpu_waves_pe
 #pragma unroll
   for (int c = 0; c < ND; ++c) A[c] = f32x16{};
 
-  if (pair_path) {
-    // Pairs of one key tile are consecutive in the list.  Per key tile: the key and value rows
-    // the pairs name (into the zeroed tiles), dP = dO V^T on the matrix cores, dS at the pair
-    // positions from the forward's x, then dq += dS K.
-    zero_tile<D>(W.a);
-    __builtin_amdgcn_s_waitcnt(0);
-    uint32_t e0 = 0;
-    while (e0 < npairs) {
-      const int kt = __builtin_amdgcn_readlane(PL.key, (int)e0) >> 5;
-      const uint64_t grp = wave_ballot((uint32_t)l >= e0 && (uint32_t)l < npairs && (PL.key >> 5) == kt);
-      const uint32_t e1 = e0 + (uint32_t)__builtin_popcountll(grp);
-      ++visited;
-      ++computed;
-      for (uint32_t e = e0; e < e1; ++e) {
-        const int j = __builtin_amdgcn_readlane(PL.key, (int)e);
-        dma_row<D>(kb, sk, j, W.a);
-        dma_row<D>(vb, sv, j, W.b);
-      }
-      wait_all_loads();
-      f32x16 Dp = f32x16{};
-#pragma unroll
-      for (int t = 0; t < NT; ++t) Dp = PolBF16::mma(tile_row_frag<D>(W.b, t), DO[t], Dp);
-      f32x16 E = f32x16{};
-      for (uint32_t e = e0; e < e1; ++e) {
-        const int j = __builtin_amdgcn_readlane(PL.key, (int)e), jl = j & 31;
-        const int il = __builtin_amdgcn_readlane(PL.row, (int)e);
-        const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, PL.x), (int)e));
-        const float rk = NORM ? nk[j] : 1.f;
-        const int rr = crow_index(jl);
-        const bool mine = n32 == il && g == ((jl >> 2) & 1);  // the lane holding (query il, key jl)
-        float dp = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dp = r == rr ? Dp[r] : dp;
-        const float ds = coef * dpow_p<PK>(x, pw) * dp;
-        bsum += mine ? ds : 0.f;
-        lsum = __builtin_fmaf(mine && want_l ? pow_p<PK>(x, pw) : 0.f, dp, lsum);
-        const float ev = NORM ? ds * rk : ds;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) E[r] = mine && r == rr ? ev : E[r];
-      }
-      const bf16x8 E0 = PolBF16::pack_c(E, 0), E1 = PolBF16::pack_c(E, 1);
-#pragma unroll
-      for (int c = 0; c < ND; ++c) {
-        A[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 0, c), E0, A[c]);
-        A[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 1, c), E1, A[c]);
-      }
-      e0 = e1;
-    }
-  }
-
-  for (int w0 = 0; w0 < (pair_path ? 0 : nw); w0 += 64) {
+  for (int w0 = 0; w0 < nw; w0 += 64) {
     const uint32_t lw = w0 == 0 ? lw0 : (w0 + l < nw) ? (occrow ? occrow[w0 + l] : 0xffffffffu) : 0u;
     for (int w = w0; w < min(nw, w0 + 64); ++w) {
       uint32_t bits = __builtin_amdgcn_readlane(lw, w - w0);
@@ -398,11 +336,9 @@ __global__ void __launch_bounds__(64 * kBwdWaves) __attribute__((amdgpu_waves_pe
   }
   if (qvalid) {
     // the query row for the normalize backward, loaded after the tiles (held during them, it
-    // would push the wave past the register budget of two waves per SIMD); rows no weight
-    // meets have a zero gradient, and zeros for their input row keep it zero
-    GradRow<D> XR = {};
-    if constexpr (NORM)
-      if (row_used) load_grad_row<D>(base(qslot) + (int64_t)ic * P.s[qslot][2], XR);
+    // would push the wave past the register budget of two waves per SIMD)
+    GradRow<D> XR;
+    if constexpr (NORM) load_grad_row<D>(base(qslot) + (int64_t)ic * P.s[qslot][2], XR);
     const int gslot = br == 0 ? B_DQ1 : B_DQ2;
     bf16* grow = (bf16*)P.grad[br == 0 ? 0 : 2] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
                  (int64_t)i * P.s[gslot][2];
@@ -418,6 +354,346 @@ __global__ void __launch_bounds__(64 * kBwdWaves) __attribute__((amdgpu_waves_pe
       atomicAdd(P.stats + 0, (unsigned long long)visited);
       atomicAdd(P.stats + 1, (unsigned long long)computed);
     }
+  }
+}
+
+// ------------------------------------------------------------------ query-major pass, pairs
+// One wave per (branch, query tile) whose pair list fit.  A list holds a few non-zero weights,
+// so the wave works on whole rows, D / 64 elements per lane: the tile's gradient rows that no
+// pair names are stored as zeros (16-byte stores), and for each named row i, in increasing
+// order, dq_i = sum over its pairs, in list order, of dS k_j (times the key's inverse norm with
+// normalisation), dS = coef p x^(p-1) (do_i . v_j) with x the forward's exact value; then the
+// normalize backward of the row.  No LDS, no matrix cores: per pair two row loads and one
+// wave-wide dot product.
+template <int D>
+struct RowVec {
+  static constexpr int E = D / 64;  // elements per lane
+  float v[E];
+};
+template <int D>
+__device__ __forceinline__ RowVec<D> load_rowvec(const bf16* row) {
+  RowVec<D> r;
+  const int l = lane_id();
+  if constexpr (D == 128) {
+    const bf16x2 x = *reinterpret_cast<const bf16x2*>(row + 2 * l);
+    r.v[0] = (float)x[0];
+    r.v[1] = (float)x[1];
+  } else {
+    r.v[0] = (float)row[l];
+  }
+  return r;
+}
+template <int D>
+__device__ __forceinline__ void store_rowvec(bf16* row, const RowVec<D>& r) {
+  const int l = lane_id();
+  if constexpr (D == 128) *reinterpret_cast<bf16x2*>(row + 2 * l) = bf16x2{(bf16)r.v[0], (bf16)r.v[1]};
+  else row[l] = (bf16)r.v[0];
+}
+template <int D>
+__device__ __forceinline__ float row_dot(const RowVec<D>& a, const RowVec<D>& b) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < RowVec<D>::E; ++e) s = __builtin_fmaf(a.v[e], b.v[e], s);
+  return wave_sum(s);
+}
+// The F.normalize backward of one row (see store_grad_rows): x the input row, rinv its inverse norm.
+template <int D, bool NORM>
+__device__ __forceinline__ RowVec<D> normalize_back(const RowVec<D>& g, const RowVec<D>& x, float rinv) {
+  if constexpr (!NORM) return g;
+  RowVec<D> xh, o;
+#pragma unroll
+  for (int e = 0; e < RowVec<D>::E; ++e) xh.v[e] = x.v[e] * rinv;
+  const float dot = row_dot<D>(xh, g);
+  const bool clamped = rinv >= 1.0f / kNormEps;
+#pragma unroll
+  for (int e = 0; e < RowVec<D>::E; ++e) o.v[e] = clamped ? g.v[e] * rinv : (g.v[e] - xh.v[e] * dot) * rinv;
+  return o;
+}
+// Zero rows 0..nrows-1 of a 32-row tile except those in `keep` (16 bytes per lane and store).
+template <int D>
+__device__ __forceinline__ void zero_rows(bf16* tile0, int64_t st, int nrows, uint32_t keep) {
+  constexpr int CH = D / 8, RPI = 64 / CH;
+  const int l = lane_id();
+#pragma unroll
+  for (int u = 0; u < 32 / RPI; ++u) {
+    const int r = u * RPI + l / CH;
+    if (r < nrows && !((keep >> r) & 1u))
+      *reinterpret_cast<u32x4*>(tile0 + (int64_t)r * st + 8 * (l % CH)) = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
+  const int l = lane_id();
+  const int BH = P.B * P.H;
+  const int64_t item = blockIdx.x;  // (query tile, head, branch), in the order of bwd_dq_fast
+  if (item >= (int64_t)BR * BH * P.nqt) return;
+  const int br = BR == 2 ? (int)(item & 1) : 0;
+  const int64_t rest = BR == 2 ? item >> 1 : item;
+  const int qt = P.nqt - 1 - (int)(rest / BH);
+  const int bh = (int)(rest % BH);
+  const int b = bh / P.H, h = bh % P.H;
+  const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
+  // the count and every entry slot at once (slots past the count are never used)
+  const PairLanes PL = load_pairs(P.pairs + lidx * (4 * kPairCap), (uint32_t)kPairCap);
+  const uint32_t npairs = P.pairs[pair_lists(BR, BH, P.nqt) * 4 * kPairCap + lidx];
+  if (npairs > (uint32_t)kPairCap) return;  // bwd_dq_fast walks the tiles
+
+  auto base = [&](int slot) {
+    return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
+  };
+  const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2, gslot = br == 0 ? B_DQ1 : B_DQ2;
+  const int64_t sq = P.s[qslot][2], sk = P.s[kslot][2], sv = P.s[B_V][2], sdo = P.s[B_DO][2], sg = P.s[gslot][2];
+  const bf16* qb = base(qslot);
+  const bf16* kb = base(kslot);
+  const bf16* vb = base(B_V);
+  const bf16* dob = base(B_DO);
+  bf16* gb = (bf16*)P.grad[br == 0 ? 0 : 2] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1];
+  const float* nq = NORM ? P.norms + norm_base(P, br == 0 ? N_Q1 : N_Q2, bh) : nullptr;
+  const float* nk = NORM ? P.norms + norm_base(P, br == 0 ? N_K1 : N_K2, bh) : nullptr;
+  const float pw = P.p;
+  float coef = 1.f;
+  if constexpr (BR == 2) coef = br == 0 ? 1.f : -clamp01(*P.lam);
+  const bool want_l = BR == 2 && br == 1;  // dlambda comes from branch 2 alone
+
+  uint32_t used = 0u;  // rows (within the tile) some pair names
+  unsigned tiles = 0;
+  int last_kt = -1;
+  for (uint32_t e = 0; e < npairs; ++e) {
+    used |= 1u << __builtin_amdgcn_readlane(PL.row, (int)e);
+    const int kt = __builtin_amdgcn_readlane(PL.key, (int)e) >> 5;
+    tiles += kt != last_kt ? 1u : 0u;  // pairs of one key tile are consecutive
+    last_kt = kt;
+  }
+  const int q0 = 32 * qt;
+  zero_rows<D>(gb + (int64_t)q0 * sg, sg, min(32, P.Nq - q0), used);
+
+  float pb = 0.f, pl = 0.f;  // dbeta, dlambda partials (the same in every lane)
+  for (uint32_t m = used; m; m &= m - 1u) {
+    const int il = __builtin_ctz(m), i = q0 + il;
+    const RowVec<D> dor = load_rowvec<D>(dob + (int64_t)i * sdo);
+    RowVec<D> xr = {};
+    if constexpr (NORM) xr = load_rowvec<D>(qb + (int64_t)i * sq);
+    const float rq = NORM ? nq[i] : 1.f;
+    const float ci = tau_coeff(P.qoff + i, P.inv_d);
+    RowVec<D> acc = {};
+    for (uint32_t e = 0; e < npairs; ++e) {
+      if (__builtin_amdgcn_readlane(PL.row, (int)e) != il) continue;
+      const int j = __builtin_amdgcn_readlane(PL.key, (int)e);
+      const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, PL.x), (int)e));
+      const RowVec<D> kr = load_rowvec<D>(kb + (int64_t)j * sk);
+      const RowVec<D> vr = load_rowvec<D>(vb + (int64_t)j * sv);
+      const float rk = NORM ? nk[j] : 1.f;
+      const float dp = row_dot<D>(dor, vr);
+      const float ds = coef * dpow_p<PK>(x, pw) * dp;
+      pb = __builtin_fmaf(-ci, ds, pb);
+      if (want_l) pl = __builtin_fmaf(-pow_p<PK>(x, pw), dp, pl);
+      const float w = NORM ? ds * rk : ds;
+#pragma unroll
+      for (int c = 0; c < RowVec<D>::E; ++c) acc.v[c] = __builtin_fmaf(w, kr.v[c], acc.v[c]);
+    }
+    store_rowvec<D>(gb + (int64_t)i * sg, normalize_back<D, NORM>(acc, xr, rq));
+  }
+  if (l == 0) {
+    P.ws[2 * item + 0] = pb;
+    P.ws[2 * item + 1] = pl;
+    if (P.stats) {
+      atomicAdd(P.stats + 0, (unsigned long long)tiles);
+      atomicAdd(P.stats + 1, (unsigned long long)tiles);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ key-major pass, pairs
+// Whether the bitmask column of key tile kt (query tiles qtf.., both branches) has a query tile
+// whose pair list did not fit: the key tile then goes to the tile pass, else to the pair pass.
+template <int BR>
+__device__ __forceinline__ bool column_overflows(const BwdParams& P, int bh, int kt, int qtf) {
+  const int BH = P.B * P.H, l = lane_id();
+  const uint32_t* counts = P.pairs + pair_lists(BR, BH, P.nqt) * 4 * kPairCap;
+  bool ovf = false;
+#pragma unroll
+  for (int br = 0; br < BR; ++br) {
+    const uint32_t* occcol = P.occ + ((int64_t)br * BH + bh) * P.nqt * P.occ_w + (kt >> 5);
+    for (int q0c = qtf; q0c < P.nqt; q0c += 64) {
+      const int qt = q0c + l;
+      const bool has = qt < P.nqt && ((occcol[(int64_t)qt * P.occ_w] >> (kt & 31)) & 1u);
+      ovf = ovf || (has && counts[((int64_t)br * BH + bh) * P.nqt + qt] > (uint32_t)kPairCap);
+    }
+  }
+  return wave_ballot(ovf) != 0ull;
+}
+
+// One wave per key tile whose column has only lists that fit.  Per branch the wave walks the
+// column's lists once and gathers the pairs with a key in this tile into "pair tiles" of up to 32:
+// row e of two LDS tiles holds the query row and the dO row pair e names (four pairs per load
+// instruction); then dP[e][jl] = do_i(e) . v_jl on the matrix cores (v resident as the B operand),
+// and dv += dO_pairs^T A, dk += Q_pairs^T dS with A[e][jl(e)] = coef x^p and
+// dS[e][jl(e)] = coef p x^(p-1) dP (times the query's inverse norm with normalisation), x the
+// forward's exact value.  Pairs meet the accumulators in column order, then list order.
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) bwd_dkv_pairs(BwdParams P) {
+  constexpr int NT = D / 16, ND = D / 32, CH = D / 8, RPI = 64 / CH;
+  __shared__ __attribute__((aligned(16))) bf16 qpt[32 * D], dpt[32 * D];  // pair tiles (swizzled rows)
+  __shared__ int ps_i[32], ps_jl[32];  // the batch's pairs: query row, key row in the tile, x
+  __shared__ float ps_x[32];
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int BH = P.B * P.H;
+  const int64_t item = blockIdx.x;  // (key tile, head), in the order of bwd_dkv_fast
+  if (item >= (int64_t)BH * P.nkt) return;
+  const int kt = (int)(item / BH), bh = (int)(item % BH);
+  const int b = bh / P.H, h = bh % P.H;
+  const int qtf = qt_first(kt, P.qoff);
+  if (column_overflows<BR>(P, bh, kt, qtf)) return;  // bwd_dkv_fast takes the key tile
+
+  auto base = [&](int slot) {
+    return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
+  };
+  const uint32_t* counts = P.pairs + pair_lists(BR, BH, P.nqt) * 4 * kPairCap;
+  const int Nk = P.Nk, j = 32 * kt + n32, jc = min(j, Nk - 1);
+  const bool kvalid = j < Nk;
+  const float pw = P.p;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+  const bf16* dob = base(B_DO);
+  const int64_t sdo = P.s[B_DO][2];
+
+  bf16x8 V[NT];  // the lane's key row of v (B operand of dP)
+  {
+    const bf16* r = base(B_V) + (int64_t)jc * P.s[B_V][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) V[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+  }
+  f32x16 AV[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) AV[c] = f32x16{};
+  unsigned visited = 0;
+  zero_tile<D>(qpt);  // rows a batch does not load must hold finite values
+  zero_tile<D>(dpt);
+  __builtin_amdgcn_s_waitcnt(0);
+
+#pragma unroll
+  for (int br = 0; br < BR; ++br) {
+    const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2, gslot = br == 0 ? B_DK1 : B_DK2;
+    const bf16* qb = base(qslot);
+    const int64_t sq = P.s[qslot][2];
+    const float* nq = NORM ? P.norms + norm_base(P, br == 0 ? N_Q1 : N_Q2, bh) : nullptr;
+    const float coef = br == 0 ? 1.f : -lam;
+    const uint32_t* occcol = P.occ + ((int64_t)br * BH + bh) * P.nqt * P.occ_w + (kt >> 5);
+    f32x16 AK[ND];
+#pragma unroll
+    for (int c = 0; c < ND; ++c) AK[c] = f32x16{};
+    bool row_used = false;  // some pair names the lane's key row
+    uint32_t np = 0;        // pairs gathered into the current batch
+
+    // dP, the weights and the accumulation for the batch's np pairs
+    auto flush = [&]() {
+      if (np == 0) return;
+      const int e_l = (uint32_t)l < np ? l : 0;  // pair tile rows past the batch repeat pair 0
+      const int i_l = ps_i[e_l];
+      float rq_l = 1.f;
+      if constexpr (NORM) rq_l = nq[i_l];
+      // only the load instructions that cover pairs (rows past the batch in them repeat pair 0;
+      // rows no instruction covers keep finite older contents, and meet zero weights)
+      for (int u = 0; u < (int)(np + RPI - 1) / RPI; ++u) {
+        const int e = u * RPI + l / CH;
+        const int i = __shfl(i_l, e);
+        const int c = (l % CH) ^ bswz<D>(e);
+        __builtin_amdgcn_global_load_lds((const void*)(qb + (int64_t)i * sq + 8 * c), LDS_PTR(void, qpt + u * RPI * D), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(dob + (int64_t)i * sdo + 8 * c), LDS_PTR(void, dpt + u * RPI * D), 16, 0, 0);
+      }
+      wait_all_loads();
+      // dv += dO^T A first, then dP and dk += Q^T dS: the weight tile, dP and dS never live together
+      {
+        f32x16 EV = f32x16{};
+        for (uint32_t e = 0; e < np; ++e) {
+          const int jl = ps_jl[e];
+          const int rr = crow_index((int)e);
+          const bool mine = n32 == jl && g == (((int)e >> 2) & 1);  // the lane holding (pair e, key jl)
+          row_used |= n32 == jl;
+          const float ev = coef * pow_p<PK>(ps_x[e], pw);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) EV[r] = mine && r == rr ? ev : EV[r];
+        }
+        const bf16x8 V0 = PolBF16::pack_c(EV, 0), V1 = PolBF16::pack_c(EV, 1);
+#pragma unroll
+        for (int c = 0; c < ND; ++c) {
+          AV[c] = PolBF16::mma(tile_tr_frag<D>(dpt, 0, c), V0, AV[c]);
+          AV[c] = PolBF16::mma(tile_tr_frag<D>(dpt, 1, c), V1, AV[c]);
+        }
+      }
+      f32x16 Dp = f32x16{};
+#pragma unroll
+      for (int t = 0; t < NT; ++t) Dp = PolBF16::mma(tile_row_frag<D>(dpt, t), V[t], Dp);
+      f32x16 EK = f32x16{};
+      for (uint32_t e = 0; e < np; ++e) {
+        const int jl = ps_jl[e];
+        const float x = ps_x[e];
+        const float rqi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, rq_l), (int)e));
+        const int rr = crow_index((int)e);
+        const bool mine = n32 == jl && g == (((int)e >> 2) & 1);
+        float dp = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dp = r == rr ? Dp[r] : dp;
+        const float ds = coef * dpow_p<PK>(x, pw) * dp;
+        const float ek = NORM ? ds * rqi : ds;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) EK[r] = mine && r == rr ? ek : EK[r];
+      }
+      const bf16x8 K0 = PolBF16::pack_c(EK, 0), K1 = PolBF16::pack_c(EK, 1);
+#pragma unroll
+      for (int c = 0; c < ND; ++c) {
+        AK[c] = PolBF16::mma(tile_tr_frag<D>(qpt, 0, c), K0, AK[c]);
+        AK[c] = PolBF16::mma(tile_tr_frag<D>(qpt, 1, c), K1, AK[c]);
+      }
+      np = 0;
+      __builtin_amdgcn_s_waitcnt(0);  // every read of the pair tiles and slots done before reuse
+    };
+
+    for (int q0c = qtf; q0c < P.nqt; q0c += 64) {
+      const int qtl = q0c + l;
+      const bool has = qtl < P.nqt && ((occcol[(int64_t)qtl * P.occ_w] >> (kt & 31)) & 1u);
+      const uint32_t cnt_l = has ? counts[((int64_t)br * BH + bh) * P.nqt + qtl] : 0u;
+      for (uint64_t mask = wave_ballot(has); mask; mask &= mask - 1ull) {
+        const int qsel = __builtin_ctzll(mask), qt = q0c + qsel;
+        const uint32_t cnt = (uint32_t)__builtin_amdgcn_readlane((int)cnt_l, qsel);
+        const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
+        const PairLanes PL = load_pairs(P.pairs + lidx * (4 * kPairCap), cnt);
+        const bool match = (uint32_t)l < cnt && (PL.key >> 5) == kt;
+        const uint64_t mm = wave_ballot(match);
+        const uint32_t nm = (uint32_t)__builtin_popcountll(mm);
+        if (nm == 0) continue;
+        ++visited;
+        if (np + nm > 32u) flush();
+        if (match) {  // append in list order
+          const uint32_t slot = np + __builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
+          ps_i[slot] = 32 * qt + PL.row;
+          ps_jl[slot] = PL.key & 31;
+          ps_x[slot] = PL.x;
+        }
+        np += nm;
+      }
+    }
+    flush();
+    if (kvalid) {
+      // the key row for the normalize backward: rows no pair names have a zero gradient
+      GradRow<D> XR = {};
+      if constexpr (NORM)
+        if (row_used) load_grad_row<D>(base(kslot) + (int64_t)jc * P.s[kslot][2], XR);
+      const float rk = NORM ? P.norms[norm_base(P, br == 0 ? N_K1 : N_K2, bh) + jc] : 1.f;
+      bf16* grow = (bf16*)P.grad[br == 0 ? 1 : 3] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
+                   (int64_t)j * P.s[gslot][2];
+      store_grad_rows<D, NORM>(AK, XR, grow, rk);
+    }
+  }
+  if (kvalid) {
+    bf16* vrow = (bf16*)P.grad[4] + (int64_t)b * P.s[B_DV][0] + (int64_t)h * P.s[B_DV][1] + (int64_t)j * P.s[B_DV][2];
+    store_grad_rows<D, false>(AV, GradRow<D>{}, vrow, 1.f);
+  }
+  if (P.stats && l == 0) {
+    atomicAdd(P.stats + 0, (unsigned long long)visited);
+    atomicAdd(P.stats + 1, (unsigned long long)visited);
   }
 }
 
@@ -441,6 +717,7 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
   const bool kvalid = j < Nk;
   const int jc = min(j, Nk - 1);
   const int qtf = qt_first(kt, qoff);  // first query tile that sees the key tile
+  if (P.pairs && !column_overflows<BR>(P, bh, kt, qtf)) return;  // bwd_dkv_pairs takes the key tile
   auto base = [&](int slot) {
     return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
   };
@@ -461,11 +738,6 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
 #pragma unroll
   for (int c = 0; c < ND; ++c) AV[c] = f32x16{};
   unsigned visited = 0, computed = 0;
-  if (P.pairs) {  // the pair path loads single rows: the others must be finite
-    zero_tile<D>(W.a);
-    zero_tile<D>(W.b);
-    __builtin_amdgcn_s_waitcnt(0);
-  }
 
   // Both branches' row operands, issued with V so that one memory round trip covers them:
   // inverse key norms, and the bitmask column bits of query tiles qtf .. qtf+63 (lane q holds
@@ -486,7 +758,6 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
     const bf16* qb = base(qslot);
     const int64_t sq = P.s[qslot][2];
     const bf16* krow = base(kslot) + (int64_t)jc * P.s[kslot][2];
-    bool row_used = false;  // the lane's key row met a non-zero weight (or the tile path ran)
     const float rk = RK[br];
     const float* nq = nullptr;
     if constexpr (NORM) nq = P.norms + norm_base(P, br == 0 ? N_Q1 : N_Q2, bh);
@@ -506,58 +777,6 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
         mask &= mask - 1ull;
         ++visited;
         const int q0 = 32 * qt;
-        const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
-        const uint32_t npairs =
-            P.pairs ? P.pairs[pair_lists(BR, BH, P.nqt) * 4 * kPairCap + lidx] : kPairOverflow;
-        if (npairs <= (uint32_t)kPairCap) {
-          // the query tile's pairs with a key in this tile: their query and dO rows (into the
-          // zeroed tiles), dP = dO V^T on the matrix cores, the weights and dS at the pair
-          // positions from the forward's x, then dv += A^T dO and dk += dS^T Q
-          const PairLanes PL = load_pairs(P.pairs + lidx * (4 * kPairCap), npairs);
-          uint64_t sel = wave_ballot((uint32_t)l < npairs && (PL.key >> 5) == kt);
-          for (uint64_t m = sel; m; m &= m - 1ull) {
-            const int i = q0 + __builtin_amdgcn_readlane(PL.row, __builtin_ctzll(m));
-            dma_row<D>(qb, sq, i, W.a);
-            dma_row<D>(dob, sdo, i, W.b);
-          }
-          wait_all_loads();
-          f32x16 Dp = f32x16{};
-#pragma unroll
-          for (int t = 0; t < NT; ++t) Dp = PolBF16::mma(tile_row_frag<D>(W.b, t), V[t], Dp);
-          f32x16 EV = f32x16{}, EK = f32x16{};
-          for (uint64_t m = sel; m; m &= m - 1ull) {
-            const int e = __builtin_ctzll(m);
-            const int jl = __builtin_amdgcn_readlane(PL.key, e) & 31, il = __builtin_amdgcn_readlane(PL.row, e);
-            const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, PL.x), e));
-            const float rqi = NORM ? nq[q0 + il] : 1.f;
-            const int rr = crow_index(il);
-            const bool mine = n32 == jl && g == ((il >> 2) & 1);  // the lane holding (key jl, query il)
-            row_used |= n32 == jl;
-            float dp = 0.f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) dp = r == rr ? Dp[r] : dp;
-            const float ev = coef * pow_p<PK>(x, pw);
-            const float ds = coef * dpow_p<PK>(x, pw) * dp;
-            const float ek = NORM ? ds * rqi : ds;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              EV[r] = mine && r == rr ? ev : EV[r];
-              EK[r] = mine && r == rr ? ek : EK[r];
-            }
-          }
-          ++computed;
-          const bf16x8 V0 = PolBF16::pack_c(EV, 0), V1 = PolBF16::pack_c(EV, 1);
-          const bf16x8 K0 = PolBF16::pack_c(EK, 0), K1 = PolBF16::pack_c(EK, 1);
-#pragma unroll
-          for (int c = 0; c < ND; ++c) {
-            AV[c] = PolBF16::mma(tile_tr_frag<D>(W.b, 0, c), V0, AV[c]);
-            AV[c] = PolBF16::mma(tile_tr_frag<D>(W.b, 1, c), V1, AV[c]);
-            AK[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 0, c), K0, AK[c]);
-            AK[c] = PolBF16::mma(tile_tr_frag<D>(W.a, 1, c), K1, AK[c]);
-          }
-          continue;
-        }
-        row_used = true;
         bf16x8 K[NT];  // the key fragments, for the score recompute
 #pragma unroll
         for (int t = 0; t < NT; ++t) K[t] = *reinterpret_cast<const bf16x8*>(krow + 16 * t + 8 * g);
@@ -603,11 +822,8 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
       }
     }
     if (kvalid) {
-      // the key row for the normalize backward; rows no weight meets have a zero gradient,
-      // and zeros for their input row keep it zero
-      GradRow<D> XR = {};
-      if constexpr (NORM)
-        if (row_used) load_grad_row<D>(krow, XR);
+      GradRow<D> XR;  // the key row for the normalize backward
+      if constexpr (NORM) load_grad_row<D>(krow, XR);
       const int gslot = br == 0 ? B_DK1 : B_DK2;
       bf16* grow = (bf16*)P.grad[br == 0 ? 1 : 3] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
                    (int64_t)j * P.s[gslot][2];
@@ -629,8 +845,10 @@ template <int D, int BR, int PK, bool NORM>
 static int launch_t(const BwdParams& p, void* stream) {
   const int64_t qitems = (int64_t)BR * p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
+  if (p.pairs) hipLaunchKernelGGL((bwd_dq_pairs<D, BR, PK, NORM>), dim3((unsigned)qitems), dim3(64), 0, s, p);
   hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3((unsigned)((qitems + kBwdWaves - 1) / kBwdWaves)),
                      dim3(64 * kBwdWaves), 0, s, p);
+  if (p.pairs) hipLaunchKernelGGL((bwd_dkv_pairs<D, BR, PK, NORM>), dim3((unsigned)kitems), dim3(64), 0, s, p);
   hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3((unsigned)((kitems + kBwdWaves - 1) / kBwdWaves)),
                      dim3(64 * kBwdWaves), 0, s, p);
   const int e = (int)hipGetLastError();
