@@ -180,8 +180,8 @@ def side_configs(steps: int, warmup: int):
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-side", action="store_true", help="skip the configs[1] / configs[4] report figures")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
