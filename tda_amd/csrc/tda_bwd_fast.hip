@@ -10,8 +10,9 @@
 // query tile), see tda_params.hpp) the backward touches only the rows those weights name:
 //   * bwd_dq_pairs: one wave per (branch, query tile) whose list fit; whole-row vector work per
 //     pair, the tile's other gradient rows stored as zeros.
-//   * bwd_dkv_pairs: one wave per key tile whose bitmask column has only lists that fit; the
-//     column's pairs gathered into 32-row "pair tiles" for the matrix cores.
+//   * bwd_dkv_pairs: one wave per key tile whose bitmask column has only lists that fit; whole-
+//     row vector work per key row its pairs name, with the dk weight of each pair stored by
+//     bwd_dq_pairs (no V, no matrix cores), the tile's other gradient rows stored as zeros.
 // The tile passes take the rest (lists past the cap, or no lists at all), driven by the bitmask:
 //   * bwd_dq_fast: one wave per (branch, query tile); walks the set bits of the bitmask row, so
 //     only key tiles with a non-zero score are touched; dq_br is finished (F.normalize backward)
@@ -83,16 +84,6 @@ __device__ __forceinline__ void dma_tile_b(const bf16* rows, int64_t st, int r0,
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(void, tile + u * RPI * D), 16, off, 0, 0, 0);
   }
 }
-// Zero a 32 x D tile (the pair paths load only the rows their pairs name; the other rows meet
-// zero weights, and must hold finite values).
-template <int D>
-__device__ __forceinline__ void zero_tile(bf16* tile) {
-  const int l = lane_id();
-#pragma unroll
-  for (int u = 0; u < 32 * D / 8 / 64; ++u) *reinterpret_cast<u32x4*>(tile + 8 * (64 * u + l)) = u32x4{0u, 0u, 0u, 0u};
-}
-// Value index r of the 32x32 C layout holding tile row `row` for lane group g = (row >> 2) & 1.
-__device__ __forceinline__ int crow_index(int row) { return 4 * (row >> 3) + (row & 3); }
 // Lane-distributed pair list: lane e < n holds entry e (key, query row in the tile, x).
 struct PairLanes {
   int key, row;
@@ -363,8 +354,9 @@ __global__ void __launch_bounds__(64 * kBwdWaves) __attribute__((amdgpu_waves_pe
 // pair names are stored as zeros (16-byte stores), and for each named row i, in increasing
 // order, dq_i = sum over its pairs, in list order, of dS k_j (times the key's inverse norm with
 // normalisation), dS = coef p x^(p-1) (do_i . v_j) with x the forward's exact value; then the
-// normalize backward of the row.  No LDS, no matrix cores: per pair two row loads and one
-// wave-wide dot product.
+// normalize backward of the row.  Each pair's dk weight, dS (times rq_i with normalisation),
+// goes to the workspace slot of its list entry for bwd_dkv_pairs.  No LDS, no matrix cores: per
+// pair two row loads and one wave-wide dot product.
 template <int D>
 struct RowVec {
   static constexpr int E = D / 64;  // elements per lane
@@ -469,6 +461,7 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   zero_rows<D>(gb + (int64_t)q0 * sg, sg, min(32, P.Nq - q0), used);
 
   float pb = 0.f, pl = 0.f;  // dbeta, dlambda partials (the same in every lane)
+  float wkl = 0.f;           // lane e: the dk weight of pair e, for the key-major pair pass
   for (uint32_t m = used; m; m &= m - 1u) {
     const int il = __builtin_ctz(m), i = q0 + il;
     const RowVec<D> dor = load_rowvec<D>(dob + (int64_t)i * sdo);
@@ -489,11 +482,13 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
       pb = __builtin_fmaf(-ci, ds, pb);
       if (want_l) pl = __builtin_fmaf(-pow_p<PK>(x, pw), dp, pl);
       const float w = NORM ? ds * rk : ds;
+      wkl = l == (int)e ? (NORM ? ds * rq : ds) : wkl;
 #pragma unroll
       for (int c = 0; c < RowVec<D>::E; ++c) acc.v[c] = __builtin_fmaf(w, kr.v[c], acc.v[c]);
     }
     store_rowvec<D>(gb + (int64_t)i * sg, normalize_back<D, NORM>(acc, xr, rq));
   }
+  if ((uint32_t)l < npairs) P.pws[lidx * kPairCap + l] = wkl;
   if (l == 0) {
     P.ws[2 * item + 0] = pb;
     P.ws[2 * item + 1] = pl;
@@ -505,40 +500,61 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
 }
 
 // ------------------------------------------------------------------ key-major pass, pairs
-// Whether the bitmask column of key tile kt (query tiles qtf.., both branches) has a query tile
+// Whether the bitmask column of key tile kt (query tiles qtf.., every branch) has a query tile
 // whose pair list did not fit: the key tile then goes to the tile pass, else to the pair pass.
+// Both key-major passes decide with this test.
 template <int BR>
 __device__ __forceinline__ bool column_overflows(const BwdParams& P, int bh, int kt, int qtf) {
   const int BH = P.B * P.H, l = lane_id();
   const uint32_t* counts = P.pairs + pair_lists(BR, BH, P.nqt) * 4 * kPairCap;
   bool ovf = false;
+  for (int q0c = qtf; q0c < P.nqt; q0c += 64) {
+    const int qt = q0c + l;
+    const bool in = qt < P.nqt;
+    uint32_t w[BR], c[BR];
 #pragma unroll
-  for (int br = 0; br < BR; ++br) {
-    const uint32_t* occcol = P.occ + ((int64_t)br * BH + bh) * P.nqt * P.occ_w + (kt >> 5);
-    for (int q0c = qtf; q0c < P.nqt; q0c += 64) {
-      const int qt = q0c + l;
-      const bool has = qt < P.nqt && ((occcol[(int64_t)qt * P.occ_w] >> (kt & 31)) & 1u);
-      ovf = ovf || (has && counts[((int64_t)br * BH + bh) * P.nqt + qt] > (uint32_t)kPairCap);
+    for (int br = 0; br < BR; ++br) {  // every load of the chunk before the first use
+      const int64_t row = ((int64_t)br * BH + bh) * P.nqt + (in ? qt : P.nqt - 1);
+      w[br] = P.occ[row * P.occ_w + (kt >> 5)];
+      c[br] = counts[row];
     }
+#pragma unroll
+    for (int br = 0; br < BR; ++br) ovf = ovf || (in && ((w[br] >> (kt & 31)) & 1u) && c[br] > (uint32_t)kPairCap);
   }
   return wave_ballot(ovf) != 0ull;
 }
 
-// One wave per key tile whose column has only lists that fit.  Per branch the wave walks the
-// column's lists once and gathers the pairs with a key in this tile into "pair tiles" of up to 32:
-// row e of two LDS tiles holds the query row and the dO row pair e names (four pairs per load
-// instruction); then dP[e][jl] = do_i(e) . v_jl on the matrix cores (v resident as the B operand),
-// and dv += dO_pairs^T A, dk += Q_pairs^T dS with A[e][jl(e)] = coef x^p and
-// dS[e][jl(e)] = coef p x^(p-1) dP (times the query's inverse norm with normalisation), x the
-// forward's exact value.  Pairs meet the accumulators in column order, then list order.
-template <int D, int BR, int PK, bool NORM>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) bwd_dkv_pairs(BwdParams P) {
-  constexpr int NT = D / 16, ND = D / 32, CH = D / 8, RPI = 64 / CH;
-  __shared__ __attribute__((aligned(16))) bf16 qpt[32 * D], dpt[32 * D];  // pair tiles (swizzled rows)
-  __shared__ int ps_i[32], ps_jl[32];  // the batch's pairs: query row, key row in the tile, x
-  __shared__ float ps_x[32];
+// LDS slots of the key-major pair pass: pairs of one column gathered at once.
+constexpr int kColPairs = 64;
 
-  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+// One entry of a column's pair list as seen by one lane of the key-major pair pass.
+struct ColEntry {
+  bool valid;  // the lane holds an entry
+  int key;     // key index j
+  int i;       // query row
+  float x;     // exact forward value
+  float wk;    // dk weight from the query-major pair pass
+};
+
+// One wave per key tile whose column has only lists that fit.  It walks the column's lists
+// (both branches, query-tile chunks of 64, two lists per step: lanes 0-31 and 32-63) and keeps
+// the pairs with a key in this tile.  For each key row j that some pair names, in increasing
+// order, whole-row vector work over its pairs:
+//   dv_j  += coef A_ij do_i          A_ij = x^p (x the forward's exact value)
+//   dk_j  += w_ij q_i                w_ij = coef p x^(p-1) (do_i . v_j) (times rq_i with
+//                                    normalisation), stored by the query-major pair pass
+// then the normalize backward of dk_j; the tile's other gradient rows are stored as zeros.
+// Pairs of a row meet its accumulators in walk order (chunk, branch, query tile, list entry).
+// Up to kColPairs pairs are gathered into LDS slots in one walk; a column with more walks its
+// lists once per named row.  No matrix cores and no V: per pair two row loads.
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
+  __shared__ int ps_i[kColPairs];    // query row, branch in bit 31
+  __shared__ int ps_jl[kColPairs];   // key row within the tile
+  __shared__ float ps_x[kColPairs];  // exact forward value x
+  __shared__ float ps_w[kColPairs];  // dk weight
+
+  const int l = lane_id();
   const int BH = P.B * P.H;
   const int64_t item = blockIdx.x;  // (key tile, head), in the order of bwd_dkv_fast
   if (item >= (int64_t)BH * P.nkt) return;
@@ -550,146 +566,181 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) bw
   auto base = [&](int slot) {
     return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
   };
+  auto gbase = [&](int slot, int gi) {
+    return (bf16*)P.grad[gi] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
+  };
   const uint32_t* counts = P.pairs + pair_lists(BR, BH, P.nqt) * 4 * kPairCap;
-  const int Nk = P.Nk, j = 32 * kt + n32, jc = min(j, Nk - 1);
-  const bool kvalid = j < Nk;
   const float pw = P.p;
   float lam = 0.f;
   if constexpr (BR == 2) lam = clamp01(*P.lam);
+
+  // Walk the column's lists: body(br, entry) once per step of two lists.
+  auto walk = [&](auto&& body) {
+    for (int q0c = qtf; q0c < P.nqt; q0c += 64) {
+      const int qtl = q0c + l;
+      const bool in = qtl < P.nqt;
+      uint64_t mask[BR];
+      uint32_t cnt_l[BR];
+#pragma unroll
+      for (int br = 0; br < BR; ++br) {
+        const int64_t row = ((int64_t)br * BH + bh) * P.nqt + (in ? qtl : P.nqt - 1);
+        const uint32_t w = P.occ[row * P.occ_w + (kt >> 5)];
+        cnt_l[br] = counts[row];
+        mask[br] = wave_ballot(in && ((w >> (kt & 31)) & 1u));
+      }
+#pragma unroll
+      for (int br = 0; br < BR; ++br) {
+        uint64_t m = mask[br];
+        while (m) {
+          const int qa = __builtin_ctzll(m);
+          m &= m - 1ull;
+          const int qb = m ? __builtin_ctzll(m) : -1;
+          if (m) m &= m - 1ull;
+          const int sel = l < 32 ? qa : qb, e = l & 31;
+          // counts by readlane (uniform lane, read whatever the exec mask): a shuffle under the
+          // select would read the count of a lane the select has switched off
+          const uint32_t ca = (uint32_t)__builtin_amdgcn_readlane((int)cnt_l[br], qa);
+          const uint32_t cb = qb >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)cnt_l[br], qb) : 0u;
+          const uint32_t cnt = l < 32 ? ca : cb;
+          const int qt = q0c + (sel >= 0 ? sel : 0);
+          const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
+          ColEntry c;
+          c.valid = (uint32_t)e < cnt;
+          u32x4 ent = u32x4{0u, 0u, 0u, 0u};
+          c.wk = 0.f;
+          if (c.valid) {
+            ent = *reinterpret_cast<const u32x4*>(P.pairs + lidx * (4 * kPairCap) + 4 * e);
+            c.wk = P.pws[lidx * kPairCap + e];
+          }
+          // x through a bit cast of the whole vector (see load_pairs)
+          const f32x4 ef = __builtin_bit_cast(f32x4, ent);
+          c.key = (int)ent[0];
+          c.i = 32 * qt + (int)ent[1];
+          c.x = ef[2];
+          body(br, c);
+        }
+      }
+    }
+  };
+
+  // ---- first walk: rows named, pairs into the slots while they fit
+  uint32_t np = 0;
+  unsigned visited = 0;
+  uint32_t used[BR];  // key rows named by a pair, per branch
+#pragma unroll
+  for (int br = 0; br < BR; ++br) used[br] = 0u;
+  walk([&](int br, const ColEntry& c) {
+    const bool match = c.valid && (c.key >> 5) == kt;
+    const uint64_t mm = wave_ballot(match);
+    visited += ((mm & 0xffffffffull) ? 1u : 0u) + ((mm >> 32) ? 1u : 0u);
+    const uint32_t slot = np + __builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
+    if (match && slot < (uint32_t)kColPairs) {
+      ps_i[slot] = c.i | (br ? (int)0x80000000u : 0);
+      ps_jl[slot] = c.key & 31;
+      ps_x[slot] = c.x;
+      ps_w[slot] = c.wk;
+    }
+    uint32_t ub = match ? 1u << (c.key & 31) : 0u;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ub |= (uint32_t)__shfl_xor((int)ub, o);
+    used[br] |= ub;
+    np += (uint32_t)__builtin_popcountll(mm);
+  });
+  wave_lds_sync();  // slots written by other lanes
+  const bool slotted = np <= (uint32_t)kColPairs;
+
+  // ---- rows: zeros for the rows no pair names, then each named key row
+  const int nrows = min(32, P.Nk - 32 * kt);
+  const uint32_t uall = BR == 2 ? used[0] | used[BR - 1] : used[0];
+  bf16* dvb = gbase(B_DV, 4);
+  const int64_t sdv = P.s[B_DV][2];
+  zero_rows<D>(dvb + (int64_t)(32 * kt) * sdv, sdv, nrows, uall);
+#pragma unroll
+  for (int br = 0; br < BR; ++br) {
+    const int gslot = br == 0 ? B_DK1 : B_DK2;
+    zero_rows<D>(gbase(gslot, br == 0 ? 1 : 3) + (int64_t)(32 * kt) * P.s[gslot][2], P.s[gslot][2], nrows, used[br]);
+  }
+  // the lane's slot (lanes past np hold no pair and never match)
+  const int sl = (uint32_t)l < np && slotted ? l : 0;
+  const int pi_l = ps_i[sl], pjl_l = (uint32_t)l < np && slotted ? ps_jl[sl] : -1;
+  const float px_l = ps_x[sl], pw_l = ps_w[sl];
   const bf16* dob = base(B_DO);
   const int64_t sdo = P.s[B_DO][2];
 
-  bf16x8 V[NT];  // the lane's key row of v (B operand of dP)
-  {
-    const bf16* r = base(B_V) + (int64_t)jc * P.s[B_V][2];
+  for (uint32_t um = uall; um; um &= um - 1u) {
+    const int jl = __builtin_ctz(um), j = 32 * kt + jl;
+    // the key rows and inverse norms for the normalize backward, issued with the first pairs
+    RowVec<D> kx[BR];
+    float rk[BR];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) V[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
-  }
-  f32x16 AV[ND];
-#pragma unroll
-  for (int c = 0; c < ND; ++c) AV[c] = f32x16{};
-  unsigned visited = 0;
-  zero_tile<D>(qpt);  // rows a batch does not load must hold finite values
-  zero_tile<D>(dpt);
-  __builtin_amdgcn_s_waitcnt(0);
-
-#pragma unroll
-  for (int br = 0; br < BR; ++br) {
-    const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2, gslot = br == 0 ? B_DK1 : B_DK2;
-    const bf16* qb = base(qslot);
-    const int64_t sq = P.s[qslot][2];
-    const float* nq = NORM ? P.norms + norm_base(P, br == 0 ? N_Q1 : N_Q2, bh) : nullptr;
-    const float coef = br == 0 ? 1.f : -lam;
-    const uint32_t* occcol = P.occ + ((int64_t)br * BH + bh) * P.nqt * P.occ_w + (kt >> 5);
-    f32x16 AK[ND];
-#pragma unroll
-    for (int c = 0; c < ND; ++c) AK[c] = f32x16{};
-    bool row_used = false;  // some pair names the lane's key row
-    uint32_t np = 0;        // pairs gathered into the current batch
-
-    // dP, the weights and the accumulation for the batch's np pairs
-    auto flush = [&]() {
-      if (np == 0) return;
-      const int e_l = (uint32_t)l < np ? l : 0;  // pair tile rows past the batch repeat pair 0
-      const int i_l = ps_i[e_l];
-      float rq_l = 1.f;
-      if constexpr (NORM) rq_l = nq[i_l];
-      // only the load instructions that cover pairs (rows past the batch in them repeat pair 0;
-      // rows no instruction covers keep finite older contents, and meet zero weights)
-      for (int u = 0; u < (int)(np + RPI - 1) / RPI; ++u) {
-        const int e = u * RPI + l / CH;
-        const int i = __shfl(i_l, e);
-        const int c = (l % CH) ^ bswz<D>(e);
-        __builtin_amdgcn_global_load_lds((const void*)(qb + (int64_t)i * sq + 8 * c), LDS_PTR(void, qpt + u * RPI * D), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(dob + (int64_t)i * sdo + 8 * c), LDS_PTR(void, dpt + u * RPI * D), 16, 0, 0);
-      }
-      wait_all_loads();
-      // dv += dO^T A first, then dP and dk += Q^T dS: the weight tile, dP and dS never live together
-      {
-        f32x16 EV = f32x16{};
-        for (uint32_t e = 0; e < np; ++e) {
-          const int jl = ps_jl[e];
-          const int rr = crow_index((int)e);
-          const bool mine = n32 == jl && g == (((int)e >> 2) & 1);  // the lane holding (pair e, key jl)
-          row_used |= n32 == jl;
-          const float ev = coef * pow_p<PK>(ps_x[e], pw);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) EV[r] = mine && r == rr ? ev : EV[r];
-        }
-        const bf16x8 V0 = PolBF16::pack_c(EV, 0), V1 = PolBF16::pack_c(EV, 1);
-#pragma unroll
-        for (int c = 0; c < ND; ++c) {
-          AV[c] = PolBF16::mma(tile_tr_frag<D>(dpt, 0, c), V0, AV[c]);
-          AV[c] = PolBF16::mma(tile_tr_frag<D>(dpt, 1, c), V1, AV[c]);
-        }
-      }
-      f32x16 Dp = f32x16{};
-#pragma unroll
-      for (int t = 0; t < NT; ++t) Dp = PolBF16::mma(tile_row_frag<D>(dpt, t), V[t], Dp);
-      f32x16 EK = f32x16{};
-      for (uint32_t e = 0; e < np; ++e) {
-        const int jl = ps_jl[e];
-        const float x = ps_x[e];
-        const float rqi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, rq_l), (int)e));
-        const int rr = crow_index((int)e);
-        const bool mine = n32 == jl && g == (((int)e >> 2) & 1);
-        float dp = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dp = r == rr ? Dp[r] : dp;
-        const float ds = coef * dpow_p<PK>(x, pw) * dp;
-        const float ek = NORM ? ds * rqi : ds;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) EK[r] = mine && r == rr ? ek : EK[r];
-      }
-      const bf16x8 K0 = PolBF16::pack_c(EK, 0), K1 = PolBF16::pack_c(EK, 1);
-#pragma unroll
-      for (int c = 0; c < ND; ++c) {
-        AK[c] = PolBF16::mma(tile_tr_frag<D>(qpt, 0, c), K0, AK[c]);
-        AK[c] = PolBF16::mma(tile_tr_frag<D>(qpt, 1, c), K1, AK[c]);
-      }
-      np = 0;
-      __builtin_amdgcn_s_waitcnt(0);  // every read of the pair tiles and slots done before reuse
-    };
-
-    for (int q0c = qtf; q0c < P.nqt; q0c += 64) {
-      const int qtl = q0c + l;
-      const bool has = qtl < P.nqt && ((occcol[(int64_t)qtl * P.occ_w] >> (kt & 31)) & 1u);
-      const uint32_t cnt_l = has ? counts[((int64_t)br * BH + bh) * P.nqt + qtl] : 0u;
-      for (uint64_t mask = wave_ballot(has); mask; mask &= mask - 1ull) {
-        const int qsel = __builtin_ctzll(mask), qt = q0c + qsel;
-        const uint32_t cnt = (uint32_t)__builtin_amdgcn_readlane((int)cnt_l, qsel);
-        const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
-        const PairLanes PL = load_pairs(P.pairs + lidx * (4 * kPairCap), cnt);
-        const bool match = (uint32_t)l < cnt && (PL.key >> 5) == kt;
-        const uint64_t mm = wave_ballot(match);
-        const uint32_t nm = (uint32_t)__builtin_popcountll(mm);
-        if (nm == 0) continue;
-        ++visited;
-        if (np + nm > 32u) flush();
-        if (match) {  // append in list order
-          const uint32_t slot = np + __builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
-          ps_i[slot] = 32 * qt + PL.row;
-          ps_jl[slot] = PL.key & 31;
-          ps_x[slot] = PL.x;
-        }
-        np += nm;
-      }
-    }
-    flush();
-    if (kvalid) {
-      // the key row for the normalize backward: rows no pair names have a zero gradient
-      GradRow<D> XR = {};
+    for (int br = 0; br < BR; ++br) {
+      kx[br] = RowVec<D>{};
+      rk[br] = 1.f;
       if constexpr (NORM)
-        if (row_used) load_grad_row<D>(base(kslot) + (int64_t)jc * P.s[kslot][2], XR);
-      const float rk = NORM ? P.norms[norm_base(P, br == 0 ? N_K1 : N_K2, bh) + jc] : 1.f;
-      bf16* grow = (bf16*)P.grad[br == 0 ? 1 : 3] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
-                   (int64_t)j * P.s[gslot][2];
-      store_grad_rows<D, NORM>(AK, XR, grow, rk);
+        if ((used[br] >> jl) & 1u) {
+          const int kslot = br == 0 ? B_K1 : B_K2;
+          kx[br] = load_rowvec<D>(base(kslot) + (int64_t)j * P.s[kslot][2]);
+          rk[br] = P.norms[norm_base(P, br == 0 ? N_K1 : N_K2, bh) + j];
+        }
     }
-  }
-  if (kvalid) {
-    bf16* vrow = (bf16*)P.grad[4] + (int64_t)b * P.s[B_DV][0] + (int64_t)h * P.s[B_DV][1] + (int64_t)j * P.s[B_DV][2];
-    store_grad_rows<D, false>(AV, GradRow<D>{}, vrow, 1.f);
+    RowVec<D> av = {}, ak[BR];
+#pragma unroll
+    for (int br = 0; br < BR; ++br) ak[br] = RowVec<D>{};
+    // pairs of the lanes in pm (lane order), up to four row pairs in flight; lane values:
+    // query row | branch << 31, x, dk weight
+    auto accumulate = [&](uint64_t pm, int pi_v, float x_v, float w_v) {
+      while (pm) {
+        int e[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          e[u] = pm ? __builtin_ctzll(pm) : -1;
+          if (pm) pm &= pm - 1ull;
+        }
+        RowVec<D> dor[4], qr[4];
+        int ibr[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          ibr[u] = 0;
+          if (e[u] < 0) continue;
+          const int pi = __builtin_amdgcn_readlane(pi_v, e[u]);
+          const int i = pi & 0x7fffffff;
+          ibr[u] = (pi >> 31) & 1;
+          const int qslot = ibr[u] ? B_Q2 : B_Q1;
+          dor[u] = load_rowvec<D>(dob + (int64_t)i * sdo);
+          qr[u] = load_rowvec<D>(base(qslot) + (int64_t)i * P.s[qslot][2]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (e[u] < 0) continue;
+          const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x_v), e[u]));
+          const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_v), e[u]));
+          const float coef = ibr[u] ? -lam : 1.f;
+          const float wa = coef * pow_p<PK>(x, pw);
+#pragma unroll
+          for (int c = 0; c < RowVec<D>::E; ++c) av.v[c] = __builtin_fmaf(wa, dor[u].v[c], av.v[c]);
+#pragma unroll
+          for (int br = 0; br < BR; ++br)
+            if (ibr[u] == br)
+#pragma unroll
+              for (int c = 0; c < RowVec<D>::E; ++c) ak[br].v[c] = __builtin_fmaf(wk, qr[u].v[c], ak[br].v[c]);
+        }
+      }
+    };
+    if (slotted) {
+      accumulate(wave_ballot(pjl_l == jl), pi_l, px_l, pw_l);
+    } else {
+      walk([&](int br, const ColEntry& c) {
+        accumulate(wave_ballot(c.valid && c.key == j), c.i | (br ? (int)0x80000000u : 0), c.x, c.wk);
+      });
+    }
+    store_rowvec<D>(dvb + (int64_t)j * sdv, av);
+#pragma unroll
+    for (int br = 0; br < BR; ++br) {
+      if (!((used[br] >> jl) & 1u)) continue;  // stored as zeros above
+      const int gslot = br == 0 ? B_DK1 : B_DK2;
+      store_rowvec<D>(gbase(gslot, br == 0 ? 1 : 3) + (int64_t)j * P.s[gslot][2],
+                      normalize_back<D, NORM>(ak[br], kx[br], rk[br]));
+    }
   }
   if (P.stats && l == 0) {
     atomicAdd(P.stats + 0, (unsigned long long)visited);

@@ -171,8 +171,9 @@ size_t tda_fwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, in
 size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim) {
   (void)head_dim;
   if (batch < 1 || heads < 1 || seq_len < 1) return 0;
-  // one (dbeta, dlambda) partial pair per (branch, head, query tile), for two branches
-  return (size_t)(2 * batch * heads * ceil_div(seq_len, 32)) * 2 * sizeof(float);
+  // per (branch, head, query tile), for two branches: one (dbeta, dlambda) partial pair, then
+  // the dk weight of each pair-list slot
+  return (size_t)(2 * batch * heads * ceil_div(seq_len, 32)) * (2 + tda::kPairCap) * sizeof(float);
 }
 
 int32_t tda_validate_fwd(const tda_fwd_args* a) {
@@ -295,6 +296,7 @@ int32_t tda_bwd(const tda_bwd_args* a, void* stream) {
   p.norms = a->normalize ? a->norms : nullptr;
   p.occ = a->occupancy;
   p.ws = static_cast<float*>(a->workspace);
+  p.pws = p.ws + 2 * 2 * (int64_t)a->batch * a->heads * p.nqt;  // after the partial pairs
   p.stats = a->stats;
   p.pairs = a->occupancy ? a->pairs : nullptr;  // the key-major pass finds the lists through the bitmask
   const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};

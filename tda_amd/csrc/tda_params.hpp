@@ -67,6 +67,8 @@ struct BwdParams {
   float* ws;                 // [branches * BH * nqt][2] dbeta / dlambda partials of the dQ pass
   unsigned long long* stats;
   const uint32_t* pairs;     // may be null: the forward's pair lists (used with occ)
+  float* pws;                // [pair lists][kPairCap] dk weight of each pair (workspace), written by
+                             // the query-major pair pass, read by the key-major one
 };
 
 // Kernel-family launchers (return a hipError_t value).  Template selection happens inside.

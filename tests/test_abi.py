@@ -234,7 +234,8 @@ def test_buffer_sizes():
     assert lib.tda_occupancy_words(1, 1, 33, 3) == 0
     assert lib.tda_norms_floats(4, 16, 4096, 2) == 4 * 64 * 4096
     assert lib.tda_norms_floats(1, 8, 128, 1) == 2 * 8 * 128
-    assert lib.tda_bwd_workspace_bytes(4, 16, 4096, 128) == 2 * 64 * 128 * 2 * 4  # two branches
+    # two branches: partial pairs and one dk weight per pair-list slot (32)
+    assert lib.tda_bwd_workspace_bytes(4, 16, 4096, 128) == 2 * 64 * 128 * (2 + 32) * 4
     # bitmask scratch, rounded up to 256 bytes
     assert lib.tda_fwd_workspace_bytes(4, 16, 4096, 2) == 2 * 64 * 128 * 4 * 4
     assert lib.tda_fwd_workspace_bytes(1, 1, 33, 1) == 256

@@ -90,6 +90,7 @@ def test_pair_lists_match_oracle(shape, branches, beta, normalize):
     ((2, 2, 97, 128), 1, 0.2, 1.0, True),    # mixed: tile passes for the overflowing lists
     ((2, 2, 97, 128), 2, 0.2, 1.5, True),
     ((1, 4, 1000, 128), 2, 1.0, 2.0, True),  # sparse: pair passes everywhere
+    ((1, 2, 2500, 128), 2, 1.0, 2.0, True),  # 79 query tiles: lists in both 64-tile chunks of a column
     ((1, 2, 600, 64), 2, 0.8, 3.0, False),
     ((1, 2, 513, 64), 1, 0.0, 2.0, True),    # dense (beta = 0): tile passes everywhere
 ])
@@ -122,3 +123,48 @@ def test_decode_forward_marks_lists_unwritten():
     b = ops.backward(*args, norms=f["norms"], occupancy=f["occ"], pairs=None, q_offset=893)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+def test_heavy_key_column_walks_lists_per_row():
+    """One key row shared by most rows of every query tile: each list fits (about 23 pairs) but
+    key tile 0 collects far more than the 64 pairs the key-major pair pass gathers at once, so
+    that pass walks the lists once per named key row.  Gradients against fp32 autograd of the
+    formula, and against the tile backward."""
+    import tda_amd
+    from tda_amd import ops
+    from tests.helpers import host, tda_grads
+    shape = (1, 1, 256, 64)
+    g = torch.Generator("cpu").manual_seed(21)
+    q1, q2, k1, k2, v, do = (torch.randn(shape, generator=g) for _ in range(6))
+    u = torch.randn(64, generator=g)
+    k1[0, 0, 5] = u
+    rows = torch.tensor([r for r in range(256) if 8 <= r % 32 < 31])
+    q1[0, 0, rows] = u + 0.3 * torch.randn(len(rows), 64, generator=g)
+    q1, q2, k1, k2, v, do = (x.to(torch.bfloat16).cuda() for x in (q1, q2, k1, k2, v, do))
+
+    # the premise: lists that fit, and more than 64 pairs with a key in tile 0
+    bt = torch.full((), 1.5, device="cuda")  # few chance weights beside the shared key's
+    lt = torch.full((), 0.5, device="cuda")
+    norms, occ = ops.side_buffers(shape, 2, True, "cuda", 256)
+    pairs = ops.pair_buffer(shape, 2, "cuda")
+    ops.forward(q1, k1, q2, k2, v, bt, lt, 2.0, True, 2, norms=norms, occupancy=occ, pairs=pairs)
+    counts, ent = _lists(pairs, 2 * 8)
+    assert (counts[:8] <= CAP).all() and (counts[:8] >= 20).all()
+    in_tile0 = sum(int((ent[li, :int(counts[li]), 0] < 32).sum()) for li in range(8))
+    assert in_tile0 > 64
+
+    leaves = [x.clone().requires_grad_(True) for x in (q1, q2, k1, k2, v)]
+    bt.requires_grad_(True)
+    lt.requires_grad_(True)
+    tda_amd.differential_threshold_rela_triton(*leaves, bt, lt, relu_power=2.0, normalize=True).backward(do)
+    ref = tda_grads(*(host(x, torch.float32) for x in (q1, q2, k1, k2, v)), host(do, torch.float32),
+                    1.5, 0.5, 2.0, True, 2, dtype=torch.float32)
+    for x, name in zip(leaves, ["dq1", "dq2", "dk1", "dk2", "dv"]):
+        assert rel_err(x.grad.float().cpu(), ref[name]) <= 2e-2, name
+    tiles = ops.backward(q1, k1, q2, k2, v, do, bt.detach(), lt.detach(), 2.0, True, 2,
+                         norms=norms, occupancy=occ, pairs=None)
+    with_pairs = ops.backward(q1, k1, q2, k2, v, do, bt.detach(), lt.detach(), 2.0, True, 2,
+                              norms=norms, occupancy=occ, pairs=pairs)
+    for a, c in zip(with_pairs, tiles):
+        if a is not None:
+            assert rel_err(a.float().cpu(), c.float().cpu()) <= 1e-2
