@@ -414,6 +414,31 @@ __device__ __forceinline__ void zero_rows(bf16* tile0, int64_t st, int nrows, ui
   }
 }
 
+// A pair list sorted by query row, then list order: lane s < n holds the entry of rank s, and
+// e = its index in the list; lanes past n hold their own slot (a permutation of the lanes, so
+// the forward permutes below write every lane once).
+struct SortedPairs {
+  int key, row, e;
+  float x;
+};
+__device__ __forceinline__ SortedPairs sort_pairs(const PairLanes& PL, uint32_t n) {
+  const int l = lane_id();
+  int rank = l;
+  if ((uint32_t)l < n) {
+    rank = 0;
+    for (uint32_t f = 0; f < n; ++f) {
+      const int rf = __builtin_amdgcn_readlane(PL.row, (int)f);
+      rank += rf < PL.row || (rf == PL.row && (int)f < l) ? 1 : 0;
+    }
+  }
+  SortedPairs S;
+  S.key = __builtin_amdgcn_ds_permute(4 * rank, PL.key);
+  S.row = __builtin_amdgcn_ds_permute(4 * rank, PL.row);
+  S.e = __builtin_amdgcn_ds_permute(4 * rank, l);
+  S.x = __builtin_bit_cast(float, __builtin_amdgcn_ds_permute(4 * rank, __builtin_bit_cast(int, PL.x)));
+  return S;
+}
+
 template <int D, int BR, int PK, bool NORM>
 __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   const int l = lane_id();
@@ -460,34 +485,68 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   const int q0 = 32 * qt;
   zero_rows<D>(gb + (int64_t)q0 * sg, sg, min(32, P.Nq - q0), used);
 
+  // The pairs sorted by query row, then list order: lane s gets the pair of rank s (lanes past
+  // the count keep their own slot, so the ranks form a permutation of the lanes).
+  const SortedPairs SP = sort_pairs(PL, npairs);
+
+  // Rows in increasing order, each row's pairs in list order; the loads of four pairs at a time
+  // are in flight together, a row is finished when the next pair names another.
   float pb = 0.f, pl = 0.f;  // dbeta, dlambda partials (the same in every lane)
-  float wkl = 0.f;           // lane e: the dk weight of pair e, for the key-major pair pass
-  for (uint32_t m = used; m; m &= m - 1u) {
-    const int il = __builtin_ctz(m), i = q0 + il;
-    const RowVec<D> dor = load_rowvec<D>(dob + (int64_t)i * sdo);
-    RowVec<D> xr = {};
-    if constexpr (NORM) xr = load_rowvec<D>(qb + (int64_t)i * sq);
-    const float rq = NORM ? nq[i] : 1.f;
-    const float ci = tau_coeff(P.qoff + i, P.inv_d);
-    RowVec<D> acc = {};
-    for (uint32_t e = 0; e < npairs; ++e) {
-      if (__builtin_amdgcn_readlane(PL.row, (int)e) != il) continue;
-      const int j = __builtin_amdgcn_readlane(PL.key, (int)e);
-      const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, PL.x), (int)e));
-      const RowVec<D> kr = load_rowvec<D>(kb + (int64_t)j * sk);
-      const RowVec<D> vr = load_rowvec<D>(vb + (int64_t)j * sv);
-      const float rk = NORM ? nk[j] : 1.f;
-      const float dp = row_dot<D>(dor, vr);
-      const float ds = coef * dpow_p<PK>(x, pw) * dp;
-      pb = __builtin_fmaf(-ci, ds, pb);
-      if (want_l) pl = __builtin_fmaf(-pow_p<PK>(x, pw), dp, pl);
-      const float w = NORM ? ds * rk : ds;
-      wkl = l == (int)e ? (NORM ? ds * rq : ds) : wkl;
+  float wks = 0.f;           // lane s: the dk weight of sorted pair s
+  int cur = -1;              // row being accumulated
+  RowVec<D> acc = {}, cur_x = {};
+  float cur_r = 1.f;
+  auto finish = [&]() {
+    if (cur >= 0) store_rowvec<D>(gb + (int64_t)(q0 + cur) * sg, normalize_back<D, NORM>(acc, cur_x, cur_r));
+  };
+  for (uint32_t s0 = 0; s0 < npairs; s0 += 4) {
+    int il[4], jj[4];
+    float xx[4], rq[4], rk[4];
+    RowVec<D> dor[4], qr[4], kr[4], vr[4];
 #pragma unroll
-      for (int c = 0; c < RowVec<D>::E; ++c) acc.v[c] = __builtin_fmaf(w, kr.v[c], acc.v[c]);
+    for (int u = 0; u < 4; ++u) {
+      const int s = (int)s0 + u;
+      if ((uint32_t)s >= npairs) continue;
+      il[u] = __builtin_amdgcn_readlane(SP.row, s);
+      jj[u] = __builtin_amdgcn_readlane(SP.key, s);
+      xx[u] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, SP.x), s));
+      const int i = q0 + il[u];
+      dor[u] = load_rowvec<D>(dob + (int64_t)i * sdo);
+      kr[u] = load_rowvec<D>(kb + (int64_t)jj[u] * sk);
+      vr[u] = load_rowvec<D>(vb + (int64_t)jj[u] * sv);
+      qr[u] = RowVec<D>{};
+      rq[u] = rk[u] = 1.f;
+      if constexpr (NORM) {
+        qr[u] = load_rowvec<D>(qb + (int64_t)i * sq);
+        rq[u] = nq[i];
+        rk[u] = nk[jj[u]];
+      }
     }
-    store_rowvec<D>(gb + (int64_t)i * sg, normalize_back<D, NORM>(acc, xr, rq));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = (int)s0 + u;
+      if ((uint32_t)s >= npairs) continue;
+      if (il[u] != cur) {
+        finish();
+        acc = RowVec<D>{};
+        cur = il[u];
+        cur_x = qr[u];
+        cur_r = rq[u];
+      }
+      const float ci = tau_coeff(P.qoff + q0 + il[u], P.inv_d);
+      const float dp = row_dot<D>(dor[u], vr[u]);
+      const float ds = coef * dpow_p<PK>(xx[u], pw) * dp;
+      pb = __builtin_fmaf(-ci, ds, pb);
+      if (want_l) pl = __builtin_fmaf(-pow_p<PK>(xx[u], pw), dp, pl);
+      const float w = NORM ? ds * rk[u] : ds;
+      wks = l == s ? (NORM ? ds * rq[u] : ds) : wks;
+#pragma unroll
+      for (int c = 0; c < RowVec<D>::E; ++c) acc.v[c] = __builtin_fmaf(w, kr[u].v[c], acc.v[c]);
+    }
   }
+  finish();
+  // back to list order: lane s sends its weight to the lane of its list entry
+  const float wkl = __builtin_bit_cast(float, __builtin_amdgcn_ds_permute(4 * SP.e, __builtin_bit_cast(int, wks)));
   if ((uint32_t)l < npairs) P.pws[lidx * kPairCap + l] = wkl;
   if (l == 0) {
     P.ws[2 * item + 0] = pb;
@@ -530,6 +589,7 @@ constexpr int kColPairs = 64;
 // One entry of a column's pair list as seen by one lane of the key-major pair pass.
 struct ColEntry {
   bool valid;  // the lane holds an entry
+  int br;      // branch of the lane's list
   int key;     // key index j
   int i;       // query row
   float x;     // exact forward value
@@ -561,7 +621,6 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
   const int kt = (int)(item / BH), bh = (int)(item % BH);
   const int b = bh / P.H, h = bh % P.H;
   const int qtf = qt_first(kt, P.qoff);
-  if (column_overflows<BR>(P, bh, kt, qtf)) return;  // bwd_dkv_fast takes the key tile
 
   auto base = [&](int slot) {
     return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
@@ -574,53 +633,88 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
   float lam = 0.f;
   if constexpr (BR == 2) lam = clamp01(*P.lam);
 
-  // Walk the column's lists: body(br, entry) once per step of two lists.
-  auto walk = [&](auto&& body) {
-    for (int q0c = qtf; q0c < P.nqt; q0c += 64) {
-      const int qtl = q0c + l;
-      const bool in = qtl < P.nqt;
-      uint64_t mask[BR];
-      uint32_t cnt_l[BR];
+  // Walk the column's lists in the order (query-tile chunk of 64, branch, query tile): the
+  // bitmask bits and counts of 128 query tiles per load round, then four lists per step, all
+  // four loaded before the first is used (lanes 0-31 and 32-63 take one list each, two rounds);
+  // body(entry) once per round.  Returns false, before any body call of that chunk pair, when a
+  // list of the column did not fit (the same test as column_overflows: the tile pass takes the
+  // key tile); the caller has then written nothing.
+  auto walk = [&](auto&& body) -> bool {
+    for (int q0c = qtf; q0c < P.nqt; q0c += 128) {
+      uint64_t mask[2 * BR];  // [chunk * BR + branch]
+      uint32_t cnt_l[2 * BR];
+      bool ovf = false;
 #pragma unroll
-      for (int br = 0; br < BR; ++br) {
+      for (int k = 0; k < 2 * BR; ++k) {
+        const int c = k / BR, br = k % BR;
+        const int qtl = q0c + 64 * c + l;
+        const bool in = qtl < P.nqt;
         const int64_t row = ((int64_t)br * BH + bh) * P.nqt + (in ? qtl : P.nqt - 1);
         const uint32_t w = P.occ[row * P.occ_w + (kt >> 5)];
-        cnt_l[br] = counts[row];
-        mask[br] = wave_ballot(in && ((w >> (kt & 31)) & 1u));
+        cnt_l[k] = counts[row];
+        const bool has = in && ((w >> (kt & 31)) & 1u);
+        ovf = ovf || (has && cnt_l[k] > (uint32_t)kPairCap);
+        mask[k] = wave_ballot(has);
       }
+      if (wave_ballot(ovf) != 0ull) return false;
+      while (true) {
+        int ix[4], sx[4];
+        uint32_t cx[4];
 #pragma unroll
-      for (int br = 0; br < BR; ++br) {
-        uint64_t m = mask[br];
-        while (m) {
-          const int qa = __builtin_ctzll(m);
-          m &= m - 1ull;
-          const int qb = m ? __builtin_ctzll(m) : -1;
-          if (m) m &= m - 1ull;
-          const int sel = l < 32 ? qa : qb, e = l & 31;
-          // counts by readlane (uniform lane, read whatever the exec mask): a shuffle under the
-          // select would read the count of a lane the select has switched off
-          const uint32_t ca = (uint32_t)__builtin_amdgcn_readlane((int)cnt_l[br], qa);
-          const uint32_t cb = qb >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)cnt_l[br], qb) : 0u;
-          const uint32_t cnt = l < 32 ? ca : cb;
-          const int qt = q0c + (sel >= 0 ? sel : 0);
-          const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
-          ColEntry c;
-          c.valid = (uint32_t)e < cnt;
-          u32x4 ent = u32x4{0u, 0u, 0u, 0u};
-          c.wk = 0.f;
-          if (c.valid) {
-            ent = *reinterpret_cast<const u32x4*>(P.pairs + lidx * (4 * kPairCap) + 4 * e);
-            c.wk = P.pws[lidx * kPairCap + e];
+        for (int u = 0; u < 4; ++u) {  // next four lists
+          ix[u] = -1;
+          sx[u] = 0;
+          cx[u] = 0u;
+          bool found = false;
+#pragma unroll
+          for (int k = 0; k < 2 * BR; ++k)
+            if (!found && mask[k]) {
+              found = true;
+              ix[u] = k;
+              sx[u] = __builtin_ctzll(mask[k]);
+              mask[k] &= mask[k] - 1ull;
+              cx[u] = (uint32_t)__builtin_amdgcn_readlane((int)cnt_l[k], sx[u]);
+            }
+        }
+        if (ix[0] < 0) break;
+        u32x4 ent[2];
+        float wk[2];
+        int brl[2], qtl[2];
+        bool valid[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int idx = l < 32 ? ix[2 * r] : ix[2 * r + 1];
+          const int sel = l < 32 ? sx[2 * r] : sx[2 * r + 1];
+          const uint32_t cnt = l < 32 ? cx[2 * r] : cx[2 * r + 1];
+          const int e = l & 31;
+          brl[r] = idx >= 0 ? idx % BR : 0;
+          qtl[r] = q0c + 64 * (idx >= 0 ? idx / BR : 0) + sel;
+          valid[r] = idx >= 0 && (uint32_t)e < cnt;
+          const int64_t lidx = ((int64_t)brl[r] * BH + bh) * P.nqt + qtl[r];
+          ent[r] = u32x4{0u, 0u, 0u, 0u};
+          wk[r] = 0.f;
+          if (valid[r]) {
+            ent[r] = *reinterpret_cast<const u32x4*>(P.pairs + lidx * (4 * kPairCap) + 4 * e);
+            wk[r] = P.pws[lidx * kPairCap + e];
           }
+        }
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          if (ix[2 * r] < 0) break;
           // x through a bit cast of the whole vector (see load_pairs)
-          const f32x4 ef = __builtin_bit_cast(f32x4, ent);
-          c.key = (int)ent[0];
-          c.i = 32 * qt + (int)ent[1];
+          const f32x4 ef = __builtin_bit_cast(f32x4, ent[r]);
+          ColEntry c;
+          c.valid = valid[r];
+          c.br = brl[r];
+          c.key = (int)ent[r][0];
+          c.i = 32 * qtl[r] + (int)ent[r][1];
           c.x = ef[2];
-          body(br, c);
+          c.wk = wk[r];
+          body(c);
         }
       }
     }
+    return true;
   };
 
   // ---- first walk: rows named, pairs into the slots while they fit
@@ -629,23 +723,27 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
   uint32_t used[BR];  // key rows named by a pair, per branch
 #pragma unroll
   for (int br = 0; br < BR; ++br) used[br] = 0u;
-  walk([&](int br, const ColEntry& c) {
+  const bool fits = walk([&](const ColEntry& c) {
     const bool match = c.valid && (c.key >> 5) == kt;
     const uint64_t mm = wave_ballot(match);
     visited += ((mm & 0xffffffffull) ? 1u : 0u) + ((mm >> 32) ? 1u : 0u);
     const uint32_t slot = np + __builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
     if (match && slot < (uint32_t)kColPairs) {
-      ps_i[slot] = c.i | (br ? (int)0x80000000u : 0);
+      ps_i[slot] = c.i | (c.br ? (int)0x80000000u : 0);
       ps_jl[slot] = c.key & 31;
       ps_x[slot] = c.x;
       ps_w[slot] = c.wk;
     }
-    uint32_t ub = match ? 1u << (c.key & 31) : 0u;
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ub |= (uint32_t)__shfl_xor((int)ub, o);
-    used[br] |= ub;
+    for (int br = 0; br < BR; ++br) {
+      uint32_t ub = match && c.br == br ? 1u << (c.key & 31) : 0u;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) ub |= (uint32_t)__shfl_xor((int)ub, o);
+      used[br] |= ub;
+    }
     np += (uint32_t)__builtin_popcountll(mm);
   });
+  if (!fits) return;  // bwd_dkv_fast takes the key tile
   wave_lds_sync();  // slots written by other lanes
   const bool slotted = np <= (uint32_t)kColPairs;
 
@@ -660,18 +758,25 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
     const int gslot = br == 0 ? B_DK1 : B_DK2;
     zero_rows<D>(gbase(gslot, br == 0 ? 1 : 3) + (int64_t)(32 * kt) * P.s[gslot][2], P.s[gslot][2], nrows, used[br]);
   }
-  // the lane's slot (lanes past np hold no pair and never match)
-  const int sl = (uint32_t)l < np && slotted ? l : 0;
-  const int pi_l = ps_i[sl], pjl_l = (uint32_t)l < np && slotted ? ps_jl[sl] : -1;
-  const float px_l = ps_x[sl], pw_l = ps_w[sl];
   const bf16* dob = base(B_DO);
   const int64_t sdo = P.s[B_DO][2];
-
-  for (uint32_t um = uall; um; um &= um - 1u) {
-    const int jl = __builtin_ctz(um), j = 32 * kt + jl;
-    // the key rows and inverse norms for the normalize backward, issued with the first pairs
-    RowVec<D> kx[BR];
-    float rk[BR];
+  // key row jl's finished rows: dv, and dk of each branch whose pairs name it (the others were
+  // stored as zeros above)
+  auto store_key_row = [&](int jl, const RowVec<D>& av, const RowVec<D>(&ak)[BR], const RowVec<D>(&kx)[BR],
+                           const float(&rk)[BR]) {
+    const int j = 32 * kt + jl;
+    store_rowvec<D>(dvb + (int64_t)j * sdv, av);
+#pragma unroll
+    for (int br = 0; br < BR; ++br) {
+      if (!((used[br] >> jl) & 1u)) continue;
+      const int gslot = br == 0 ? B_DK1 : B_DK2;
+      store_rowvec<D>(gbase(gslot, br == 0 ? 1 : 3) + (int64_t)j * P.s[gslot][2],
+                      normalize_back<D, NORM>(ak[br], kx[br], rk[br]));
+    }
+  };
+  // the key rows and inverse norms of key row jl for the normalize backward
+  auto load_key_rows = [&](int jl, RowVec<D>(&kx)[BR], float(&rk)[BR]) {
+    const int j = 32 * kt + jl;
 #pragma unroll
     for (int br = 0; br < BR; ++br) {
       kx[br] = RowVec<D>{};
@@ -683,63 +788,129 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
           rk[br] = P.norms[norm_base(P, br == 0 ? N_K1 : N_K2, bh) + j];
         }
     }
-    RowVec<D> av = {}, ak[BR];
-#pragma unroll
-    for (int br = 0; br < BR; ++br) ak[br] = RowVec<D>{};
-    // pairs of the lanes in pm (lane order), up to four row pairs in flight; lane values:
-    // query row | branch << 31, x, dk weight
-    auto accumulate = [&](uint64_t pm, int pi_v, float x_v, float w_v) {
-      while (pm) {
-        int e[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          e[u] = pm ? __builtin_ctzll(pm) : -1;
-          if (pm) pm &= pm - 1ull;
-        }
-        RowVec<D> dor[4], qr[4];
-        int ibr[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          ibr[u] = 0;
-          if (e[u] < 0) continue;
-          const int pi = __builtin_amdgcn_readlane(pi_v, e[u]);
-          const int i = pi & 0x7fffffff;
-          ibr[u] = (pi >> 31) & 1;
-          const int qslot = ibr[u] ? B_Q2 : B_Q1;
-          dor[u] = load_rowvec<D>(dob + (int64_t)i * sdo);
-          qr[u] = load_rowvec<D>(base(qslot) + (int64_t)i * P.s[qslot][2]);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (e[u] < 0) continue;
-          const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x_v), e[u]));
-          const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w_v), e[u]));
-          const float coef = ibr[u] ? -lam : 1.f;
-          const float wa = coef * pow_p<PK>(x, pw);
-#pragma unroll
-          for (int c = 0; c < RowVec<D>::E; ++c) av.v[c] = __builtin_fmaf(wa, dor[u].v[c], av.v[c]);
-#pragma unroll
-          for (int br = 0; br < BR; ++br)
-            if (ibr[u] == br)
-#pragma unroll
-              for (int c = 0; c < RowVec<D>::E; ++c) ak[br].v[c] = __builtin_fmaf(wk, qr[u].v[c], ak[br].v[c]);
-        }
+  };
+
+  if (slotted) {
+    // The slots sorted by key row, then slot order: lane s gets the pair of rank s (lanes past
+    // np keep their own slot).  Then the pairs in that order, the loads of four at a time in
+    // flight together; a key row is finished when the next pair names another.
+    const int sl = (uint32_t)l < np ? l : 0;
+    const int pi_l = ps_i[sl], pjl_l = ps_jl[sl];
+    const float px_l = ps_x[sl], pw_l = ps_w[sl];
+    int rank = l;
+    if ((uint32_t)l < np) {
+      rank = 0;
+      for (uint32_t f = 0; f < np; ++f) {
+        const int jf = __builtin_amdgcn_readlane(pjl_l, (int)f);
+        rank += jf < pjl_l || (jf == pjl_l && (int)f < l) ? 1 : 0;
       }
-    };
-    if (slotted) {
-      accumulate(wave_ballot(pjl_l == jl), pi_l, px_l, pw_l);
-    } else {
-      walk([&](int br, const ColEntry& c) {
-        accumulate(wave_ballot(c.valid && c.key == j), c.i | (br ? (int)0x80000000u : 0), c.x, c.wk);
-      });
     }
-    store_rowvec<D>(dvb + (int64_t)j * sdv, av);
+    const int s_i = __builtin_amdgcn_ds_permute(4 * rank, pi_l);
+    const int s_jl = __builtin_amdgcn_ds_permute(4 * rank, pjl_l);
+    const int s_x = __builtin_amdgcn_ds_permute(4 * rank, __builtin_bit_cast(int, px_l));
+    const int s_w = __builtin_amdgcn_ds_permute(4 * rank, __builtin_bit_cast(int, pw_l));
+    int cur = -1;
+    RowVec<D> av = {}, ak[BR], kx[BR];
+    float rk[BR];
 #pragma unroll
     for (int br = 0; br < BR; ++br) {
-      if (!((used[br] >> jl) & 1u)) continue;  // stored as zeros above
-      const int gslot = br == 0 ? B_DK1 : B_DK2;
-      store_rowvec<D>(gbase(gslot, br == 0 ? 1 : 3) + (int64_t)j * P.s[gslot][2],
-                      normalize_back<D, NORM>(ak[br], kx[br], rk[br]));
+      ak[br] = kx[br] = RowVec<D>{};
+      rk[br] = 1.f;
+    }
+    for (uint32_t s0 = 0; s0 < np; s0 += 4) {
+      int jl[4], ibr[4];
+      RowVec<D> dor[4], qr[4], kxu[4][BR];
+      float rku[4][BR];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = (int)s0 + u;
+        ibr[u] = 0;
+        if ((uint32_t)s >= np) continue;
+        jl[u] = __builtin_amdgcn_readlane(s_jl, s);
+        const int pi = __builtin_amdgcn_readlane(s_i, s);
+        const int i = pi & 0x7fffffff;
+        ibr[u] = (pi >> 31) & 1;
+        const int qslot = ibr[u] ? B_Q2 : B_Q1;
+        dor[u] = load_rowvec<D>(dob + (int64_t)i * sdo);
+        qr[u] = load_rowvec<D>(base(qslot) + (int64_t)i * P.s[qslot][2]);
+        load_key_rows(jl[u], kxu[u], rku[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = (int)s0 + u;
+        if ((uint32_t)s >= np) continue;
+        if (jl[u] != cur) {
+          if (cur >= 0) store_key_row(cur, av, ak, kx, rk);
+          cur = jl[u];
+          av = RowVec<D>{};
+#pragma unroll
+          for (int br = 0; br < BR; ++br) {
+            ak[br] = RowVec<D>{};
+            kx[br] = kxu[u][br];
+            rk[br] = rku[u][br];
+          }
+        }
+        const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(s_x, s));
+        const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(s_w, s));
+        const float wa = (ibr[u] ? -lam : 1.f) * pow_p<PK>(x, pw);
+#pragma unroll
+        for (int c = 0; c < RowVec<D>::E; ++c) av.v[c] = __builtin_fmaf(wa, dor[u].v[c], av.v[c]);
+#pragma unroll
+        for (int br = 0; br < BR; ++br)
+          if (ibr[u] == br)
+#pragma unroll
+            for (int c = 0; c < RowVec<D>::E; ++c) ak[br].v[c] = __builtin_fmaf(wk, qr[u].v[c], ak[br].v[c]);
+      }
+    }
+    if (cur >= 0) store_key_row(cur, av, ak, kx, rk);
+  } else {
+    // more pairs than slots: each named key row walks the lists for its own pairs (lane order
+    // within a step), up to four row pairs in flight
+    for (uint32_t um = uall; um; um &= um - 1u) {
+      const int jl = __builtin_ctz(um), j = 32 * kt + jl;
+      RowVec<D> kx[BR];
+      float rk[BR];
+      load_key_rows(jl, kx, rk);
+      RowVec<D> av = {}, ak[BR];
+#pragma unroll
+      for (int br = 0; br < BR; ++br) ak[br] = RowVec<D>{};
+      walk([&](const ColEntry& c) {
+        uint64_t pm = wave_ballot(c.valid && c.key == j);
+        while (pm) {
+          int e[4], ibr[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            e[u] = pm ? __builtin_ctzll(pm) : -1;
+            if (pm) pm &= pm - 1ull;
+          }
+          RowVec<D> dor[4], qr[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            ibr[u] = 0;
+            if (e[u] < 0) continue;
+            const int i = __builtin_amdgcn_readlane(c.i, e[u]);
+            ibr[u] = __builtin_amdgcn_readlane(c.br, e[u]);
+            const int qslot = ibr[u] ? B_Q2 : B_Q1;
+            dor[u] = load_rowvec<D>(dob + (int64_t)i * sdo);
+            qr[u] = load_rowvec<D>(base(qslot) + (int64_t)i * P.s[qslot][2]);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (e[u] < 0) continue;
+            const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c.x), e[u]));
+            const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c.wk), e[u]));
+            const float wa = (ibr[u] ? -lam : 1.f) * pow_p<PK>(x, pw);
+#pragma unroll
+            for (int cc = 0; cc < RowVec<D>::E; ++cc) av.v[cc] = __builtin_fmaf(wa, dor[u].v[cc], av.v[cc]);
+#pragma unroll
+            for (int br = 0; br < BR; ++br)
+              if (ibr[u] == br)
+#pragma unroll
+                for (int cc = 0; cc < RowVec<D>::E; ++cc) ak[br].v[cc] = __builtin_fmaf(wk, qr[u].v[cc], ak[br].v[cc]);
+          }
+        }
+      });
+      store_key_row(jl, av, ak, kx, rk);
     }
   }
   if (P.stats && l == 0) {
