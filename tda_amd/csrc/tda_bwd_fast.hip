@@ -339,8 +339,8 @@ __global__ void __launch_bounds__(64 * kBwdWaves) __attribute__((amdgpu_waves_pe
   const float pb = wave_sum(-ci * bsum);
   const float pl = wave_sum(-lsum);
   if (l == 0) {
-    P.ws[2 * item + 0] = pb;
-    P.ws[2 * item + 1] = pl;
+    P.ws[2 * lidx + 0] = pb;  // slot of (branch, head, query tile), whichever pass takes it
+    P.ws[2 * lidx + 1] = pl;
     if (P.stats) {
       atomicAdd(P.stats + 0, (unsigned long long)visited);
       atomicAdd(P.stats + 1, (unsigned long long)computed);
@@ -374,6 +374,25 @@ __device__ __forceinline__ RowVec<D> load_rowvec(const bf16* row) {
     r.v[0] = (float)row[l];
   }
   return r;
+}
+// The lane's D/64 elements of a row as loaded (bf16 bits, element 2l in the low half for
+// D = 128): one register per row while loads are in flight.
+template <int D>
+struct RowRaw {
+  uint32_t u;
+};
+template <int D>
+__device__ __forceinline__ RowRaw<D> load_rowraw(const bf16* row) {
+  const int l = lane_id();
+  if constexpr (D == 128) return RowRaw<D>{*reinterpret_cast<const uint32_t*>(row + 2 * l)};
+  else return RowRaw<D>{(uint32_t)*reinterpret_cast<const uint16_t*>(row + l)};
+}
+template <int D>
+__device__ __forceinline__ RowVec<D> unpack(RowRaw<D> r) {
+  RowVec<D> v;
+  v.v[0] = __uint_as_float(r.u << 16);
+  if constexpr (D == 128) v.v[1] = __uint_as_float(r.u & 0xffff0000u);
+  return v;
 }
 template <int D>
 __device__ __forceinline__ void store_rowvec(bf16* row, const RowVec<D>& r) {
@@ -414,6 +433,9 @@ __device__ __forceinline__ void zero_rows(bf16* tile0, int64_t st, int nrows, ui
   }
 }
 
+// Pairs whose row loads the pair passes keep in flight together.
+constexpr int kRowBatch = 8;
+
 // A pair list sorted by query row, then list order: lane s < n holds the entry of rank s, and
 // e = its index in the list; lanes past n hold their own slot (a permutation of the lanes, so
 // the forward permutes below write every lane once).
@@ -443,11 +465,13 @@ template <int D, int BR, int PK, bool NORM>
 __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   const int l = lane_id();
   const int BH = P.B * P.H;
-  const int64_t item = blockIdx.x;  // (query tile, head, branch), in the order of bwd_dq_fast
+  // (query tile, head, branch), query tiles ascending: the early rows' thresholds are the
+  // lowest, their lists the longest
+  const int64_t item = blockIdx.x;
   if (item >= (int64_t)BR * BH * P.nqt) return;
   const int br = BR == 2 ? (int)(item & 1) : 0;
   const int64_t rest = BR == 2 ? item >> 1 : item;
-  const int qt = P.nqt - 1 - (int)(rest / BH);
+  const int qt = (int)(rest / BH);
   const int bh = (int)(rest % BH);
   const int b = bh / P.H, h = bh % P.H;
   const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
@@ -489,8 +513,8 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   // the count keep their own slot, so the ranks form a permutation of the lanes).
   const SortedPairs SP = sort_pairs(PL, npairs);
 
-  // Rows in increasing order, each row's pairs in list order; the loads of four pairs at a time
-  // are in flight together, a row is finished when the next pair names another.
+  // Rows in increasing order, each row's pairs in list order; the loads of kRowBatch pairs at a
+  // time are in flight together, a row is finished when the next pair names another.
   float pb = 0.f, pl = 0.f;  // dbeta, dlambda partials (the same in every lane)
   float wks = 0.f;           // lane s: the dk weight of sorted pair s
   int cur = -1;              // row being accumulated
@@ -499,49 +523,50 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   auto finish = [&]() {
     if (cur >= 0) store_rowvec<D>(gb + (int64_t)(q0 + cur) * sg, normalize_back<D, NORM>(acc, cur_x, cur_r));
   };
-  for (uint32_t s0 = 0; s0 < npairs; s0 += 4) {
-    int il[4], jj[4];
-    float xx[4], rq[4], rk[4];
-    RowVec<D> dor[4], qr[4], kr[4], vr[4];
+  for (uint32_t s0 = 0; s0 < npairs; s0 += kRowBatch) {
+    int il[kRowBatch], jj[kRowBatch];
+    float rq[kRowBatch], rk[kRowBatch];
+    RowRaw<D> dor[kRowBatch], qr[kRowBatch], kr[kRowBatch], vr[kRowBatch];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kRowBatch; ++u) {
       const int s = (int)s0 + u;
       if ((uint32_t)s >= npairs) continue;
       il[u] = __builtin_amdgcn_readlane(SP.row, s);
       jj[u] = __builtin_amdgcn_readlane(SP.key, s);
-      xx[u] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, SP.x), s));
       const int i = q0 + il[u];
-      dor[u] = load_rowvec<D>(dob + (int64_t)i * sdo);
-      kr[u] = load_rowvec<D>(kb + (int64_t)jj[u] * sk);
-      vr[u] = load_rowvec<D>(vb + (int64_t)jj[u] * sv);
-      qr[u] = RowVec<D>{};
+      dor[u] = load_rowraw<D>(dob + (int64_t)i * sdo);
+      kr[u] = load_rowraw<D>(kb + (int64_t)jj[u] * sk);
+      vr[u] = load_rowraw<D>(vb + (int64_t)jj[u] * sv);
+      qr[u] = RowRaw<D>{0u};
       rq[u] = rk[u] = 1.f;
       if constexpr (NORM) {
-        qr[u] = load_rowvec<D>(qb + (int64_t)i * sq);
+        qr[u] = load_rowraw<D>(qb + (int64_t)i * sq);
         rq[u] = nq[i];
         rk[u] = nk[jj[u]];
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kRowBatch; ++u) {
       const int s = (int)s0 + u;
       if ((uint32_t)s >= npairs) continue;
       if (il[u] != cur) {
         finish();
         acc = RowVec<D>{};
         cur = il[u];
-        cur_x = qr[u];
+        cur_x = unpack<D>(qr[u]);
         cur_r = rq[u];
       }
+      const float xx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, SP.x), s));
       const float ci = tau_coeff(P.qoff + q0 + il[u], P.inv_d);
-      const float dp = row_dot<D>(dor[u], vr[u]);
-      const float ds = coef * dpow_p<PK>(xx[u], pw) * dp;
+      const float dp = row_dot<D>(unpack<D>(dor[u]), unpack<D>(vr[u]));
+      const float ds = coef * dpow_p<PK>(xx, pw) * dp;
       pb = __builtin_fmaf(-ci, ds, pb);
-      if (want_l) pl = __builtin_fmaf(-pow_p<PK>(xx[u], pw), dp, pl);
+      if (want_l) pl = __builtin_fmaf(-pow_p<PK>(xx, pw), dp, pl);
       const float w = NORM ? ds * rk[u] : ds;
       wks = l == s ? (NORM ? ds * rq[u] : ds) : wks;
+      const RowVec<D> kv = unpack<D>(kr[u]);
 #pragma unroll
-      for (int c = 0; c < RowVec<D>::E; ++c) acc.v[c] = __builtin_fmaf(w, kr[u].v[c], acc.v[c]);
+      for (int c = 0; c < RowVec<D>::E; ++c) acc.v[c] = __builtin_fmaf(w, kv.v[c], acc.v[c]);
     }
   }
   finish();
@@ -549,8 +574,8 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   const float wkl = __builtin_bit_cast(float, __builtin_amdgcn_ds_permute(4 * SP.e, __builtin_bit_cast(int, wks)));
   if ((uint32_t)l < npairs) P.pws[lidx * kPairCap + l] = wkl;
   if (l == 0) {
-    P.ws[2 * item + 0] = pb;
-    P.ws[2 * item + 1] = pl;
+    P.ws[2 * lidx + 0] = pb;  // slot of (branch, head, query tile), whichever pass takes it
+    P.ws[2 * lidx + 1] = pl;
     if (P.stats) {
       atomicAdd(P.stats + 0, (unsigned long long)tiles);
       atomicAdd(P.stats + 1, (unsigned long long)tiles);
@@ -585,6 +610,8 @@ __device__ __forceinline__ bool column_overflows(const BwdParams& P, int bh, int
 
 // LDS slots of the key-major pair pass: pairs of one column gathered at once.
 constexpr int kColPairs = 64;
+// List-load rounds of one walk step of the key-major pair pass (two lists per round).
+constexpr int kWalkRounds = 4;
 
 // One entry of a column's pair list as seen by one lane of the key-major pair pass.
 struct ColEntry {
@@ -634,9 +661,9 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
   if constexpr (BR == 2) lam = clamp01(*P.lam);
 
   // Walk the column's lists in the order (query-tile chunk of 64, branch, query tile): the
-  // bitmask bits and counts of 128 query tiles per load round, then four lists per step, all
-  // four loaded before the first is used (lanes 0-31 and 32-63 take one list each, two rounds);
-  // body(entry) once per round.  Returns false, before any body call of that chunk pair, when a
+  // bitmask bits and counts of 128 query tiles per load round, then 2 kWalkRounds lists per
+  // step, all loaded before the first is used (lanes 0-31 and 32-63 take one list each per
+  // round); body(entry) once per round.  Returns false, before any body call of that chunk pair, when a
   // list of the column did not fit (the same test as column_overflows: the tile pass takes the
   // key tile); the caller has then written nothing.
   auto walk = [&](auto&& body) -> bool {
@@ -658,10 +685,10 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
       }
       if (wave_ballot(ovf) != 0ull) return false;
       while (true) {
-        int ix[4], sx[4];
-        uint32_t cx[4];
+        int ix[2 * kWalkRounds], sx[2 * kWalkRounds];
+        uint32_t cx[2 * kWalkRounds];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {  // next four lists
+        for (int u = 0; u < 2 * kWalkRounds; ++u) {  // next lists
           ix[u] = -1;
           sx[u] = 0;
           cx[u] = 0u;
@@ -677,12 +704,12 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
             }
         }
         if (ix[0] < 0) break;
-        u32x4 ent[2];
-        float wk[2];
-        int brl[2], qtl[2];
-        bool valid[2];
+        u32x4 ent[kWalkRounds];
+        float wk[kWalkRounds];
+        int brl[kWalkRounds], qtl[kWalkRounds];
+        bool valid[kWalkRounds];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < kWalkRounds; ++r) {
           const int idx = l < 32 ? ix[2 * r] : ix[2 * r + 1];
           const int sel = l < 32 ? sx[2 * r] : sx[2 * r + 1];
           const uint32_t cnt = l < 32 ? cx[2 * r] : cx[2 * r + 1];
@@ -699,7 +726,7 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
           }
         }
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < kWalkRounds; ++r) {
           if (ix[2 * r] < 0) break;
           // x through a bit cast of the whole vector (see load_pairs)
           const f32x4 ef = __builtin_bit_cast(f32x4, ent[r]);
@@ -774,6 +801,21 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
                       normalize_back<D, NORM>(ak[br], kx[br], rk[br]));
     }
   };
+  // the same, packed (rows zero, norms 1 where not needed)
+  auto load_key_raw = [&](int jl, RowRaw<D>(&kx)[BR], float(&rk)[BR]) {
+    const int j = 32 * kt + jl;
+#pragma unroll
+    for (int br = 0; br < BR; ++br) {
+      kx[br] = RowRaw<D>{0u};
+      rk[br] = 1.f;
+      if constexpr (NORM)
+        if ((used[br] >> jl) & 1u) {
+          const int kslot = br == 0 ? B_K1 : B_K2;
+          kx[br] = load_rowraw<D>(base(kslot) + (int64_t)j * P.s[kslot][2]);
+          rk[br] = P.norms[norm_base(P, br == 0 ? N_K1 : N_K2, bh) + j];
+        }
+    }
+  };
   // the key rows and inverse norms of key row jl for the normalize backward
   auto load_key_rows = [&](int jl, RowVec<D>(&kx)[BR], float(&rk)[BR]) {
     const int j = 32 * kt + jl;
@@ -792,8 +834,8 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
 
   if (slotted) {
     // The slots sorted by key row, then slot order: lane s gets the pair of rank s (lanes past
-    // np keep their own slot).  Then the pairs in that order, the loads of four at a time in
-    // flight together; a key row is finished when the next pair names another.
+    // np keep their own slot).  Then the pairs in that order, the loads of kRowBatch at a time
+    // in flight together; a key row is finished when the next pair names another.
     const int sl = (uint32_t)l < np ? l : 0;
     const int pi_l = ps_i[sl], pjl_l = ps_jl[sl];
     const float px_l = ps_x[sl], pw_l = ps_w[sl];
@@ -817,12 +859,12 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
       ak[br] = kx[br] = RowVec<D>{};
       rk[br] = 1.f;
     }
-    for (uint32_t s0 = 0; s0 < np; s0 += 4) {
-      int jl[4], ibr[4];
-      RowVec<D> dor[4], qr[4], kxu[4][BR];
-      float rku[4][BR];
+    for (uint32_t s0 = 0; s0 < np; s0 += kRowBatch) {
+      int jl[kRowBatch], ibr[kRowBatch];
+      RowRaw<D> dor[kRowBatch], qr[kRowBatch], kxu[kRowBatch][BR];
+      float rku[kRowBatch][BR];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kRowBatch; ++u) {
         const int s = (int)s0 + u;
         ibr[u] = 0;
         if ((uint32_t)s >= np) continue;
@@ -831,12 +873,12 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
         const int i = pi & 0x7fffffff;
         ibr[u] = (pi >> 31) & 1;
         const int qslot = ibr[u] ? B_Q2 : B_Q1;
-        dor[u] = load_rowvec<D>(dob + (int64_t)i * sdo);
-        qr[u] = load_rowvec<D>(base(qslot) + (int64_t)i * P.s[qslot][2]);
-        load_key_rows(jl[u], kxu[u], rku[u]);
+        dor[u] = load_rowraw<D>(dob + (int64_t)i * sdo);
+        qr[u] = load_rowraw<D>(base(qslot) + (int64_t)i * P.s[qslot][2]);
+        load_key_raw(jl[u], kxu[u], rku[u]);
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kRowBatch; ++u) {
         const int s = (int)s0 + u;
         if ((uint32_t)s >= np) continue;
         if (jl[u] != cur) {
@@ -846,20 +888,21 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
 #pragma unroll
           for (int br = 0; br < BR; ++br) {
             ak[br] = RowVec<D>{};
-            kx[br] = kxu[u][br];
+            kx[br] = unpack<D>(kxu[u][br]);
             rk[br] = rku[u][br];
           }
         }
         const float x = __builtin_bit_cast(float, __builtin_amdgcn_readlane(s_x, s));
         const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(s_w, s));
         const float wa = (ibr[u] ? -lam : 1.f) * pow_p<PK>(x, pw);
+        const RowVec<D> dv_ = unpack<D>(dor[u]), qv = unpack<D>(qr[u]);
 #pragma unroll
-        for (int c = 0; c < RowVec<D>::E; ++c) av.v[c] = __builtin_fmaf(wa, dor[u].v[c], av.v[c]);
+        for (int c = 0; c < RowVec<D>::E; ++c) av.v[c] = __builtin_fmaf(wa, dv_.v[c], av.v[c]);
 #pragma unroll
         for (int br = 0; br < BR; ++br)
           if (ibr[u] == br)
 #pragma unroll
-            for (int c = 0; c < RowVec<D>::E; ++c) ak[br].v[c] = __builtin_fmaf(wk, qr[u].v[c], ak[br].v[c]);
+            for (int c = 0; c < RowVec<D>::E; ++c) ak[br].v[c] = __builtin_fmaf(wk, qv.v[c], ak[br].v[c]);
       }
     }
     if (cur >= 0) store_key_row(cur, av, ak, kx, rk);
