@@ -266,8 +266,9 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
   // Per lane and query tile: bit kt % 32 set when the lane's test passed for key tile kt.  The
   // wave ORs them when a 32-tile word is complete (cheaper than a ballot per tile).
   uint32_t hb[QPW];
+  uint32_t cn[QPW];  // candidate keys met per query tile (may pass the cap)
 #pragma unroll
-  for (int s = 0; s < QPW; ++s) hb[s] = 0u;
+  for (int s = 0; s < QPW; ++s) hb[s] = cn[s] = 0u;
   const int koff = n32 * KS + 8 * g;
 
   // Threshold test of key tile kt (in stage st) against this wave's query tiles.
@@ -309,8 +310,22 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
       bool hit;
       if constexpr (NORM) hit = maximum16(S[s]) * rk > tau[s];  // largest score of the lane's key
       else hit = valid[s] && max16(S[s]) > tau[s];          // largest score of the lane's query
-      // key tiles after the query tile's last position hold no causal pair
-      hb[s] |= hit && kt <= ktl[s] ? bit : 0u;
+      // key tiles after the query tile's last position hold no causal pair; a query tile past
+      // the last row (the wave's second, at the end of the sequence) has no list
+      const bool lh = live[s] && hit && kt <= ktl[s];
+      hb[s] |= lh ? bit : 0u;
+      if constexpr (NORM) {
+        // candidate keys (a few per cent of the tiles have one): the keys of the passing lanes,
+        // in increasing order, appended to the query tile's list
+        const uint64_t bal = wave_ballot(lh);
+        if (P.cand && bal) {
+          const uint32_t keys = (uint32_t)bal | (uint32_t)(bal >> 32);
+          const uint32_t slot = cn[s] + (uint32_t)__builtin_popcount(keys & ((1u << n32) - 1u));
+          if (l < 32 && ((keys >> l) & 1u) && slot < (uint32_t)kCandCap)
+            P.cand[((int64_t)sidx * nqt + qt0 + s) * kCandCap + slot] = (uint32_t)(32 * kt + l);
+          cn[s] += (uint32_t)__builtin_popcount(keys);
+        }
+      }
     }
   };
   // bitmask words of this wave's rows: word kt/32 is complete after key tile kt
@@ -348,6 +363,11 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     if (it + 1 < nit) commit(it + 1);
     if (it + 2 < nit) fetch(it + 2);
     __syncthreads();
+  }
+  if (NORM && P.cand && l == 0) {
+#pragma unroll
+    for (int s = 0; s < QPW; ++s)
+      if (live[s]) P.cand[pair_lists(BR, BH, nqt) * kCandCap + (int64_t)sidx * nqt + qt0 + s] = cn[s];
   }
   if (P.stats && l == 0) {
     // causal (query tile, key tile) pairs of this wave: key tiles 0 .. qt of each live query tile
@@ -402,6 +422,13 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
   }
   const int qt = kPvWaves * blk + wv;
   if (qt >= nqt) return;
+  if (NORM && P.cand) {  // fwd_pv_cand takes the query tiles whose candidate lists all fit
+    const uint32_t* counts = P.cand + pair_lists(BR, BH, nqt) * kCandCap;
+    bool fit = true;
+#pragma unroll
+    for (int br = 0; br < BR; ++br) fit = fit && counts[((int64_t)br * BH + bh) * nqt + qt] <= (uint32_t)kCandCap;
+    if (fit) return;
+  }
   const int b = bh / P.H, h = bh % P.H;
   const int iq = 32 * qt + n32;
   const bool valid = iq < Nq;
@@ -562,6 +589,212 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
   }
 }
 
+// ------------------------------------------------------------------ fwd_pv_cand
+// The exact pass of the query tiles whose candidate-key lists (every branch, normalised scores)
+// fit: per branch the candidate keys' K and V rows are gathered into one 32-row tile (row c =
+// candidate c, rows past the count zero), the score tile is computed with the instruction
+// sequence of fwd_pv (the same rows in the same operands: bitwise the same scores), and the
+// exact weights with the causal mask accumulate out += coef A V as in fwd_pv.  One gather round
+// per branch replaces one per kept key tile.  The bitmask row is rewritten from the key tiles
+// holding a non-zero weight; the pair list takes the non-zero weights in the order (value r,
+// lane).
+template <int D, int BR, int PK>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fwd_pv_cand(FwdParams P) {
+  constexpr int NT = D / 16, ND = D / 32;
+  constexpr int VS = D + 32;     // LDS row stride of the V tile: conflict-free transpose reads
+  constexpr int CPR = D / 8;     // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;  // rows per load instruction
+  constexpr int VL = 32 / RPI;   // load instructions per tile
+  constexpr int KS = D + 8;      // LDS row stride of the K tile: conflict-free row-fragment reads
+  __shared__ __attribute__((aligned(16))) bf16 vt[32 * VS];
+  __shared__ __attribute__((aligned(16))) bf16 ktl[32 * KS];
+  __shared__ __attribute__((aligned(16))) int ckey[32];    // candidate keys (padding: -1)
+  __shared__ __attribute__((aligned(16))) float crk[32];  // their inverse norms
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
+  int bh, qt;
+  {
+    const int bid = blockIdx.x;
+    if (BH % 8 == 0) {  // one head's query tiles consecutive on one XCD, longest first
+      const int x = bid & 7, j = bid >> 3;
+      bh = x + 8 * (j / nqt);
+      qt = nqt - 1 - j % nqt;
+    } else {
+      bh = bid / nqt;
+      qt = nqt - 1 - bid % nqt;
+    }
+  }
+  if (bh >= BH) return;
+  const uint32_t* counts = P.cand + pair_lists(BR, BH, nqt) * kCandCap;
+  uint32_t nc[BR];
+#pragma unroll
+  for (int br = 0; br < BR; ++br) nc[br] = counts[((int64_t)br * BH + bh) * nqt + qt];
+#pragma unroll
+  for (int br = 0; br < BR; ++br)
+    if (nc[br] > (uint32_t)kCandCap) return;  // fwd_pv walks the bitmask tiles
+
+  const int b = bh / P.H, h = bh % P.H;
+  const int iq = 32 * qt + n32;
+  const bool valid = iq < Nq;
+  const int pq = qoff + iq;                    // the lane's query position
+  const int klast = kt_last(qt, qoff, P.nkt);  // last key tile the query tile sees
+  const int nw = (klast >> 5) + 1;             // bitmask words of the row
+  const float tau = *P.beta * tau_coeff(pq, P.inv_d);
+  const float pw = P.p;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+  const int vrow = l / CPR, vch = l % CPR;
+  const int bk = l >> 4, jj = l & 15;
+  const int voff = (4 * (bk >> 1) + (jj >> 2)) * VS + 16 * (bk & 1) + 4 * (jj & 3);
+
+  f32x16 O[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) O[c] = f32x16{};
+  unsigned computed = 0, checked = 0;
+
+#pragma unroll
+  for (int br = 0; br < BR; ++br) {
+    const uint32_t n = nc[br];
+    const int64_t lidx = ((int64_t)br * BH + bh) * nqt + qt;
+    uint32_t* orow = P.occ + lidx * P.occ_w;
+    uint32_t npairs = 0;
+    if (n > 0) {
+      const int qslot = br ? F_Q2 : F_Q1, kslot = br ? F_K2 : F_K1;
+      const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
+      const bf16* khead = (const bf16*)P.in[kslot] + (int64_t)b * P.s[kslot][0] + (int64_t)h * P.s[kslot][1];
+      const bf16* vhead = (const bf16*)P.in[F_V] + (int64_t)b * P.s[F_V][0] + (int64_t)h * P.s[F_V][1];
+      const int64_t sq = P.s[qslot][2], sk = P.s[kslot][2], sv = P.s[F_V][2];
+      const float coef = br == 0 ? 1.f : -lam;
+      // every load of the branch in one round: the candidate keys (lane c < n), their norms,
+      // the query rows, the gathered key and value rows
+      const int key_l = l < (int)n ? (int)P.cand[lidx * kCandCap + l] : -1;
+      const float rk_l = key_l >= 0 ? P.norms[norm_base(P, br ? N_K2 : N_K1, bh) + key_l] : 0.f;
+      const float rq = P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + min(iq, Nq - 1)];
+      u32x4 qr[VL], kr[VL], vr[VL];
+#pragma unroll
+      for (int i = 0; i < VL; ++i) {
+        const int row = vrow + RPI * i;
+        qr[i] = *reinterpret_cast<const u32x4*>(qhead + (int64_t)min(32 * qt + row, Nq - 1) * sq + 8 * vch);
+        const int key = __shfl(key_l, row);
+        kr[i] = vr[i] = u32x4{0u, 0u, 0u, 0u};
+        if (key >= 0) {
+          kr[i] = *reinterpret_cast<const u32x4*>(khead + (int64_t)key * sk + 8 * vch);
+          vr[i] = *reinterpret_cast<const u32x4*>(vhead + (int64_t)key * sv + 8 * vch);
+        }
+      }
+      // query fragments through the K tile buffer, then the gathered rows
+      wave_lds_sync();
+#pragma unroll
+      for (int i = 0; i < VL; ++i) *reinterpret_cast<u32x4*>(ktl + (vrow + RPI * i) * KS + 8 * vch) = qr[i];
+      if (l < 32) {
+        ckey[l] = key_l;
+        crk[l] = rk_l;
+      }
+      wave_lds_sync();
+      bf16x8 Q[NT];
+      {
+        const bf16* qp = ktl + n32 * KS + 8 * g;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) Q[t] = *reinterpret_cast<const bf16x8*>(qp + 16 * t);
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int i = 0; i < VL; ++i) {
+        *reinterpret_cast<u32x4*>(ktl + (vrow + RPI * i) * KS + 8 * vch) = kr[i];
+        *reinterpret_cast<u32x4*>(vt + (vrow + RPI * i) * VS + 8 * vch) = vr[i];
+      }
+      wave_lds_sync();
+      f32x16 S = {};
+      const bf16* kp = ktl + n32 * KS + 8 * g;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) S = PolBF16::mma(*reinterpret_cast<const bf16x8*>(kp + 16 * t), Q[t], S);
+      // value r of the lane: candidate crow(r, g)
+      f32x4 rk4[4];
+      u32x4 key4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        rk4[u] = *reinterpret_cast<const f32x4*>(crk + 8 * u + 4 * g);
+        key4[u] = *reinterpret_cast<const u32x4*>(ckey + 8 * u + 4 * g);
+      }
+      uint32_t* pent = P.pairs ? P.pairs + lidx * (4 * kPairCap) : nullptr;
+      uint32_t cnz = 0u;  // candidates with a non-zero weight
+      f32x16 C;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * u + e;
+          const int key = (int)key4[u][e];
+          const float x = __builtin_fmaf(S[r] * rk4[u][e], rq, -tau);
+          const bool pos = key >= 0 && key <= pq && key < Nk && x > 0.f;
+          C[r] = pos ? coef * pow_p<PK>(x, pw) : 0.f;
+          const bool hit = valid && pos;
+          const uint64_t bal = wave_ballot(hit);
+          cnz |= ((uint32_t)bal ? 1u << crow(r, 0) : 0u) | ((uint32_t)(bal >> 32) ? 1u << crow(r, 1) : 0u);
+          if (pent) {
+            const uint32_t slot = npairs + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            if (hit && slot < (uint32_t)kPairCap)
+              *reinterpret_cast<u32x4*>(pent + 4 * slot) = u32x4{(uint32_t)key, (uint32_t)n32, __builtin_bit_cast(uint32_t, x), 0u};
+            npairs += (uint32_t)__builtin_popcountll(bal);
+          }
+        }
+      if (cnz) {
+        const bf16x8 PF0 = PolBF16::pack_c(C, 0), PF1 = PolBF16::pack_c(C, 1);
+        const bf16* vp = vt + voff;
+#pragma unroll
+        for (int c = 0; c < ND; ++c) {
+          O[c] = PolBF16::mma(tr_frag<VS>(vp + 32 * c), PF0, O[c]);
+          O[c] = PolBF16::mma(tr_frag<VS>(vp + 32 * c + 16 * VS), PF1, O[c]);
+        }
+      }
+      // the bitmask row: lane w rewrites word w from the key tiles of the candidates with a
+      // non-zero weight (the screen's words cover the key tiles of all candidates, nothing else)
+      for (int w0 = 0; w0 < nw; w0 += 64) {
+        uint32_t word = 0u;
+        for (uint32_t m = cnz; m; m &= m - 1u) {
+          const int kt = __builtin_amdgcn_readfirstlane(ckey[__builtin_ctz(m)]) >> 5;
+          word |= (kt >> 5) == w0 + l ? 1u << (kt & 31) : 0u;
+        }
+        if (w0 + l < nw) {
+          if (P.stats) checked += (unsigned)__builtin_popcount(orow[w0 + l]);
+          orow[w0 + l] = word;
+        }
+        computed += (unsigned)__builtin_popcount(word);
+      }
+      wave_lds_sync();  // the tiles are reused by the next branch and the output
+    }
+    if (P.pairs && l == 0) P.pairs[pair_lists(P.nbr, BH, nqt) * 4 * kPairCap + lidx] = npairs;
+  }
+
+  // Output rows through LDS (the K tile buffer), as in fwd_pv.
+  wave_lds_sync();
+#pragma unroll
+  for (int c = 0; c < ND; ++c)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      store4(ktl + n32 * KS + 32 * c + 8 * u + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2], O[c][4 * u + 3]);
+  wave_lds_sync();
+  {
+    bf16* ohead = (bf16*)P.out + (int64_t)b * P.s[F_OUT][0] + (int64_t)h * P.s[F_OUT][1];
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      const int r = vrow + RPI * i, row = 32 * qt + r;
+      if (row < Nq)
+        *reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch) =
+            *reinterpret_cast<const u32x4*>(ktl + r * KS + 8 * vch);
+    }
+  }
+  if (P.stats) {
+    const float cs = wave_sum((float)computed), ks = wave_sum((float)checked);
+    if (l == 0 && ks > 0.f) {
+      atomicAdd(P.stats + 1, (unsigned long long)cs);
+      atomicAdd(P.stats + 2, (unsigned long long)ks);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ dispatch
 template <int D, int BR, int PK, bool NORM>
 int launch_sparse_t(const FwdParams& p, hipStream_t s) {
@@ -574,6 +807,8 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   const unsigned nqb = (unsigned)((p.Nq + 255) / 256);
   constexpr int QPW = 2, TPB = 1;
   hipLaunchKernelGGL((fwd_screen<D, NORM, QPW, TPB>), dim3((unsigned)(BR * BH) * nqb), dim3(512 / QPW), 0, s, p, BR);
+  if (NORM && p.cand)
+    hipLaunchKernelGGL((fwd_pv_cand<D, BR, PK>), dim3((unsigned)(BH * p.nqt)), dim3(64), 0, s, p);
   const unsigned nblk = (unsigned)((p.nqt + kPvWaves - 1) / kPvWaves);
   hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)BH * nblk), dim3(64 * kPvWaves), 0, s, p);
   return (int)hipGetLastError();

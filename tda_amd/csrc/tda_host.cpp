@@ -73,7 +73,7 @@ int64_t occ_words(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t branc
 // Forward workspace: the bitmask scratch (used when the caller asks for no occupancy output;
 // the bf16 forward always builds the bitmask), then, when there is a single query tile
 // (seq_len <= 32), the per-chunk partial outputs of the bf16 decode kernels:
-// [B*H][ceil(key tiles / 32)][seq_len][128] floats (head_dim <= 128).
+// [B*H][ceil(key tiles / 32)][seq_len][128] floats (head_dim <= 128) ...
 int64_t fwd_occ_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t branches) {
   return round256(occ_words(bh, seq_len, seq_len_kv, branches) * (int64_t)sizeof(uint32_t));
 }
@@ -81,8 +81,14 @@ int64_t fwd_part_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv) {
   if (seq_len > 32) return 0;
   return round256(bh * ceil_div(ceil_div(seq_len_kv, 32), 32) * seq_len * 128 * (int64_t)sizeof(float));
 }
+// ... or, with more than one query tile, the candidate lists of the bf16 screen.
+int64_t fwd_cand_bytes(int64_t bh, int64_t seq_len, int64_t branches) {
+  if (seq_len <= 32) return 0;
+  return round256(tda::cand_words(branches * bh * ceil_div(seq_len, 32)) * (int64_t)sizeof(uint32_t));
+}
 int64_t fwd_ws_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t branches) {
-  return fwd_occ_bytes(bh, seq_len, seq_len_kv, branches) + fwd_part_bytes(bh, seq_len, seq_len_kv);
+  return fwd_occ_bytes(bh, seq_len, seq_len_kv, branches) + fwd_part_bytes(bh, seq_len, seq_len_kv) +
+         fwd_cand_bytes(bh, seq_len, branches);
 }
 bool size_args_ok(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv, int32_t branches) {
   return batch >= 1 && heads >= 1 && seq_len >= 1 && seq_len_kv >= 1 && (branches == 1 || branches == 2);
@@ -243,9 +249,10 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
   p.lam = a->lambda_param;
   p.norms = a->normalize ? a->norms : nullptr;
   p.occ = a->occupancy ? a->occupancy : static_cast<uint32_t*>(a->workspace);
-  if (a->seq_len <= 32)
-    p.part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) +
-                                      fwd_occ_bytes(a->batch * a->heads, a->seq_len, c.seq_len_kv, a->branches));
+  char* after_occ = static_cast<char*>(a->workspace) +
+                   fwd_occ_bytes(a->batch * a->heads, a->seq_len, c.seq_len_kv, a->branches);
+  if (a->seq_len <= 32) p.part = reinterpret_cast<float*>(after_occ);
+  else p.cand = reinterpret_cast<uint32_t*>(after_occ);
   p.stats = a->stats;
   p.pairs = a->pairs;
   p.nbr = a->branches;

@@ -28,6 +28,16 @@ constexpr int64_t pair_words(int64_t branches, int64_t bh, int64_t nqt) {
 }
 constexpr uint32_t kPairOverflow = 0xffffffffu;  // count of a list the forward did not write
 
+// Candidate keys (bf16 with normalisation, forward workspace): for each (branch, head, query
+// tile) the keys j whose screen lane passed (max over its query rows of the screen score above
+// the tile's threshold minus the screen's proven margin), a superset of the keys with a non-zero
+// weight in the query tile; the exact pass gathers only these rows.  Layout: the keys,
+// kCandCap u32 per list, in the order the screen met them (increasing); then the counts, u32 per
+// list.  A count above kCandCap marks a list that did not fit: the exact pass then walks the
+// bitmask tiles of that query tile.
+constexpr int kCandCap = 32;
+constexpr int64_t cand_words(int64_t lists) { return lists * (1 + kCandCap); }
+
 // Positions: query row i of a head sits at absolute position qoff + i and sees the keys
 // j <= qoff + i of the Nk key rows (qoff = 0 and Nq = Nk is the plain causal case).  Tiles are
 // 32 rows: nqt = ceil(Nq / 32) query tiles, nkt = ceil(Nk / 32) key tiles.
@@ -49,6 +59,7 @@ struct FwdParams {
   float* part;               // bf16 with one query tile: per-chunk partial outputs (workspace)
   uint32_t* pairs;           // may be null: pair lists (bf16)
   int nbr;                   // branches
+  uint32_t* cand;            // candidate keys (workspace; null for a single query tile)
 };
 
 struct BwdParams {
