@@ -314,18 +314,6 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
       // the last row (the wave's second, at the end of the sequence) has no list
       const bool lh = live[s] && hit && kt <= ktl[s];
       hb[s] |= lh ? bit : 0u;
-      if constexpr (NORM) {
-        // candidate keys (a few per cent of the tiles have one): the keys of the passing lanes,
-        // in increasing order, appended to the query tile's list
-        const uint64_t bal = wave_ballot(lh);
-        if (P.cand && bal) {
-          const uint32_t keys = (uint32_t)bal | (uint32_t)(bal >> 32);
-          const uint32_t slot = cn[s] + (uint32_t)__builtin_popcount(keys & ((1u << n32) - 1u));
-          if (l < 32 && ((keys >> l) & 1u) && slot < (uint32_t)kCandCap)
-            P.cand[((int64_t)sidx * nqt + qt0 + s) * kCandCap + slot] = (uint32_t)(32 * kt + l);
-          cn[s] += (uint32_t)__builtin_popcount(keys);
-        }
-      }
     }
   };
   // bitmask words of this wave's rows: word kt/32 is complete after key tile kt
@@ -334,9 +322,25 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
 #pragma unroll
       for (int s = 0; s < QPW; ++s) {
         uint32_t w = hb[s];
+        const uint32_t hm = w | (uint32_t)__shfl_xor((int)w, 32);  // lane n32: tiles its key passed
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) w |= (uint32_t)__shfl_xor((int)w, o);
         hb[s] = 0u;
+        if constexpr (NORM) {
+          // candidate keys of the word's tiles: per tile with a passing lane (a few per cent),
+          // the keys of its passing lanes in increasing order, appended to the query tile's list
+          if (P.cand) {
+            uint32_t* clist = P.cand + ((int64_t)sidx * nqt + qt0 + s) * kCandCap;
+            for (uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)w); m; m &= m - 1u) {
+              const int b = __builtin_ctz(m);
+              const uint32_t keys = (uint32_t)wave_ballot(l < 32 && ((hm >> b) & 1u));
+              const uint32_t slot = cn[s] + (uint32_t)__builtin_popcount(keys & ((1u << n32) - 1u));
+              if (l < 32 && ((keys >> l) & 1u) && slot < (uint32_t)kCandCap)
+                clist[slot] = (uint32_t)(32 * (32 * (kt >> 5) + b) + l);
+              cn[s] += (uint32_t)__builtin_popcount(keys);
+            }
+          }
+        }
         if (l == 0 && live[s]) {
           uint32_t* row = occ0 + s * P.occ_w;
           row[kt >> 5] = w;
