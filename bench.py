@@ -28,11 +28,11 @@ SHAPE = (4, 16, 4096, 128)
 BETA, LAM, POWER = 1.0, 0.5, 2.0
 FWD_UNITS, FWDBWD_UNITS = 3.0, 11.0          # counted causal-dense units (U = B*H*N^2*d)
 REF_FWD_UNITS, REF_FWDBWD_UNITS = 4.0, 14.0  # the reference's two independent TRA calls
-# HBM bytes moved by one forward call (key_norms + fwd_screen + fwd_pv) at SHAPE, from rocprofv3
+# HBM bytes moved by one forward call (key_norms + fwd_screen + fwd_pv_cand + fwd_pv) at SHAPE, from rocprofv3
 # --pmc FETCH_SIZE and --pmc WRITE_SIZE runs of this script, each scaled by what the same counter
 # reads for --copy-probe (a 2^30-byte device copy): FETCH_SIZE x 2.000, WRITE_SIZE x 1.000.
 # Recorded with the command lines in profiles/tda_c2_bf16_counters.md; re-measure after kernel changes.
-FWD_HBM_BYTES = 1.215e9
+FWD_HBM_BYTES = 1.014e9
 
 
 def units(shape, u):
@@ -293,7 +293,8 @@ def main(argv=None) -> int:
             "note": "FLOPs of two independent TRA calls (4U fwd, 14U fwd+bwd), as the reference executes",
             "fwd_tflops": units(SHAPE, REF_FWD_UNITS) / (fwd_ms * 1e-3) / 1e12,
             "fwd_bwd_tflops": units(SHAPE, REF_FWDBWD_UNITS) / (max(step_ms, wall_ms) * 1e-3) / 1e12},
-        "roofline": {"kernel": "forward (key_norms + fwd_screen + fwd_pv), events around the launches", "bound": "mfma",
+        "roofline": {"kernel": "forward (key_norms + fwd_screen + fwd_pv_cand + fwd_pv), events around the launches",
+                     "bound": "mfma",
                      "achieved": fwd_tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": fwd_tf / PEAK_BF16_TFLOPS, "traffic": FWD_HBM_BYTES,
                      "algorithmic": "3U = 4.1232e11 FLOP per launch (causal dense)",
