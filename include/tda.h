@@ -115,7 +115,8 @@ typedef struct tda_fwd_args {
   void*  workspace;         /* device scratch of tda_fwd_workspace_bytes_kv() bytes,
                                16-byte aligned: holds the tile bitmask when occupancy is NULL
                                and, when seq_len <= 32, the fp32 per-chunk partial outputs of
-                               the single-query-tile (decode) kernels */
+                               the single-query-tile (decode) kernels, else the screen's
+                               candidate keys per (branch, head, query tile) */
   size_t workspace_bytes;
   int64_t seq_len_kv;       /* Nk, the key/value rows; 0 means Nk = seq_len */
   int64_t q_offset;         /* position of query row 0 (>= 0); 0 with Nk = Nq is the
@@ -144,7 +145,9 @@ typedef struct tda_bwd_args {
   float* dlambda;           /* device scalar out (branches == 2), may be NULL */
   const float*    norms;    /* the forward's norms output; required when normalize == 1 */
   const uint32_t* occupancy;/* the forward's bitmask, or NULL to test every causal tile */
-  void*  workspace;         /* device scratch of tda_bwd_workspace_bytes() bytes */
+  void*  workspace;         /* device scratch of tda_bwd_workspace_bytes() bytes, 16-byte
+                               aligned: dbeta / dlambda partials and the dk weight of each
+                               pair-list entry */
   size_t workspace_bytes;
   unsigned long long* stats;/* optional: [0] += tiles visited, [1] += tiles computed */
   int64_t seq_len_kv;       /* as in tda_fwd_args (dq, dout: Nq rows; dk, dv: Nk rows) */
