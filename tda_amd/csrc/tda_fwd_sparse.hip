@@ -630,10 +630,13 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
     }
   }
   if (bh >= BH) return;
+  // the counts of every branch and, in the same round, every list slot (lanes 0-31: branch 0,
+  // lanes 32-63: branch 1; slots past a count are never used)
   const uint32_t* counts = P.cand + pair_lists(BR, BH, nqt) * kCandCap;
   uint32_t nc[BR];
 #pragma unroll
   for (int br = 0; br < BR; ++br) nc[br] = counts[((int64_t)br * BH + bh) * nqt + qt];
+  const int kraw = (int)P.cand[(((int64_t)(BR == 2 ? (l >> 5) : 0) * BH + bh) * nqt + qt) * kCandCap + (l & 31)];
 #pragma unroll
   for (int br = 0; br < BR; ++br)
     if (nc[br] > (uint32_t)kCandCap) return;  // fwd_pv walks the bitmask tiles
@@ -672,7 +675,8 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
       const float coef = br == 0 ? 1.f : -lam;
       // every load of the branch in one round: the candidate keys (lane c < n), their norms,
       // the query rows, the gathered key and value rows
-      const int key_l = l < (int)n ? (int)P.cand[lidx * kCandCap + l] : -1;
+      const int kb = __shfl(kraw, (32 * br + (l & 31)) & 63);  // this branch's slots: lanes 32 br ..
+      const int key_l = l < (int)n ? kb : -1;
       const float rk_l = key_l >= 0 ? P.norms[norm_base(P, br ? N_K2 : N_K1, bh) + key_l] : 0.f;
       const float rq = P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + min(iq, Nq - 1)];
       u32x4 qr[VL], kr[VL], vr[VL];
