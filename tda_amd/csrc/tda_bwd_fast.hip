@@ -210,22 +210,24 @@ constexpr int kBwdWaves = 1;
 // walks the set bits of the branch's bitmask row.  A branch's resident operands (its query
 // fragments, dO, one dq accumulator) are half of both branches', which lets two waves share a
 // SIMD.
-template <int D, int BR, int PK, bool NORM>
-__global__ void __launch_bounds__(64 * kBwdWaves) __attribute__((amdgpu_waves_per_eu(2))) bwd_dq_fast(BwdParams P) {
-  constexpr int NT = D / 16, ND = D / 32;
-  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> lds_all[kBwdWaves];
-
-  const int l = lane_id(), n32 = l & 31, g = l >> 5;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  BwdWaveLds<D>& W = lds_all[wv];
-  const int BH = P.B * P.H;
-  const int64_t item = (int64_t)blockIdx.x * kBwdWaves + wv;  // (query tile, head, branch)
-  if (item >= (int64_t)BR * BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
-  // longest first (query tiles from the last); the two branches of a (head, query tile) adjacent
-  const int br = BR == 2 ? (int)(item & 1) : 0;
+// (branch, head, query tile) of query-major tile-pass item `item`: longest first (query tiles
+// from the last); the two branches of a (head, query tile) adjacent.
+template <int BR>
+__device__ __forceinline__ void dq_item(int64_t item, int BH, int nqt, int& br, int& qt, int& bh) {
+  br = BR == 2 ? (int)(item & 1) : 0;
   const int64_t rest = BR == 2 ? item >> 1 : item;
-  const int qt = P.nqt - 1 - (int)(rest / BH);
-  const int bh = (int)(rest % BH);
+  qt = nqt - 1 - (int)(rest / BH);
+  bh = (int)(rest % BH);
+}
+
+// The tile pass over one (branch, query tile) item: one wave, W its LDS.
+template <int D, int BR, int PK, bool NORM>
+__device__ __forceinline__ void bwd_dq_tile(const BwdParams& P, BwdWaveLds<D>& W, int64_t item) {
+  constexpr int NT = D / 16, ND = D / 32;
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int BH = P.B * P.H;
+  int br, qt, bh;
+  dq_item<BR>(item, BH, P.nqt, br, qt, bh);
   const int b = bh / P.H, h = bh % P.H;
   const int Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
   const int i = qt * 32 + n32;
@@ -346,6 +348,28 @@ __global__ void __launch_bounds__(64 * kBwdWaves) __attribute__((amdgpu_waves_pe
       atomicAdd(P.stats + 1, (unsigned long long)computed);
     }
   }
+}
+
+// One wave per workgroup and `per_wave` consecutive items per wave.  With pair lists, the items
+// whose list fit belong to bwd_dq_pairs: the wave tests its items' counts in one lane-parallel
+// round and runs only the others (per_wave 8: a launch where every list fits costs two waves per
+// SIMD); without lists every item runs (per_wave 1).
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) bwd_dq_fast(BwdParams P, int per_wave) {
+  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> W;
+  const int l = lane_id();
+  const int BH = P.B * P.H;
+  const int64_t n = (int64_t)BR * BH * P.nqt, first = (int64_t)blockIdx.x * per_wave;
+  bool need = false;
+  if (l < per_wave && first + l < n) {
+    need = true;
+    if (P.pairs) {
+      int br, qt, bh;
+      dq_item<BR>(first + l, BH, P.nqt, br, qt, bh);
+      need = P.pairs[pair_lists(BR, BH, P.nqt) * 4 * kPairCap + ((int64_t)br * BH + bh) * P.nqt + qt] > (uint32_t)kPairCap;
+    }
+  }
+  for (uint64_t m = wave_ballot(need); m; m &= m - 1ull) bwd_dq_tile<D, BR, PK, NORM>(P, W, first + __builtin_ctzll(m));
 }
 
 // ------------------------------------------------------------------ query-major pass, pairs
@@ -1111,8 +1135,9 @@ static int launch_t(const BwdParams& p, void* stream) {
   const int64_t qitems = (int64_t)BR * p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
   if (p.pairs) hipLaunchKernelGGL((bwd_dq_pairs<D, BR, PK, NORM>), dim3((unsigned)qitems), dim3(64), 0, s, p);
-  hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3((unsigned)((qitems + kBwdWaves - 1) / kBwdWaves)),
-                     dim3(64 * kBwdWaves), 0, s, p);
+  const int dq_per_wave = p.pairs ? 8 : 1;  // with pair lists most items exit at once
+  hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3((unsigned)((qitems + dq_per_wave - 1) / dq_per_wave)),
+                     dim3(64), 0, s, p, dq_per_wave);
   if (p.pairs) hipLaunchKernelGGL((bwd_dkv_pairs<D, BR, PK, NORM>), dim3((unsigned)kitems), dim3(64), 0, s, p);
   hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3((unsigned)((kitems + kBwdWaves - 1) / kBwdWaves)),
                      dim3(64 * kBwdWaves), 0, s, p);

@@ -393,46 +393,17 @@ __device__ __forceinline__ bf16x8 tr_frag(const bf16* p) {
   return bf16x8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
 }
 
-// One wave per query tile and one wave per workgroup: the work per query tile varies with its
-// number of non-zero tiles, and single-wave workgroups retire independently (a 4-wave
-// workgroup would hold its slot until its slowest wave ends).  No barriers.
-constexpr int kPvWaves = 1;  // waves per workgroup
+// The tile pass over one query tile (bh, qt): one wave; vt / ktl its LDS tiles.
 template <int D, int BR, int PK, bool NORM>
-__global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per_eu(2))) fwd_pv(FwdParams P) {
+__device__ __forceinline__ void fwd_pv_tile(const FwdParams& P, bf16* vt_, bf16* kt_, int bh, int qt) {
   constexpr int NT = D / 16, ND = D / 32;
   constexpr int VS = D + 32;     // LDS row stride of a V tile: conflict-free transpose reads
   constexpr int CPR = D / 8;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;  // rows per V load instruction
   constexpr int VL = 32 / RPI;   // V load instructions per tile
   constexpr int KS = D + 8;      // LDS row stride of a K tile: conflict-free row-fragment reads
-  __shared__ __attribute__((aligned(16))) bf16 vst[kPvWaves][32 * VS];
-  __shared__ __attribute__((aligned(16))) bf16 kst[kPvWaves][32 * KS];
-
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
-  const int nblk = (nqt + kPvWaves - 1) / kPvWaves;
-  int bh, blk;
-  {
-    const int bid = blockIdx.x;
-    if (BH % 8 == 0) {  // one head's blocks consecutive on one XCD, longest first
-      const int x = bid & 7, j = bid >> 3;
-      bh = x + 8 * (j / nblk);
-      blk = nblk - 1 - j % nblk;
-    } else {
-      bh = bid / nblk;
-      blk = nblk - 1 - bid % nblk;
-    }
-  }
-  const int qt = kPvWaves * blk + wv;
-  if (qt >= nqt) return;
-  if (NORM && P.cand) {  // fwd_pv_cand takes the query tiles whose candidate lists all fit
-    const uint32_t* counts = P.cand + pair_lists(BR, BH, nqt) * kCandCap;
-    bool fit = true;
-#pragma unroll
-    for (int br = 0; br < BR; ++br) fit = fit && counts[((int64_t)br * BH + bh) * nqt + qt] <= (uint32_t)kCandCap;
-    if (fit) return;
-  }
   const int b = bh / P.H, h = bh % P.H;
   const int iq = 32 * qt + n32;
   const bool valid = iq < Nq;
@@ -443,8 +414,8 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
   float lam = 0.f;
   if constexpr (BR == 2) lam = clamp01(*P.lam);
 
-  bf16* vt = vst[wv];
-  bf16* ktl = kst[wv];
+  bf16* vt = vt_;
+  bf16* ktl = kt_;
   const int vrow = l / CPR, vch = l % CPR;
   const int bk = l >> 4, jj = l & 15;
   const int voff = (4 * (bk >> 1) + (jj >> 2)) * VS + 16 * (bk & 1) + 4 * (jj & 3);
@@ -590,6 +561,53 @@ __global__ void __launch_bounds__(64 * kPvWaves) __attribute__((amdgpu_waves_per
   if (P.stats && l == 0 && checked) {
     atomicAdd(P.stats + 1, (unsigned long long)computed);
     atomicAdd(P.stats + 2, (unsigned long long)checked);
+  }
+}
+
+// Query tile of tile-pass item `item`: one head's query tiles consecutive on one XCD (when the
+// heads fill the eight XCDs), longest (last query tile) first.
+__device__ __forceinline__ void pv_item(int item, int BH, int nqt, int& bh, int& qt) {
+  if (BH % 8 == 0) {
+    const int x = item & 7, j = item >> 3;
+    bh = x + 8 * (j / nqt);
+    qt = nqt - 1 - j % nqt;
+  } else {
+    bh = item / nqt;
+    qt = nqt - 1 - item % nqt;
+  }
+}
+
+// One wave per workgroup and `per_wave` consecutive items per wave: the work per query tile
+// varies with its number of non-zero tiles, and single-wave workgroups retire independently.
+// With candidate lists (normalised bf16) the items whose lists all fit belong to fwd_pv_cand:
+// the wave tests its items' counts in one lane-parallel round and runs only the others, so a
+// launch where every list fits costs a few waves per SIMD (per_wave 4) instead of one per
+// query tile; without lists every item runs (per_wave 1).
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fwd_pv(FwdParams P, int per_wave) {
+  constexpr int VS = D + 32, KS = D + 8;
+  __shared__ __attribute__((aligned(16))) bf16 vst[32 * VS];
+  __shared__ __attribute__((aligned(16))) bf16 kst[32 * KS];
+  const int l = lane_id();
+  const int BH = P.B * P.H, nqt = P.nqt, n = BH * nqt;
+  const int first = (int)blockIdx.x * per_wave;
+  bool need = false;
+  if (l < per_wave && first + l < n) {
+    int bh, qt;
+    pv_item(first + l, BH, nqt, bh, qt);
+    need = true;
+    if (NORM && P.cand) {
+      const uint32_t* counts = P.cand + pair_lists(BR, BH, nqt) * kCandCap;
+      bool fit = true;
+#pragma unroll
+      for (int br = 0; br < BR; ++br) fit = fit && counts[((int64_t)br * BH + bh) * nqt + qt] <= (uint32_t)kCandCap;
+      need = !fit;
+    }
+  }
+  for (uint64_t m = wave_ballot(need); m; m &= m - 1ull) {
+    int bh, qt;
+    pv_item(first + __builtin_ctzll(m), BH, nqt, bh, qt);
+    fwd_pv_tile<D, BR, PK, NORM>(P, vst, kst, bh, qt);
   }
 }
 
@@ -817,8 +835,9 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   hipLaunchKernelGGL((fwd_screen<D, NORM, QPW, TPB>), dim3((unsigned)(BR * BH) * nqb), dim3(512 / QPW), 0, s, p, BR);
   if (NORM && p.cand)
     hipLaunchKernelGGL((fwd_pv_cand<D, BR, PK>), dim3((unsigned)(BH * p.nqt)), dim3(64), 0, s, p);
-  const unsigned nblk = (unsigned)((p.nqt + kPvWaves - 1) / kPvWaves);
-  hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)BH * nblk), dim3(64 * kPvWaves), 0, s, p);
+  const int per_wave = NORM && p.cand ? 4 : 1;  // with candidate lists most items exit at once
+  const unsigned pv_waves = (unsigned)((BH * p.nqt + per_wave - 1) / per_wave);
+  hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3(pv_waves), dim3(64), 0, s, p, per_wave);
   return (int)hipGetLastError();
 }
 
