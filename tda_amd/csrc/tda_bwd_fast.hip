@@ -502,6 +502,7 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   // the count and every entry slot at once (slots past the count are never used)
   const PairLanes PL = load_pairs(P.pairs + lidx * (4 * kPairCap), (uint32_t)kPairCap);
   const uint32_t npairs = P.pairs[pair_lists(BR, BH, P.nqt) * 4 * kPairCap + lidx];
+  if (P.dkvq && item == 0 && l == 0) P.dkvq[0] = 0u;  // the key-major pair pass fills it later
   if (npairs > (uint32_t)kPairCap) return;  // bwd_dq_fast walks the tiles
 
   auto base = [&](int slot) {
@@ -794,7 +795,10 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
     }
     np += (uint32_t)__builtin_popcountll(mm);
   });
-  if (!fits) return;  // bwd_dkv_fast takes the key tile
+  if (!fits) {  // bwd_dkv_fast takes the key tile
+    if (P.dkvq && l == 0) P.dkvq[1 + atomicAdd(P.dkvq, 1u)] = (uint32_t)item;
+    return;
+  }
   wave_lds_sync();  // slots written by other lanes
   const bool slotted = np <= (uint32_t)kColPairs;
 
@@ -987,17 +991,12 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
 }
 
 // ------------------------------------------------------------------ key-major pass
+// The tile pass over one key tile (item = (key tile, head)): one wave, W its LDS.
 template <int D, int BR, int PK, bool NORM>
-__global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
+__device__ __forceinline__ void bwd_dkv_tile(const BwdParams& P, BwdWaveLds<D>& W, int64_t item) {
   constexpr int NT = D / 16, ND = D / 32;
-  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> lds_all[kBwdWaves];
-
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  BwdWaveLds<D>& W = lds_all[wv];
   const int BH = P.B * P.H;
-  const int64_t item = (int64_t)blockIdx.x * kBwdWaves + wv;
-  if (item >= (int64_t)BH * P.nkt) return;  // whole wave leaves; no workgroup barriers below
   const int kt = (int)(item / BH);
   const int bh = (int)(item % BH);
   const int b = bh / P.H, h = bh % P.H;
@@ -1006,7 +1005,6 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
   const bool kvalid = j < Nk;
   const int jc = min(j, Nk - 1);
   const int qtf = qt_first(kt, qoff);  // first query tile that sees the key tile
-  if (P.pairs && !column_overflows<BR>(P, bh, kt, qtf)) return;  // bwd_dkv_pairs takes the key tile
   auto base = [&](int slot) {
     return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
   };
@@ -1129,6 +1127,68 @@ __global__ void __launch_bounds__(64 * kBwdWaves) bwd_dkv_fast(BwdParams P) {
   }
 }
 
+// Bit k set when the column of key-major item first + k (k < count <= 4) has a list that did
+// not fit (the test of column_overflows): the bitmask bits and counts of the first 128 query
+// tiles of every column in one round, longer columns' rest column by column.
+template <int BR>
+__device__ __forceinline__ uint32_t columns_overflow(const BwdParams& P, int64_t first, int count) {
+  const int BH = P.B * P.H, l = lane_id();
+  const uint32_t* counts = P.pairs + pair_lists(BR, BH, P.nqt) * 4 * kPairCap;
+  int kt[4], bh[4], qtf[4];
+  bool ovf[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t item = first + (k < count ? k : 0);
+    kt[k] = (int)(item / BH);
+    bh[k] = (int)(item % BH);
+    qtf[k] = qt_first(kt[k], P.qoff);
+    ovf[k] = false;
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int br = 0; br < BR; ++br) {
+        const int qt = qtf[k] + 64 * c + l;
+        const bool in = k < count && qt < P.nqt;
+        const int64_t row = ((int64_t)br * BH + bh[k]) * P.nqt + (in ? qt : P.nqt - 1);
+        const uint32_t w = P.occ[row * P.occ_w + (kt[k] >> 5)];
+        const uint32_t n = counts[row];
+        ovf[k] = ovf[k] || (in && ((w >> (kt[k] & 31)) & 1u) && n > (uint32_t)kPairCap);
+      }
+  uint32_t out = 0u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (k >= count) continue;
+    bool o = wave_ballot(ovf[k]) != 0ull;
+    if (!o && qtf[k] + 128 < P.nqt) o = column_overflows<BR>(P, bh[k], kt[k], qtf[k] + 128);
+    out |= o ? 1u << k : 0u;
+  }
+  return out;
+}
+
+// One wave per workgroup and `per_wave` consecutive items per wave.  With pair lists, the key
+// tiles whose columns have only lists that fit belong to bwd_dkv_pairs: the wave tests its
+// items' columns in one round and runs only the others (per_wave 4); without lists every item
+// runs (per_wave 1).
+// With the key-tile queue (per_wave 0), the waves take the queued key tiles in turn instead.
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(64) bwd_dkv_fast(BwdParams P, int per_wave) {
+  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> W;
+  if (per_wave == 0) {
+    const uint32_t queued = P.dkvq[0];
+    for (uint32_t k = blockIdx.x; k < queued; k += gridDim.x) bwd_dkv_tile<D, BR, PK, NORM>(P, W, P.dkvq[1 + k]);
+    return;
+  }
+  const int64_t n = (int64_t)P.B * P.H * P.nkt, first = (int64_t)blockIdx.x * per_wave;
+  const int count = (int)min((int64_t)per_wave, n - first);
+  if (count <= 0) return;
+  uint32_t run = count >= 32 ? 0xffffffffu : (1u << count) - 1u;
+  if (P.pairs) run = columns_overflow<BR>(P, first, count);
+  for (; run; run &= run - 1u) bwd_dkv_tile<D, BR, PK, NORM>(P, W, first + __builtin_ctz(run));
+}
+
 // ------------------------------------------------------------------ dispatch
 template <int D, int BR, int PK, bool NORM>
 static int launch_t(const BwdParams& p, void* stream) {
@@ -1139,8 +1199,14 @@ static int launch_t(const BwdParams& p, void* stream) {
   hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3((unsigned)((qitems + dq_per_wave - 1) / dq_per_wave)),
                      dim3(64), 0, s, p, dq_per_wave);
   if (p.pairs) hipLaunchKernelGGL((bwd_dkv_pairs<D, BR, PK, NORM>), dim3((unsigned)kitems), dim3(64), 0, s, p);
-  hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3((unsigned)((kitems + kBwdWaves - 1) / kBwdWaves)),
-                     dim3(64 * kBwdWaves), 0, s, p);
+  if (p.dkvq) {  // the key tiles the pair pass could not take, from its queue: one wave per SIMD
+    hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3((unsigned)(kitems < 1024 ? kitems : 1024)), dim3(64), 0, s,
+                       p, 0);
+  } else {
+    const int dkv_per_wave = p.pairs ? 4 : 1;  // with pair lists most key tiles exit at once
+    hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3((unsigned)((kitems + dkv_per_wave - 1) / dkv_per_wave)),
+                       dim3(64), 0, s, p, dkv_per_wave);
+  }
   const int e = (int)hipGetLastError();
   return e ? e : launch_bwd_finish(p, BR, qitems, stream);
 }

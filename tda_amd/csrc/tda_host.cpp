@@ -178,8 +178,10 @@ size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, in
   (void)head_dim;
   if (batch < 1 || heads < 1 || seq_len < 1) return 0;
   // per (branch, head, query tile), for two branches: one (dbeta, dlambda) partial pair, then
-  // the dk weight of each pair-list slot
-  return (size_t)(2 * batch * heads * ceil_div(seq_len, 32)) * (2 + tda::kPairCap) * sizeof(float);
+  // the dk weight of each pair-list slot; then a queue of key tiles (a count and as many items
+  // as dk weights; used when every key tile fits, i.e. Nk <= 64 Nq)
+  const int64_t lists = 2 * batch * heads * ceil_div(seq_len, 32);
+  return (size_t)(lists * (2 + tda::kPairCap) + 64 + lists * tda::kPairCap) * sizeof(float);
 }
 
 int32_t tda_validate_fwd(const tda_fwd_args* a) {
@@ -303,9 +305,13 @@ int32_t tda_bwd(const tda_bwd_args* a, void* stream) {
   p.norms = a->normalize ? a->norms : nullptr;
   p.occ = a->occupancy;
   p.ws = static_cast<float*>(a->workspace);
-  p.pws = p.ws + 2 * 2 * (int64_t)a->batch * a->heads * p.nqt;  // after the partial pairs
+  const int64_t lists = 2 * (int64_t)a->batch * a->heads * p.nqt;
+  p.pws = p.ws + 2 * lists;  // after the partial pairs
   p.stats = a->stats;
   p.pairs = a->occupancy ? a->pairs : nullptr;  // the key-major pass finds the lists through the bitmask
+  // the key-tile queue, when it holds every key tile
+  if (p.pairs && (int64_t)a->batch * a->heads * p.nkt <= lists * tda::kPairCap)
+    p.dkvq = reinterpret_cast<uint32_t*>(p.pws + lists * tda::kPairCap);
   const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};
   const int e = tda::launch_bwd(p, key, stream);
   if (e != 0) {

@@ -80,6 +80,9 @@ struct BwdParams {
   const uint32_t* pairs;     // may be null: the forward's pair lists (used with occ)
   float* pws;                // [pair lists][kPairCap] dk weight of each pair (workspace), written by
                              // the query-major pair pass, read by the key-major one
+  uint32_t* dkvq;            // may be null: key tiles for the key-major tile pass ([0] count, then
+                             // items), zeroed by the query-major pair pass, filled by the key-major
+                             // pair pass (workspace)
 };
 
 // Kernel-family launchers (return a hipError_t value).  Template selection happens inside.

@@ -236,8 +236,10 @@ def test_buffer_sizes():
     assert lib.tda_occupancy_words(1, 1, 33, 3) == 0
     assert lib.tda_norms_floats(4, 16, 4096, 2) == 4 * 64 * 4096
     assert lib.tda_norms_floats(1, 8, 128, 1) == 2 * 8 * 128
-    # two branches: partial pairs and one dk weight per pair-list slot (32)
-    assert lib.tda_bwd_workspace_bytes(4, 16, 4096, 128) == 2 * 64 * 128 * (2 + 32) * 4
+    # two branches: partial pairs and one dk weight per pair-list slot (32), then a key-tile
+    # queue (a count block of 64 words and one item per pair-list slot)
+    lists = 2 * 64 * 128
+    assert lib.tda_bwd_workspace_bytes(4, 16, 4096, 128) == (lists * (2 + 32) + 64 + lists * 32) * 4
     # bitmask scratch, rounded up to 256 bytes, then the candidate lists
     assert lib.tda_fwd_workspace_bytes(4, 16, 4096, 2) == 2 * 64 * 128 * 4 * 4 + cand(2 * 64 * 128)
     assert lib.tda_fwd_workspace_bytes(1, 1, 33, 1) == 256 + cand(2)
