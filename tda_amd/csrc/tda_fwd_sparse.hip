@@ -169,6 +169,7 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
   const int l = lane_id(), n32 = l & 31, g = l >> 5, tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
+  if (NORM && P.pvq && blockIdx.x == 0 && tid == 0) P.pvq[0] = 0u;  // the candidate pass fills it
   const WorkItem wi = xcd_order(blockIdx.x, BR * BH, (Nq + 255) / 256);
   const int sidx = wi.stream, qb = wi.block;
   const int br = sidx / BH, bh = sidx % BH;
@@ -583,6 +584,7 @@ __device__ __forceinline__ void pv_item(int item, int BH, int nqt, int& bh, int&
 // the wave tests its items' counts in one lane-parallel round and runs only the others, so a
 // launch where every list fits costs a few waves per SIMD (per_wave 4) instead of one per
 // query tile; without lists every item runs (per_wave 1).
+// With the candidate pass's queue (per_wave 0), the waves take the queued query tiles in turn.
 template <int D, int BR, int PK, bool NORM>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fwd_pv(FwdParams P, int per_wave) {
   constexpr int VS = D + 32, KS = D + 8;
@@ -590,6 +592,14 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
   __shared__ __attribute__((aligned(16))) bf16 kst[32 * KS];
   const int l = lane_id();
   const int BH = P.B * P.H, nqt = P.nqt, n = BH * nqt;
+  if (per_wave == 0) {
+    const uint32_t queued = P.pvq[0];
+    for (uint32_t k = blockIdx.x; k < queued; k += gridDim.x) {
+      const int v = (int)P.pvq[1 + k];
+      fwd_pv_tile<D, BR, PK, NORM>(P, vst, kst, v / nqt, v % nqt);
+    }
+    return;
+  }
   const int first = (int)blockIdx.x * per_wave;
   bool need = false;
   if (l < per_wave && first + l < n) {
@@ -655,9 +665,13 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
 #pragma unroll
   for (int br = 0; br < BR; ++br) nc[br] = counts[((int64_t)br * BH + bh) * nqt + qt];
   const int kraw = (int)P.cand[(((int64_t)(BR == 2 ? (l >> 5) : 0) * BH + bh) * nqt + qt) * kCandCap + (l & 31)];
+  bool fit = true;
 #pragma unroll
-  for (int br = 0; br < BR; ++br)
-    if (nc[br] > (uint32_t)kCandCap) return;  // fwd_pv walks the bitmask tiles
+  for (int br = 0; br < BR; ++br) fit = fit && nc[br] <= (uint32_t)kCandCap;
+  if (!fit) {  // fwd_pv walks the bitmask tiles
+    if (l == 0) P.pvq[1 + atomicAdd(P.pvq, 1u)] = (uint32_t)(bh * nqt + qt);
+    return;
+  }
 
   const int b = bh / P.H, h = bh % P.H;
   const int iq = 32 * qt + n32;
@@ -835,9 +849,12 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   hipLaunchKernelGGL((fwd_screen<D, NORM, QPW, TPB>), dim3((unsigned)(BR * BH) * nqb), dim3(512 / QPW), 0, s, p, BR);
   if (NORM && p.cand)
     hipLaunchKernelGGL((fwd_pv_cand<D, BR, PK>), dim3((unsigned)(BH * p.nqt)), dim3(64), 0, s, p);
-  const int per_wave = NORM && p.cand ? 4 : 1;  // with candidate lists most items exit at once
-  const unsigned pv_waves = (unsigned)((BH * p.nqt + per_wave - 1) / per_wave);
-  hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3(pv_waves), dim3(64), 0, s, p, per_wave);
+  if (NORM && p.cand) {  // the query tiles the candidate pass could not take, from its queue
+    const int items = BH * p.nqt;
+    hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)(items < 2048 ? items : 2048)), dim3(64), 0, s, p, 0);
+  } else {
+    hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)(BH * p.nqt)), dim3(64), 0, s, p, 1);
+  }
   return (int)hipGetLastError();
 }
 

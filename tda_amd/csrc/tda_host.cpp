@@ -82,9 +82,14 @@ int64_t fwd_part_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv) {
   return round256(bh * ceil_div(ceil_div(seq_len_kv, 32), 32) * seq_len * 128 * (int64_t)sizeof(float));
 }
 // ... or, with more than one query tile, the candidate lists of the bf16 screen.
+// ... and a queue of query tiles for the tile pass (a count block, one item per (head, tile)).
+int64_t fwd_cand_list_bytes(int64_t bh, int64_t seq_len, int64_t branches) {
+  return round256(tda::cand_words(branches * bh * ceil_div(seq_len, 32)) * (int64_t)sizeof(uint32_t));
+}
 int64_t fwd_cand_bytes(int64_t bh, int64_t seq_len, int64_t branches) {
   if (seq_len <= 32) return 0;
-  return round256(tda::cand_words(branches * bh * ceil_div(seq_len, 32)) * (int64_t)sizeof(uint32_t));
+  return fwd_cand_list_bytes(bh, seq_len, branches) +
+         round256((64 + bh * ceil_div(seq_len, 32)) * (int64_t)sizeof(uint32_t));
 }
 int64_t fwd_ws_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t branches) {
   return fwd_occ_bytes(bh, seq_len, seq_len_kv, branches) + fwd_part_bytes(bh, seq_len, seq_len_kv) +
@@ -254,7 +259,10 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
   char* after_occ = static_cast<char*>(a->workspace) +
                    fwd_occ_bytes(a->batch * a->heads, a->seq_len, c.seq_len_kv, a->branches);
   if (a->seq_len <= 32) p.part = reinterpret_cast<float*>(after_occ);
-  else p.cand = reinterpret_cast<uint32_t*>(after_occ);
+  else {
+    p.cand = reinterpret_cast<uint32_t*>(after_occ);
+    p.pvq = reinterpret_cast<uint32_t*>(after_occ + fwd_cand_list_bytes(a->batch * a->heads, a->seq_len, a->branches));
+  }
   p.stats = a->stats;
   p.pairs = a->pairs;
   p.nbr = a->branches;

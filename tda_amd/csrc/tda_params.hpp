@@ -60,6 +60,8 @@ struct FwdParams {
   uint32_t* pairs;           // may be null: pair lists (bf16)
   int nbr;                   // branches
   uint32_t* cand;            // candidate keys (workspace; null for a single query tile)
+  uint32_t* pvq;             // with cand: query tiles for the tile pass ([0] count, then bh nqt + qt),
+                             // zeroed by the screen, filled by the candidate pass (workspace)
 };
 
 struct BwdParams {

@@ -229,9 +229,11 @@ def test_buffer_sizes():
     assert lib.tda_norms_floats_kv(2, 3, 10, 10, 1) == lib.tda_norms_floats(2, 3, 10, 1)
     # one query tile: + the decode partials, [B*H][ceil(key tiles / 32)][Nq][128] floats
     assert lib.tda_fwd_workspace_bytes_kv(1, 1, 1, 5000, 1) == 256 + 5 * 1 * 128 * 4
-    # more query tiles: + the candidate keys, per list 32 keys and a count
-    cand = lambda lists: 256 * ((lists * (1 + 32) * 4 + 255) // 256)  # noqa: E731
-    assert lib.tda_fwd_workspace_bytes_kv(1, 1, 33, 5000, 1) == 256 * ((2 * 5 * 4 + 255) // 256) + cand(2)
+    # more query tiles: + the candidate keys, per list 32 keys and a count, then a queue of query
+    # tiles (a count block of 64 words and one item per head and query tile)
+    r256 = lambda b: 256 * ((b + 255) // 256)  # noqa: E731
+    cand = lambda lists, tiles: r256(lists * (1 + 32) * 4) + r256((64 + tiles) * 4)  # noqa: E731
+    assert lib.tda_fwd_workspace_bytes_kv(1, 1, 33, 5000, 1) == 256 * ((2 * 5 * 4 + 255) // 256) + cand(2, 2)
     assert lib.tda_occupancy_words_kv(1, 1, 33, 0, 2) == 0
     assert lib.tda_occupancy_words(1, 1, 33, 3) == 0
     assert lib.tda_norms_floats(4, 16, 4096, 2) == 4 * 64 * 4096
@@ -241,8 +243,8 @@ def test_buffer_sizes():
     lists = 2 * 64 * 128
     assert lib.tda_bwd_workspace_bytes(4, 16, 4096, 128) == (lists * (2 + 32) + 64 + lists * 32) * 4
     # bitmask scratch, rounded up to 256 bytes, then the candidate lists
-    assert lib.tda_fwd_workspace_bytes(4, 16, 4096, 2) == 2 * 64 * 128 * 4 * 4 + cand(2 * 64 * 128)
-    assert lib.tda_fwd_workspace_bytes(1, 1, 33, 1) == 256 + cand(2)
+    assert lib.tda_fwd_workspace_bytes(4, 16, 4096, 2) == 2 * 64 * 128 * 4 * 4 + cand(2 * 64 * 128, 64 * 128)
+    assert lib.tda_fwd_workspace_bytes(1, 1, 33, 1) == 256 + cand(2, 2)
     assert lib.tda_fwd_workspace_bytes(1, 1, 33, 3) == 0
     assert lib.tda_occupancy_words(0, 1, 1, 1) == 0
 
