@@ -221,4 +221,37 @@ __device__ __forceinline__ f32x4 load4(const bf16* p) {
 }
 __device__ __forceinline__ f32x4 load4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
+
+// ------------------------------------------------------------------ swizzled LDS tiles
+#define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte chunk swizzle of a row-major 32-row tile (D/8 chunks per row).  Conflict-free for the
+// row-fragment reads (32 rows, one chunk each) and for the transpose reads (4 rows x 2 chunks
+// per 16 lanes), with 32 or 64 banks.
+template <int D>
+__device__ __forceinline__ int bswz(int r) {
+  if constexpr (D == 128) return (r ^ (4 * (r & 3))) & 15;
+  else return ((r ^ (r >> 1)) ^ (2 * (r & 1)) ^ (4 * ((r >> 1) & 1))) & 7;
+}
+
+// Transposed fragment (step st over the 32 rows, column block dsub): lane (n, g) gets column
+// 32*dsub + n at tile rows crow(8*st + j, g), j = 0..7.
+template <int D>
+__device__ __forceinline__ bf16x8 tile_tr_frag(const bf16* tile, int st, int dsub) {
+  const int l = lane_id(), bk = l >> 4, j = l & 15;
+  const int d = 32 * dsub + 16 * (bk & 1) + 4 * (j & 3);
+  bf16x8 out;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int r = 16 * st + 8 * hh + 4 * (bk >> 1) + (j >> 2);
+    const bf16* p = tile + r * D + 8 * ((d >> 3) ^ bswz<D>(r)) + (d & 7);
+    const bf16x4 w = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(s16x4, p)));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[4 * hh + e] = w[e];
+  }
+  return out;
+}
+
 }  // namespace tda

@@ -30,9 +30,6 @@
 namespace tda {
 namespace {
 
-#define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // Raw buffer descriptor over [base, base + bytes): loads past the end return zeros.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -623,25 +620,23 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
 
 // ------------------------------------------------------------------ fwd_pv_cand
 // The exact pass of the query tiles whose candidate-key lists (every branch, normalised scores)
-// fit: per branch the candidate keys' K and V rows are gathered into one 32-row tile (row c =
-// candidate c, rows past the count zero), the score tile is computed with the instruction
-// sequence of fwd_pv (the same rows in the same operands: bitwise the same scores), and the
-// exact weights with the causal mask accumulate out += coef A V as in fwd_pv.  One gather round
+// fit: per branch the score tile of the query rows against the candidate keys' rows (row c =
+// candidate c, rows past the count zero) is computed with the MFMA sequence of fwd_pv, its
+// operands loaded straight from the rows (the same values in the same operands: bitwise the same
+// scores); the candidates' V rows go to a swizzled LDS tile by direct loads, and the exact
+// weights with the causal mask accumulate out += coef A V as in fwd_pv.  One gather round
 // per branch replaces one per kept key tile.  The bitmask row is rewritten from the key tiles
 // holding a non-zero weight; the pair list takes the non-zero weights in the order (value r,
 // lane).
 template <int D, int BR, int PK>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fwd_pv_cand(FwdParams P) {
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fwd_pv_cand(FwdParams P) {
   constexpr int NT = D / 16, ND = D / 32;
-  constexpr int VS = D + 32;     // LDS row stride of the V tile: conflict-free transpose reads
   constexpr int CPR = D / 8;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;  // rows per load instruction
   constexpr int VL = 32 / RPI;   // load instructions per tile
-  constexpr int KS = D + 8;      // LDS row stride of the K tile: conflict-free row-fragment reads
-  __shared__ __attribute__((aligned(16))) bf16 vt[32 * VS];
-  __shared__ __attribute__((aligned(16))) bf16 ktl[32 * KS];
-  __shared__ __attribute__((aligned(16))) int ckey[32];    // candidate keys (padding: -1)
-  __shared__ __attribute__((aligned(16))) float crk[32];  // their inverse norms
+  __shared__ __attribute__((aligned(16))) bf16 vt[32 * D];  // V rows, chunk-swizzled (bswz)
+  __shared__ __attribute__((aligned(16))) int ckey[32];     // candidate keys (padding: -1)
+  __shared__ __attribute__((aligned(16))) float crk[32];   // their inverse norms
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
@@ -684,8 +679,6 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
   float lam = 0.f;
   if constexpr (BR == 2) lam = clamp01(*P.lam);
   const int vrow = l / CPR, vch = l % CPR;
-  const int bk = l >> 4, jj = l & 15;
-  const int voff = (4 * (bk >> 1) + (jj >> 2)) * VS + 16 * (bk & 1) + 4 * (jj & 3);
 
   f32x16 O[ND];
 #pragma unroll
@@ -705,50 +698,49 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
       const bf16* vhead = (const bf16*)P.in[F_V] + (int64_t)b * P.s[F_V][0] + (int64_t)h * P.s[F_V][1];
       const int64_t sq = P.s[qslot][2], sk = P.s[kslot][2], sv = P.s[F_V][2];
       const float coef = br == 0 ? 1.f : -lam;
-      // every load of the branch in one round: the candidate keys (lane c < n), their norms,
-      // the query rows, the gathered key and value rows
       const int kb = __shfl(kraw, (32 * br + (l & 31)) & 63);  // this branch's slots: lanes 32 br ..
       const int key_l = l < (int)n ? kb : -1;
       const float rk_l = key_l >= 0 ? P.norms[norm_base(P, br ? N_K2 : N_K1, bh) + key_l] : 0.f;
       const float rq = P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + min(iq, Nq - 1)];
-      u32x4 qr[VL], kr[VL], vr[VL];
+      // Every load of the branch in one round.  The operands of the score MFMAs straight from
+      // the rows (lane (m, g): elements 16 t + 8 g .. of query row m, and of candidate m's key
+      // row): no LDS staging.  V rows by direct global->LDS loads into the swizzled tile (rows
+      // past the count take candidate 0's row, zeroed below).
+      const int key_m = __shfl(key_l, n32);
+      const int key0 = __builtin_amdgcn_readfirstlane(key_l);
+      const bf16* qrow = qhead + (int64_t)min(iq, Nq - 1) * sq;
+      const bf16* krow = khead + (int64_t)(key_m >= 0 ? key_m : key0) * sk;
+      bf16x8 Q[NT], K[NT];
 #pragma unroll
-      for (int i = 0; i < VL; ++i) {
-        const int row = vrow + RPI * i;
-        qr[i] = *reinterpret_cast<const u32x4*>(qhead + (int64_t)min(32 * qt + row, Nq - 1) * sq + 8 * vch);
-        const int key = __shfl(key_l, row);
-        kr[i] = vr[i] = u32x4{0u, 0u, 0u, 0u};
-        if (key >= 0) {
-          kr[i] = *reinterpret_cast<const u32x4*>(khead + (int64_t)key * sk + 8 * vch);
-          vr[i] = *reinterpret_cast<const u32x4*>(vhead + (int64_t)key * sv + 8 * vch);
-        }
+      for (int t = 0; t < NT; ++t) {
+        Q[t] = *reinterpret_cast<const bf16x8*>(qrow + 16 * t + 8 * g);
+        K[t] = *reinterpret_cast<const bf16x8*>(krow + 16 * t + 8 * g);
       }
-      // query fragments through the K tile buffer, then the gathered rows
-      wave_lds_sync();
+      wave_lds_sync();  // the previous branch's reads of the tile are done
 #pragma unroll
-      for (int i = 0; i < VL; ++i) *reinterpret_cast<u32x4*>(ktl + (vrow + RPI * i) * KS + 8 * vch) = qr[i];
+      for (int u = 0; u < VL; ++u) {
+        const int r = u * RPI + l / CPR;
+        const int key = __shfl(key_l, r);
+        const int c = (l % CPR) ^ bswz<D>(r);
+        __builtin_amdgcn_global_load_lds((const void*)(vhead + (int64_t)(key >= 0 ? key : key0) * sv + 8 * c),
+                                         LDS_PTR(void, vt + u * RPI * D), 16, 0, 0);
+      }
       if (l < 32) {
         ckey[l] = key_l;
         crk[l] = rk_l;
       }
-      wave_lds_sync();
-      bf16x8 Q[NT];
-      {
-        const bf16* qp = ktl + n32 * KS + 8 * g;
+      __builtin_amdgcn_s_waitcnt(0);
+      if (n < 32u) {  // rows past the count: zeros (their weights are zero; keep them finite)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) Q[t] = *reinterpret_cast<const bf16x8*>(qp + 16 * t);
-      }
-      wave_lds_sync();
-#pragma unroll
-      for (int i = 0; i < VL; ++i) {
-        *reinterpret_cast<u32x4*>(ktl + (vrow + RPI * i) * KS + 8 * vch) = kr[i];
-        *reinterpret_cast<u32x4*>(vt + (vrow + RPI * i) * VS + 8 * vch) = vr[i];
+        for (int u = 0; u < VL; ++u) {
+          const int r = u * RPI + l / CPR;
+          if (r >= (int)n) *reinterpret_cast<u32x4*>(vt + r * D + 8 * (l % CPR)) = u32x4{0u, 0u, 0u, 0u};
+        }
       }
       wave_lds_sync();
       f32x16 S = {};
-      const bf16* kp = ktl + n32 * KS + 8 * g;
 #pragma unroll
-      for (int t = 0; t < NT; ++t) S = PolBF16::mma(*reinterpret_cast<const bf16x8*>(kp + 16 * t), Q[t], S);
+      for (int t = 0; t < NT; ++t) S = PolBF16::mma(key_m >= 0 ? K[t] : bf16x8{}, Q[t], S);
       // value r of the lane: candidate crow(r, g)
       f32x4 rk4[4];
       u32x4 key4[4];
@@ -782,11 +774,10 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
         }
       if (cnz) {
         const bf16x8 PF0 = PolBF16::pack_c(C, 0), PF1 = PolBF16::pack_c(C, 1);
-        const bf16* vp = vt + voff;
 #pragma unroll
         for (int c = 0; c < ND; ++c) {
-          O[c] = PolBF16::mma(tr_frag<VS>(vp + 32 * c), PF0, O[c]);
-          O[c] = PolBF16::mma(tr_frag<VS>(vp + 32 * c + 16 * VS), PF1, O[c]);
+          O[c] = PolBF16::mma(tile_tr_frag<D>(vt, 0, c), PF0, O[c]);
+          O[c] = PolBF16::mma(tile_tr_frag<D>(vt, 1, c), PF1, O[c]);
         }
       }
       // the bitmask row: lane w rewrites word w from the key tiles of the candidates with a
@@ -808,13 +799,15 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
     if (P.pairs && l == 0) P.pairs[pair_lists(P.nbr, BH, nqt) * 4 * kPairCap + lidx] = npairs;
   }
 
-  // Output rows through LDS (the K tile buffer), as in fwd_pv.
+  // Output rows through LDS (the swizzled V tile): lane (n, g) holds elements 32c + crow(r, g) of
+  // row n, i.e. half g of chunk 4c + u for values 4u .. 4u + 3; stores then cover whole rows.
   wave_lds_sync();
 #pragma unroll
   for (int c = 0; c < ND; ++c)
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      store4(ktl + n32 * KS + 32 * c + 8 * u + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2], O[c][4 * u + 3]);
+      store4(vt + n32 * D + 8 * ((4 * c + u) ^ bswz<D>(n32)) + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2],
+             O[c][4 * u + 3]);
   wave_lds_sync();
   {
     bf16* ohead = (bf16*)P.out + (int64_t)b * P.s[F_OUT][0] + (int64_t)h * P.s[F_OUT][1];
@@ -823,7 +816,7 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
       const int r = vrow + RPI * i, row = 32 * qt + r;
       if (row < Nq)
         *reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch) =
-            *reinterpret_cast<const u32x4*>(ktl + r * KS + 8 * vch);
+            *reinterpret_cast<const u32x4*>(vt + r * D + 8 * (vch ^ bswz<D>(r)));
     }
   }
   if (P.stats) {
