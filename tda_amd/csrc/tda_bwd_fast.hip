@@ -391,7 +391,9 @@ __device__ __forceinline__ RowVec<D> unpack(RowRaw<D> r) {
 template <int D>
 __device__ __forceinline__ void store_rowvec(bf16* row, const RowVec<D>& r) {
   const int l = lane_id();
-  if constexpr (D == 128) *reinterpret_cast<bf16x2*>(row + 2 * l) = bf16x2{(bf16)r.v[0], (bf16)r.v[1]};
+  if constexpr (D == 128)
+    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, bf16x2{(bf16)r.v[0], (bf16)r.v[1]}),
+                                reinterpret_cast<uint32_t*>(row + 2 * l));
   else row[l] = (bf16)r.v[0];
 }
 template <int D>
@@ -422,8 +424,8 @@ __device__ __forceinline__ void zero_rows(bf16* tile0, int64_t st, int nrows, ui
 #pragma unroll
   for (int u = 0; u < 32 / RPI; ++u) {
     const int r = u * RPI + l / CH;
-    if (r < nrows && !((keep >> r) & 1u))
-      *reinterpret_cast<u32x4*>(tile0 + (int64_t)r * st + 8 * (l % CH)) = u32x4{0u, 0u, 0u, 0u};
+    if (r < nrows && !((keep >> r) & 1u))  // streaming stores: nothing reads them soon
+      __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u}, reinterpret_cast<u32x4*>(tile0 + (int64_t)r * st + 8 * (l % CH)));
   }
 }
 
