@@ -552,8 +552,8 @@ __device__ __forceinline__ void fwd_pv_tile(const FwdParams& P, bf16* vt_, bf16*
     for (int i = 0; i < VL; ++i) {
       const int r = vrow + RPI * i, row = 32 * qt + r;
       if (row < Nq)
-        *reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch) =
-            *reinterpret_cast<const u32x4*>(ktl + r * KS + 8 * vch);
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(ktl + r * KS + 8 * vch),
+                                    reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch));
     }
   }
   if (P.stats && l == 0 && checked) {
@@ -800,7 +800,8 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
   }
 
   // Output rows through LDS (the swizzled V tile): lane (n, g) holds elements 32c + crow(r, g) of
-  // row n, i.e. half g of chunk 4c + u for values 4u .. 4u + 3; stores then cover whole rows.
+  // row n, i.e. half g of chunk 4c + u for values 4u .. 4u + 3; stores then cover whole rows
+  // (streaming stores, as in fwd_pv: nothing here reads the output again).
   wave_lds_sync();
 #pragma unroll
   for (int c = 0; c < ND; ++c)
@@ -815,8 +816,8 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
     for (int i = 0; i < VL; ++i) {
       const int r = vrow + RPI * i, row = 32 * qt + r;
       if (row < Nq)
-        *reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch) =
-            *reinterpret_cast<const u32x4*>(vt + r * D + 8 * (vch ^ bswz<D>(r)));
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(vt + r * D + 8 * (vch ^ bswz<D>(r))),
+                                    reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch));
     }
   }
   if (P.stats) {
