@@ -32,7 +32,7 @@ REF_FWD_UNITS, REF_FWDBWD_UNITS = 4.0, 14.0  # the reference's two independent T
 # --pmc FETCH_SIZE and --pmc WRITE_SIZE runs of this script, each scaled by what the same counter
 # reads for --copy-probe (a 2^30-byte device copy): FETCH_SIZE x 2.000, WRITE_SIZE x 1.000.
 # Recorded with the command lines in profiles/tda_c2_bf16_counters.md; re-measure after kernel changes.
-FWD_HBM_BYTES = 1.017e9
+FWD_HBM_BYTES = 1.020e9
 
 
 def units(shape, u):
