@@ -13,12 +13,14 @@
 //   * bwd_dkv_pairs: one wave per key tile whose bitmask column has only lists that fit; whole-
 //     row vector work per key row its pairs name, with the dk weight of each pair stored by
 //     bwd_dq_pairs (no V, no matrix cores), the tile's other gradient rows stored as zeros.
+// Gradient rows are streaming (non-temporal) stores: nothing reads them back soon.
 // The tile passes take the rest (lists past the cap, or no lists at all), driven by the bitmask:
-//   * bwd_dq_fast: one wave per (branch, query tile); walks the set bits of the bitmask row, so
-//     only key tiles with a non-zero score are touched; dq_br is finished (F.normalize backward)
-//     at the end.
-//   * bwd_dkv_fast: one wave per key tile; walks the set bits of the bitmask column of each
-//     branch; dv accumulates over both branches (A1 - lam A2), dk_br is finished per branch.
+//   * bwd_dq_fast: per (branch, query tile), several to a wave when lists exist (their counts
+//     tested in one round); walks the set bits of the bitmask row, so only key tiles with a
+//     non-zero score are touched; dq_br is finished (F.normalize backward) at the end.
+//   * bwd_dkv_fast: per key tile, from the queue bwd_dkv_pairs fills when lists exist; walks
+//     the set bits of the bitmask column of each branch; dv accumulates over both branches
+//     (A1 - lam A2), dk_br is finished per branch.
 // The tile passes fetch each visited tile with direct global->LDS loads into a wave-private,
 // chunk-swizzled row-major tile that serves both as row fragments (ds_read_b128) and, through
 // the LDS transpose read, as transposed fragments.  dbeta / dlambda partials: one pair per

@@ -6,7 +6,7 @@
 // (TTA:19-115: scores, threshold, ReLU^p, causal mask, A.V) and the differential composition
 // out = A1 V - clamp(lambda, 0, 1) A2 V (TTA:489-519).
 //
-// Three launches, in stream order:
+// Launches, in stream order:
 //   key_norms   inverse L2 norms rk_j of the key rows, into the norms table (normalize only).
 //   fwd_screen  for every causal (query tile, key tile) pair of a branch, a score tile on the
 //               matrix cores and a test that keeps every tile holding a non-zero weight
@@ -15,12 +15,18 @@
 //               and the test carries a proven margin (kScreenMargin), so it may keep a few
 //               tiles whose weights are all zero.  No V and no output accumulators: the kernel
 //               holds only Q fragments and two score tiles per wave, so MFMA results stay in
-//               ordinary VGPRs and several waves share a SIMD.
-//   fwd_pv      one wave per query tile walks the set bits of both branches: recomputes the
-//               score tile with the same instruction sequence (so the same values), forms the
-//               exact weights ReLU(x)^p with the causal mask, and accumulates out += coef A V.
-//               Tiles whose exact weights are all zero lose their bit, so the bitmask ends
-//               exact.
+//               ordinary VGPRs and several waves share a SIMD.  With normalisation it also
+//               lists each query tile's candidate keys (the keys of its passing lanes).
+//   fwd_pv_cand (normalize) one wave per query tile whose candidate lists fit: the score tile
+//               of its rows against the candidate keys (the same MFMA sequence and operand
+//               values as fwd_pv, so the same scores), the exact weights and out += coef A V
+//               over the candidates' V rows; the bitmask row is rewritten exactly.  Query
+//               tiles whose lists overflow go to a queue for fwd_pv.
+//   fwd_pv      the tile pass, one wave per query tile (every tile without normalisation, the
+//               queued ones with it): walks the set bits of both branches, recomputes the
+//               score tile, forms the exact weights ReLU(x)^p with the causal mask, and
+//               accumulates out += coef A V.  Tiles whose exact weights are all zero lose their
+//               bit, so the bitmask ends exact.
 // The screen tests every key of the tile, including keys after the query on the diagonal tile
 // and padding keys past N: it may keep a tile the mask empties, never drop a non-zero one.
 #include "tda_common.hpp"
