@@ -649,13 +649,15 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
   int bh, qt;
   {
     const int bid = blockIdx.x;
-    if (BH % 8 == 0) {  // one head's query tiles consecutive on one XCD, longest first
+    // one head's query tiles consecutive on one XCD, early tiles (lowest thresholds, the most
+    // candidates) first
+    if (BH % 8 == 0) {
       const int x = bid & 7, j = bid >> 3;
       bh = x + 8 * (j / nqt);
-      qt = nqt - 1 - j % nqt;
+      qt = j % nqt;
     } else {
       bh = bid / nqt;
-      qt = nqt - 1 - bid % nqt;
+      qt = bid % nqt;
     }
   }
   if (bh >= BH) return;
