@@ -12,8 +12,9 @@
 //               matrix cores and a test that keeps every tile holding a non-zero weight
 //               (x_ij = fma(s_ij rk_j, rq_i, -tau_i) > 0 for some pair).  Without normalisation
 //               the test is exact; with it, the queries enter pre-scaled by their inverse norms
-//               and the test carries a proven margin (kScreenMargin), so it may keep a few
-//               tiles whose weights are all zero.  No V and no output accumulators: the kernel
+//               and the test carries a margin bounded per query tile from the bf16 rounding
+//               residuals of its rows (screen_tlo), so it may keep a few tiles whose weights
+//               are all zero.  No V and no output accumulators: the kernel
 //               holds only Q fragments and two score tiles per wave, so MFMA results stay in
 //               ordinary VGPRs and several waves share a SIMD.  With normalisation it also
 //               lists each query tile's candidate keys (the keys of its passing lanes).
@@ -28,7 +29,9 @@
 //               accumulates out += coef A V.  Tiles whose exact weights are all zero lose their
 //               bit, so the bitmask ends exact.
 // The screen tests every key of the tile, including keys after the query on the diagonal tile
-// and padding keys past N: it may keep a tile the mask empties, never drop a non-zero one.
+// (and, without normalisation, padding keys past Nk): it may keep a tile the mask empties, never
+// drop a non-zero one.  With normalisation padding keys are cleared from the hit bits, so no
+// candidate list names a key row past Nk.
 #include "tda_common.hpp"
 #include "tda_params.hpp"
 #include "tda_pos.hpp"
@@ -73,18 +76,28 @@ __device__ __forceinline__ float maximum16(const f32x16& v) {
   return m3(m3(a, b, c), m3(d, e, v[15]), v[15]);
 }
 
-// Margin of the normalised screen, in cosine units.  The screen's scores sh_ij = qh_i . k_j,
-// qh_i = bf16(q_i rq_i), differ from rq_i s_ij by at most (2^-9 + 2^-22) |k_j|: each element of
-// qh_i carries a relative rounding error of at most 2^-9 (bf16) + 2^-23 (the fp32 product),
-// summed against k_j by Cauchy-Schwarz with rq_i |q_i| <= 1 + 2^-16.  The fp32 accumulations of
-// the screen's and the exact path's MFMAs add at most 2^-17 |q||k| each (128 terms, unit
-// roundoff 2^-24), the fp32 products of the tests a few units of 2^-24.  Times rk_j
-// (rk_j |k_j| <= 1 + 2^-16) the total stays below 2^-9 + 2^-14; the margin doubles the part past
-// 2^-9.  tau_i, evaluated in fp32 with a few ulps of error, is monotone in i up to a relative
-// 2^-20; screen_tlo takes twice that off the smallest end value of the tile.
-constexpr float kScreenMargin = 0x1p-9f + 0x1p-13f;
-__device__ __forceinline__ float screen_tlo(float tmin) {
-  return tmin - fabsf(tmin) * 0x1p-19f - kScreenMargin;
+// Threshold of the normalised screen for one query tile, in cosine units.
+//
+// The exact pass keeps weight (i, j) iff x_ij = fma(fl(S_ij rk_j), rq_i, -tau_i) > 0, with S_ij
+// the fp32 MFMA sum of q_i . k_j; the screen tests fl(sh_ij rk_j) > tlo with sh_ij the fp32 MFMA
+// sum of qh_i . k_j and qh_i = bf16(fl(q_i rq_i)) (rq_i, rk_j: the same fp32 inverse norms on
+// both sides).  Write qh_i = rq_i q_i + r_i + f_i, r_i = qh_i - fl(q_i rq_i) the bf16 rounding
+// residual (exact in fp32) and |f_i| <= 2^-24 rq_i |q_i| the fp32 product's.  Then
+//   |sh_ij - rq_i S_ij| <= (|r_i| + 2^-24 + 2^-17 |qh_i| + 2^-17 rq_i |q_i|) |k_j|
+// (each 128-term fp32 accumulation errs by at most 128 * 2^-24 = 2^-17 of |a||b|, Cauchy-
+// Schwarz), and with rq_i |q_i|, rk_j |k_j| <= 1 + 2^-16 and |qh_i| <= 1.01 the difference
+// after the factor rk_j stays below |r_i| (1 + 2^-16) + 2^-15.  The two fp32 products of the
+// tests add a relative 2^-24 each on values of magnitude <= 1.02.  So with
+//   tlo = min_i tau_i - |min_i tau_i| 2^-19 - (max_i |r_i| (1 + 2^-14) + 2^-14)
+// every kept weight passes the screen: max_i |r_i| is computed per query tile where qh is
+// formed (fp32 sum of squares and square root: relative error below 2^-16, covered by the
+// 2^-14 factor), and 2^-14 covers the 2^-15 of the accumulations plus the products' 2^-22.
+// tau_i, evaluated in fp32 with a few ulps of error, is monotone in i up to a relative 2^-20;
+// the 2^-19 term covers that and the products' relative error on tau.  A bf16 residual is
+// at most 2^-8 of each element (unit roundoff of an 8-bit significand), so |r_i| <= 2^-8 |qh_i|;
+// on N(0,1) rows it is about 0.0016.
+__device__ __forceinline__ float screen_tlo(float tmin, float rmax) {
+  return tmin - fabsf(tmin) * 0x1p-19f - (rmax * (1.f + 0x1p-14f) + 0x1p-14f);
 }
 
 // XCD-aware order of the (stream, block) work items of a grid: consecutive workgroup ids go to
@@ -250,17 +263,26 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
       // are 0 (x > 0 fails on NaN), so a NaN score can only come from a non-finite key row:
       // it poisons the maximum of that key's lane alone, whose weights are 0 as well
       const float sc = valid[s] ? rq : 0.f;
+      float r2 = 0.f;  // squared norm of the row's bf16 rounding residual (this lane's half)
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float x = (float)Q[s][t][j] * sc;
-          Q[s][t][j] = (bf16)(__builtin_isfinite(x) ? x : 0.f);
+          const float x0 = (float)Q[s][t][j] * sc;
+          const float x = __builtin_isfinite(x0) ? x0 : 0.f;
+          const bf16 xb = (bf16)x;
+          const float r = (float)xb - x;  // exact: xb and x are within a factor of two
+          r2 = __builtin_fmaf(r, r, r2);
+          Q[s][t][j] = xb;
         }
+      r2 += __shfl_xor(r2, 32);
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) r2 = fmaxf(r2, __shfl_xor(r2, o));  // largest of the tile
       // tau is monotone in the position: its smallest value over the tile's rows is at one of
       // the ends
       const int i0 = q0w + 32 * s, i1 = max(i0, min(i0 + 31, Nq - 1));
-      tau[s] = screen_tlo(fminf(beta * tau_coeff(qoff + i0, P.inv_d), beta * tau_coeff(qoff + i1, P.inv_d)));
+      tau[s] = screen_tlo(fminf(beta * tau_coeff(qoff + i0, P.inv_d), beta * tau_coeff(qoff + i1, P.inv_d)),
+                          sqrtf(r2));
     } else {
       tau[s] = beta * tau_coeff(qoff + iq, P.inv_d);
     }
@@ -321,11 +343,17 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     }
   };
   // bitmask words of this wave's rows: word kt/32 is complete after key tile kt
+  const int kpad = P.nkt - 1;  // the key tile that may hold padding keys
   auto flush = [&](int kt) {
     if (live[0] && ((kt & 31) == 31 || kt == nkt - 1)) {
 #pragma unroll
       for (int s = 0; s < QPW; ++s) {
         uint32_t w = hb[s];
+        if constexpr (NORM) {
+          // a padding key (past Nk, in the last key tile) scores 0 and passes a threshold below 0
+          // (the query tile at position 0, beta <= 0): it holds no weight and must not be listed
+          if ((kt >> 5) == (kpad >> 5) && n32 >= Nk - 32 * kpad) w &= ~(1u << (kpad & 31));
+        }
         const uint32_t hm = w | (uint32_t)__shfl_xor((int)w, 32);  // lane n32: tiles its key passed
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) w |= (uint32_t)__shfl_xor((int)w, o);
@@ -707,7 +735,7 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
       const int64_t sq = P.s[qslot][2], sk = P.s[kslot][2], sv = P.s[F_V][2];
       const float coef = br == 0 ? 1.f : -lam;
       const int kb = __shfl(kraw, (32 * br + (l & 31)) & 63);  // this branch's slots: lanes 32 br ..
-      const int key_l = l < (int)n ? kb : -1;
+      const int key_l = l < (int)n && kb >= 0 && kb < Nk ? kb : -1;  // the screen lists keys < Nk only
       const float rk_l = key_l >= 0 ? P.norms[norm_base(P, br ? N_K2 : N_K1, bh) + key_l] : 0.f;
       const float rq = P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + min(iq, Nq - 1)];
       // Every load of the branch in one round.  The operands of the score MFMAs straight from
@@ -715,7 +743,7 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
       // row): no LDS staging.  V rows by direct global->LDS loads into the swizzled tile (rows
       // past the count take candidate 0's row, zeroed below).
       const int key_m = __shfl(key_l, n32);
-      const int key0 = __builtin_amdgcn_readfirstlane(key_l);
+      const int key0 = max(__builtin_amdgcn_readfirstlane(key_l), 0);  // a row every lane may load
       const bf16* qrow = qhead + (int64_t)min(iq, Nq - 1) * sq;
       const bf16* krow = khead + (int64_t)(key_m >= 0 ? key_m : key0) * sk;
       bf16x8 Q[NT], K[NT];

@@ -30,7 +30,7 @@ constexpr uint32_t kPairOverflow = 0xffffffffu;  // count of a list the forward 
 
 // Candidate keys (bf16 with normalisation, forward workspace): for each (branch, head, query
 // tile) the keys j whose screen lane passed (max over its query rows of the screen score above
-// the tile's threshold minus the screen's proven margin), a superset of the keys with a non-zero
+// the tile's threshold minus the screen's rounding margin), a superset of the keys with a non-zero
 // weight in the query tile; the exact pass gathers only these rows.  Layout: the keys,
 // kCandCap u32 per list, in the order the screen met them (increasing); then the counts, u32 per
 // list.  A count above kCandCap marks a list that did not fit: the exact pass then walks the

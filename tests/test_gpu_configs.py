@@ -1,10 +1,10 @@
 """GPU parity at the benchmark configurations (BASELINE configs[1..4]) at full size.
 
-The CPU oracle cannot evaluate every head in seconds at these sizes, so each test checks a
-sample of (b, h) heads against the oracle and covers the rest with size-independent
-properties: bitwise run-to-run determinism, head equivariance (a head computed inside the
-full call equals the same head computed alone) and additivity of d beta / d lambda over
-heads.  Tolerance: bf16 2e-2 normwise against the fp32 formula on the same bf16 values."""
+Every (b, h) head of every config is compared with the CPU oracle (outputs, and at configs[3]
+every gradient and the totals d beta / d lambda), so each branch of the kernels' XCD-aware
+block orders is exercised; size-independent properties add bitwise run-to-run determinism and
+head equivariance (a head computed inside the full call equals the same head computed alone).
+Tolerance: bf16 2e-2 normwise per head against the fp32 formula on the same bf16 values."""
 import pytest
 import torch
 
@@ -25,14 +25,26 @@ def _tra(*a, **kw):
     return threshold_rela_triton(*a, **kw)
 
 
+def _every_head(out, ref, tol=2e-2):
+    """Normwise error of every (b, h) head; a head whose reference output is zero must be zero."""
+    B, H = ref.shape[:2]
+    assert ref.abs().max() > 0
+    for b in range(B):
+        for h in range(H):
+            r, o = ref[b, h], out[b, h]
+            if r.abs().max() == 0:
+                assert o.abs().max() == 0, (b, h)
+            else:
+                e = rel_err(o, r)
+                assert e <= tol, (b, h, e)
+
+
 def test_c1_tra_bf16():
     """TRA fwd (4,16,2048,64) bf16 seed 1, beta=1, p=2, normalize, causal."""
     q, k, v = make_inputs((4, 16, 2048, 64), 1, 3, BF)
     out = _tra(q, k, v, torch.tensor(1.0), relu_power=2.0, normalize=True)
-    heads = [(0, 0), (3, 15), (2, 7)]
-    ref = oracle_out(q, None, k, None, v, 1.0, 0.0, 2.0, True, 1, heads=heads, dtype=torch.float32)
-    assert heads_of(ref, heads).abs().max() > 0
-    assert rel_err(heads_of(out, heads), heads_of(ref, heads)) <= 2e-2
+    ref = oracle_out(q, None, k, None, v, 1.0, 0.0, 2.0, True, 1, dtype=torch.float32)
+    _every_head(out, ref)
     assert torch.isfinite(out.float()).all()
 
 
@@ -41,10 +53,8 @@ def test_c2_tda_forward():
     xs = make_inputs((4, 16, 4096, 128), 2, 5, BF)
     kw = dict(relu_power=2.0, normalize=True)
     out = _tda(*xs, torch.tensor(1.0), torch.tensor(0.5), **kw)
-    heads = [(0, 0), (3, 15)]
-    ref = oracle_out(*xs, 1.0, 0.5, 2.0, True, 2, heads=heads, dtype=torch.float32)
-    assert heads_of(ref, heads).abs().max() > 0
-    assert rel_err(heads_of(out, heads), heads_of(ref, heads)) <= 2e-2
+    ref = oracle_out(*xs, 1.0, 0.5, 2.0, True, 2, dtype=torch.float32)
+    _every_head(out, ref)
     # determinism and head equivariance
     again = _tda(*xs, torch.tensor(1.0), torch.tensor(0.5), **kw)
     assert torch.equal(out, again)
@@ -68,35 +78,36 @@ def test_c3_tda_forward_backward():
     names = ["dq1", "dq2", "dk1", "dk2", "dv"]
     for g in grads:
         assert torch.isfinite(g.float()).all()
-    sample = [(1, 4), (3, 11)]
-    for (b, h) in sample:
-        ref = tda_grads(*(host(x[b:b + 1, h:h + 1], torch.float32) for x in xs),
-                        host(do[b:b + 1, h:h + 1], torch.float32), 1.0, 0.5, 2.0, True, 2, dtype=torch.float32)
-        for g, name in zip(grads, names):
-            e = rel_err(g[b:b + 1, h:h + 1], ref[name])
-            assert e <= 2e-2, (b, h, name, e)
-        # per-head dbeta / dlambda from a GPU call on that head alone
-        sub = [x[b:b + 1, h:h + 1].clone().requires_grad_(True) for x in xs]
-        bs = torch.tensor(1.0, device="cuda", requires_grad=True)
-        ls = torch.tensor(0.5, device="cuda", requires_grad=True)
-        _tda(*sub, bs, ls, relu_power=2.0, normalize=True).backward(do[b:b + 1, h:h + 1])
-        for got, want in ((bs.grad, ref["dbeta"]), (ls.grad, ref["dlambda"])):
-            assert abs(got.item() - want.item()) <= 2e-2 * abs(want.item()), (got.item(), want.item())
-        for s, g in zip(sub, grads):  # head equivariance of the gradients
-            assert torch.equal(s.grad[0, 0], g[b, h])
-    # additivity over heads: full-call dbeta / dlambda == sum of per-batch calls
-    tot_b, tot_l, mag_b, mag_l = 0.0, 0.0, 0.0, 0.0
+    # every head's gradients against fp32 autograd of the formula on that head; the totals
+    # d beta and d lambda against the sum of the heads' reference values
+    want_b, want_l, mag_b, mag_l = 0.0, 0.0, 0.0, 0.0
+    grads_h = [g.cpu() for g in grads]
     for b in range(shape[0]):
-        sub = [x[b:b + 1].clone().requires_grad_(True) for x in xs]
-        bs = torch.tensor(1.0, device="cuda", requires_grad=True)
-        ls = torch.tensor(0.5, device="cuda", requires_grad=True)
-        _tda(*sub, bs, ls, relu_power=2.0, normalize=True).backward(do[b:b + 1])
-        tot_b += bs.grad.item()
-        tot_l += ls.grad.item()
-        mag_b += abs(bs.grad.item())
-        mag_l += abs(ls.grad.item())
-    assert abs(bt.grad.item() - tot_b) <= 1e-4 * max(mag_b, 1e-30)
-    assert abs(lt.grad.item() - tot_l) <= 1e-4 * max(mag_l, 1e-30)
+        for h in range(shape[1]):
+            ref = tda_grads(*(host(x[b:b + 1, h:h + 1], torch.float32) for x in xs),
+                            host(do[b:b + 1, h:h + 1], torch.float32), 1.0, 0.5, 2.0, True, 2,
+                            dtype=torch.float32)
+            for g, name in zip(grads_h, names):
+                r = ref[name]
+                if r.abs().max() == 0:
+                    assert g[b, h].abs().max() == 0, (b, h, name)
+                else:
+                    e = rel_err(g[b:b + 1, h:h + 1], r)
+                    assert e <= 2e-2, (b, h, name, e)
+            want_b += ref["dbeta"].item()
+            want_l += ref["dlambda"].item()
+            mag_b += abs(ref["dbeta"].item())
+            mag_l += abs(ref["dlambda"].item())
+    assert abs(bt.grad.item() - want_b) <= 2e-2 * abs(want_b), (bt.grad.item(), want_b, mag_b)
+    assert abs(lt.grad.item() - want_l) <= 2e-2 * abs(want_l), (lt.grad.item(), want_l, mag_l)
+    # head equivariance of the gradients: one head computed alone
+    b, h = 1, 4
+    sub = [x[b:b + 1, h:h + 1].clone().requires_grad_(True) for x in xs]
+    bs = torch.tensor(1.0, device="cuda", requires_grad=True)
+    ls = torch.tensor(0.5, device="cuda", requires_grad=True)
+    _tda(*sub, bs, ls, relu_power=2.0, normalize=True).backward(do[b:b + 1, h:h + 1])
+    for s, g in zip(sub, grads):
+        assert torch.equal(s.grad[0, 0], g[b, h])
 
 
 @pytest.mark.parametrize("p", [1.0, 1.5])
@@ -109,14 +120,8 @@ def test_c4_long_context(p):
     lam = torch.full((), 0.3, device="cuda")
     stats = torch.zeros(3, dtype=torch.int64, device="cuda")
     out = ops.forward(q1, k1, q2, k2, v, beta, lam, p, True, 2, stats=stats)
-    heads = [(0, 17)]
-    ref = oracle_out(*xs, 2.0, 0.3, p, True, 2, heads=heads, dtype=torch.float32)
-    r = heads_of(ref, heads)
-    o = heads_of(out, heads)
-    if r.abs().max() == 0:
-        assert o.abs().max() == 0
-    else:
-        assert rel_err(o, r) <= 2e-2
+    ref = oracle_out(*xs, 2.0, 0.3, p, True, 2, dtype=torch.float32)
+    _every_head(out, ref)
     visited, computed, checked = (int(x) for x in stats.tolist())
     assert computed <= checked
     nt = 16384 // 32
@@ -159,11 +164,18 @@ def test_occupancy_and_norms_match_oracle(shape, heads):
         for br, (q, k) in enumerate(((q1, k1), (q2, k2))):
             qf = torch.nn.functional.normalize(q[b, h].float().cpu(), dim=-1)
             kf = torch.nn.functional.normalize(k[b, h].float().cpu(), dim=-1)
+            x = qf @ kf.T - t
             nz = torch.zeros(32 * nqt, 32 * nqt, dtype=torch.bool)
-            nz[:N, :N] = ((qf @ kf.T - t) > 0) & causal
+            nz[:N, :N] = (x > 0) & causal
             tiles = nz.view(nqt, 32, nqt, 32).any(3).any(1)
-            mism += (tiles != bits[br, bh, :, :nqt].bool()).sum().item()
+            got = bits[br, bh, :, :nqt].bool()
+            mism += (tiles != got).sum().item()
             assert 0.01 < tiles.float().sum().item() / (nqt * (nqt + 1) / 2) < 0.5
+            # one-sided: every tile holding a weight clear of fp32 rounding (x > 4e-6 in cosine
+            # units; the two evaluations differ by ~1e-7) is set
+            nz[:N, :N] = (x > 4e-6) & causal
+            strong = nz.view(nqt, 32, nqt, 32).any(3).any(1)
+            assert not (strong & ~got).any(), (bh, br, int((strong & ~got).sum()))
     assert mism <= 4, mism  # only threshold ties within rounding may differ
     # the screen keeps a superset of the non-zero tiles (its margin covers the bf16 rounding of
     # the pre-scaled queries); the exact pass clears the rest, and the margin costs little

@@ -1,0 +1,232 @@
+"""GPU parity at edge cases of the reference's formula (TTA:59-109, :505-517), through the
+public entry points, against the CPU oracle on the same values:
+
+* an adversarial query/key pair for the normalised bf16 screen: a weight the reference keeps
+  (cosine 1e-4 above tau) whose screen score falls below a constant margin of 2^-9 + 2^-13
+  (tests/screen_emulation.py builds it); at p < 1 a dropped weight is a large error;
+* key rows shorter than the query rows with lists that fit (padding keys past Nk in the last
+  key tile), and beta <= 0 with a ragged key count;
+* powers below 1 (p = 0.5 and p = 0: x^0 = 1 for x > 0, zero gradient through the scores);
+* bfloat16 (B, N, H, d) views, forward and backward, at the operator's 2e-2;
+* rows whose norm is below the normalisation eps 1e-12 (the backward then divides by eps).
+Tolerances: float32 1e-4, bfloat16 2e-2, normwise (max|y - y_ref| / max|y_ref|)."""
+import pytest
+import torch
+
+from tests.helpers import TOL, host, make_inputs, oracle_out, rel_err, tda_grads
+from tests.screen_emulation import MARGIN_FIXED_OLD, adversarial_key, adversarial_row, prescale, tlo
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def _tra(*a, **kw):
+    from tda_amd import threshold_rela_triton
+    return threshold_rela_triton(*a, **kw)
+
+
+def _tda(*a, **kw):
+    from tda_amd import differential_threshold_rela_triton
+    return differential_threshold_rela_triton(*a, **kw)
+
+
+def _adversarial_head(seed=0, d=128, n=64):
+    """q, k (n, d) float32 holding bf16 values: query rows 32..63 are copies of a row with a
+    large bf16 rounding residual once pre-scaled, key 5 has cosine tau + [8e-5, 1.3e-4] with
+    it (tau = 0 at beta = 0) and the screen score the search makes lowest, every other key of
+    key tiles 0 and 1 points against that row (cosine -1); query rows 0..31 are N(0, 1)."""
+    qa = adversarial_row(d, seed, steps=8000)
+    k5, cos, sv = adversarial_key(qa, 0.0, lo=8e-5, hi=1.3e-4, seed=seed)
+    _, _, r = prescale(qa)
+    assert sv <= tlo(0.0, MARGIN_FIXED_OLD)  # a constant 2^-9 + 2^-13 margin would drop it
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(n, d, generator=g).to(BF).float()
+    q[32:] = torch.from_numpy(qa)
+    k = -torch.from_numpy(qa).repeat(n, 1)
+    k[5] = torch.from_numpy(k5)
+    return q, k, cos
+
+
+@pytest.mark.parametrize("p", [0.25, 0.5])
+def test_screen_keeps_adversarial_weight_tra(p):
+    q, k, cos = _adversarial_head()
+    v = torch.randn(64, 128, generator=torch.Generator().manual_seed(3)).to(BF)
+    q, k, v = (x.to(BF).reshape(1, 1, 64, 128).cuda() for x in (q, k, v))
+    out = _tra(q, k, v, 0.0, relu_power=p, normalize=True)
+    ref = oracle_out(q, None, k, None, v, 0.0, 0.0, p, True, 1)
+    tail = ref[..., 32:, :]
+    assert tail.abs().max() > 0.5 * (cos ** p) * v[0, 0, 5].float().abs().max().item()
+    assert rel_err(out[..., 32:, :], tail) <= 2e-2
+    assert rel_err(out, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("p", [0.25, 0.5])
+def test_screen_keeps_adversarial_weight_tda_with_gradients(p):
+    """Branch 2 carries the adversarial pair, branch 1 has no weight in query tile 1; the
+    gradients of every input against fp64 autograd of the formula."""
+    q2, k2, _ = _adversarial_head(seed=1)
+    q1, k1, _ = _adversarial_head(seed=1)
+    k1[5] = -k1[5]  # cosine -(tau + 1e-4): no weight
+    g = torch.Generator().manual_seed(4)
+    v = torch.randn(64, 128, generator=g)
+    do = torch.randn(64, 128, generator=g)
+    xs = [x.to(BF).reshape(1, 1, 64, 128).cuda() for x in (q1, q2, k1, k2, v)]
+    do = do.to(BF).reshape(1, 1, 64, 128).cuda()
+    leaves = [x.clone().requires_grad_(True) for x in xs]
+    bt = torch.tensor(0.0, device="cuda", requires_grad=True)
+    lt = torch.tensor(0.5, device="cuda", requires_grad=True)
+    out = _tda(*leaves, bt, lt, relu_power=p, normalize=True)
+    out.backward(do)
+    ref = tda_grads(*(host(x) for x in xs), host(do), 0.0, 0.5, p, True, 2)
+    assert ref["out"][..., 32:, :].abs().max() > 0
+    assert rel_err(out[..., 32:, :], ref["out"][..., 32:, :]) <= 2e-2
+    assert rel_err(out, ref["out"]) <= 2e-2
+    for leaf, name in zip(leaves, ["dq1", "dq2", "dk1", "dk2", "dv"]):
+        assert rel_err(leaf.grad, ref[name]) <= 2e-2, (name, rel_err(leaf.grad, ref[name]))
+    for got, name in ((bt.grad, "dbeta"), (lt.grad, "dlambda")):
+        want = ref[name].item()
+        assert abs(got.item() - want) <= 2e-2 * abs(want), (name, got.item(), want)
+
+
+@pytest.mark.parametrize("branches", [1, 2])
+@pytest.mark.parametrize("nq,nk,beta", [(64, 20, 1.0), (64, 20, 0.0), (20, 20, 0.0), (20, 20, -0.5),
+                                        (50, 50, -0.5), (70, 45, 0.5)])
+def test_short_key_rows_and_nonpositive_beta(branches, nq, nk, beta):
+    """Padding keys past Nk in the last key tile score 0 and pass a threshold <= 0 (position 0,
+    beta <= 0): they must never enter a candidate list (their rows lie past the tensor)."""
+    g = 300 + nq + nk
+    qs = make_inputs((1, 3, nq, 128), g, 2, BF)
+    ks = make_inputs((1, 3, nk, 128), g + 1, 3, BF)
+    if branches == 2:
+        out = _tda(qs[0], qs[1], ks[0], ks[1], ks[2], beta, 0.5, relu_power=2.0, normalize=True, q_offset=0)
+        ref = oracle_out(qs[0], qs[1], ks[0], ks[1], ks[2], beta, 0.5, 2.0, True, 2)
+    else:
+        out = _tra(qs[0], ks[0], ks[2], beta, relu_power=2.0, normalize=True, q_offset=0)
+        ref = oracle_out(qs[0], None, ks[0], None, ks[2], beta, 0.0, 2.0, True, 1)
+    assert torch.isfinite(out.float()).all()
+    assert ref.abs().max() > 0
+    assert rel_err(out, ref) <= 2e-2
+
+
+def test_short_key_rows_gradients():
+    q1, q2 = make_inputs((1, 2, 64, 128), 401, 2, BF)
+    k1, k2, v = make_inputs((1, 2, 20, 128), 402, 3, BF)
+    (do,) = make_inputs((1, 2, 64, 128), 403, 1, BF)
+    xs = [q1, q2, k1, k2, v]
+    leaves = [x.clone().requires_grad_(True) for x in xs]
+    bt = torch.tensor(0.3, device="cuda", requires_grad=True)
+    lt = torch.tensor(0.5, device="cuda", requires_grad=True)
+    out = _tda(*leaves, bt, lt, relu_power=2.0, normalize=True, q_offset=0)
+    out.backward(do)
+    ref = tda_grads(*(host(x) for x in xs), host(do), 0.3, 0.5, 2.0, True, 2)
+    assert rel_err(out, ref["out"]) <= 2e-2
+    for leaf, name in zip(leaves, ["dq1", "dq2", "dk1", "dk2", "dv"]):
+        assert rel_err(leaf.grad, ref[name]) <= 2e-2, name
+
+
+@pytest.mark.parametrize("dt", [torch.float32, BF])
+@pytest.mark.parametrize("p", [0.5, 0.0])
+@pytest.mark.parametrize("normalize", [True, False])
+def test_powers_below_one_forward_and_gradients(dt, p, normalize):
+    shape = (1, 3, 130, 64)
+    xs = make_inputs(shape, 51, 5, dt)
+    (do,) = make_inputs(shape, 52, 1, dt)
+    beta = 0.2 if normalize else 3.0
+    leaves = [x.clone().requires_grad_(True) for x in xs]
+    bt = torch.tensor(beta, device="cuda", requires_grad=True)
+    lt = torch.tensor(0.4, device="cuda", requires_grad=True)
+    out = _tda(*leaves, bt, lt, relu_power=p, normalize=normalize)
+    out.backward(do)
+    ref = tda_grads(*(host(x) for x in xs), host(do), beta, 0.4, p, normalize, 2)
+    # p x^(p-1) is unbounded near x = 0: the gradients are ill-conditioned there, and the
+    # formula evaluated in float32 (as the reference computes, TTA:355-360) already differs
+    # from float64 by up to ~1e-3 on these inputs.  The float32 bound on the gradients is
+    # therefore 8x that error of the float32 formula, or 1e-4 when larger.
+    r32 = tda_grads(*(host(x, torch.float32) for x in xs), host(do, torch.float32), beta, 0.4, p,
+                    normalize, 2, dtype=torch.float32)
+    tol = TOL[dt]
+
+    def gtol(name):
+        if ref[name].abs().max() == 0:
+            return tol
+        return max(tol, 8 * rel_err(r32[name], ref[name]))
+
+    assert ref["out"].abs().max() > 0
+    assert rel_err(out, ref["out"]) <= tol
+    for leaf, name in zip(leaves, ["dq1", "dq2", "dk1", "dk2", "dv"]):
+        if p == 0.0 and name != "dv":  # x^0 is flat: no gradient reaches the scores
+            assert ref[name].abs().max() == 0 and leaf.grad.abs().max() == 0, name
+        else:
+            assert rel_err(leaf.grad, ref[name]) <= gtol(name), (name, rel_err(leaf.grad, ref[name]))
+    want = ref["dbeta"].item()
+    if p == 0.0:
+        assert want == 0.0 and bt.grad.item() == 0.0
+    else:
+        assert abs(bt.grad.item() - want) <= gtol("dbeta") * abs(want)
+    want = ref["dlambda"].item()
+    assert abs(lt.grad.item() - want) <= tol * abs(want)
+
+
+@pytest.mark.parametrize("branches", [1, 2])
+def test_bf16_bnhd_views_forward_backward(branches):
+    """(B, N, H, d) storage of a fused projection viewed as (B, H, N, d), bf16, forward and
+    all gradients at 2e-2 (strided inputs, strided upstream gradient)."""
+    B, N, H, d = 2, 150, 3, 128
+    base = make_inputs((B, N, H, d), 61, 5, BF)
+    (dob,) = make_inputs((B, N, H, d), 62, 1, BF)
+    xs = [x.transpose(1, 2) for x in base]
+    do = dob.transpose(1, 2)
+    assert not xs[0].is_contiguous()
+    if branches == 1:
+        xs = [xs[0], xs[2], xs[4]]
+    leaves = [x.detach().requires_grad_(True) for x in xs]
+    bt = torch.tensor(0.1, device="cuda", requires_grad=True)
+    lt = torch.tensor(0.6, device="cuda", requires_grad=True)
+    if branches == 2:
+        out = _tda(*leaves, bt, lt, relu_power=2.0, normalize=True)
+        ref = tda_grads(*(host(x) for x in xs), host(do), 0.1, 0.6, 2.0, True, 2)
+        names = ["dq1", "dq2", "dk1", "dk2", "dv"]
+    else:
+        out = _tra(*leaves, bt, relu_power=2.0, normalize=True)
+        ref = tda_grads(host(xs[0]), None, host(xs[1]), None, host(xs[2]), host(do), 0.1, 0.0, 2.0, True, 1)
+        names = ["dq1", "dk1", "dv"]
+    out.backward(do)
+    assert rel_err(out, ref["out"]) <= 2e-2
+    for leaf, name in zip(leaves, names):
+        assert rel_err(leaf.grad, ref[name]) <= 2e-2, (name, rel_err(leaf.grad, ref[name]))
+    want = ref["dbeta"].item()
+    assert abs(bt.grad.item() - want) <= 2e-2 * abs(want)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, BF])
+def test_rows_below_normalisation_eps(dt):
+    """Query row 10 and key row 7 of each branch have norm ~1.1e-13 < 1e-12: F.normalize
+    divides by eps there (the normalised row has norm ~0.11), and its backward is dx = g / eps.
+    Key 3 points along query row 10 so that the tiny row holds weights."""
+    shape = (1, 2, 64, 128)
+    xs = make_inputs(shape, 71, 5, dt)
+    (do,) = make_inputs(shape, 72, 1, dt)
+    q1, q2, k1, k2, v = xs
+    for q, k in ((q1, k1), (q2, k2)):
+        k[:, :, 3] = q[:, :, 10]
+        q[:, :, 10] = (torch.sign(q[:, :, 10]) * 1e-14).to(dt)
+        k[:, :, 7] = (torch.sign(k[:, :, 7]) * 1e-14).to(dt)
+    leaves = [x.clone().requires_grad_(True) for x in xs]
+    bt = torch.tensor(0.05, device="cuda", requires_grad=True)
+    lt = torch.tensor(0.5, device="cuda", requires_grad=True)
+    out = _tda(*leaves, bt, lt, relu_power=2.0, normalize=True)
+    out.backward(do)
+    ref = tda_grads(*(host(x) for x in xs), host(do), 0.05, 0.5, 2.0, True, 2)
+    tol = TOL[dt]
+    assert rel_err(out, ref["out"]) <= tol
+    assert ref["out"][..., 10, :].abs().max() > 0  # the tiny row holds weights
+    tiny = {"dq1": 10, "dq2": 10, "dk1": 7, "dk2": 7}
+    for leaf, name in zip(leaves, ["dq1", "dq2", "dk1", "dk2", "dv"]):
+        g, want = leaf.grad, ref[name]
+        if name in tiny:  # the tiny row's gradient is ~1e12 larger: check it and the rest apart
+            r = tiny[name]
+            rest = [i for i in range(64) if i != r]
+            assert rel_err(g[..., r, :], want[..., r, :]) <= tol, (name, "tiny row")
+            assert rel_err(g[..., rest, :], want[..., rest, :]) <= tol, (name, "other rows")
+        else:
+            assert rel_err(g, want) <= tol, name

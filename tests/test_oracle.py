@@ -160,6 +160,24 @@ def test_chunked_equals_full():
     torch.testing.assert_close(ch1, full1, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("p", [2.0, 1.5, 0.5])
+def test_chunked_sparse_evaluation_equals_full(p):
+    """At a high threshold fewer than 1 in 20 weights are non-zero and the chunked evaluation
+    sums only those: it must equal the dense formula."""
+    x = [_rand((1, 2, 64, 8), s, torch.float64) for s in range(70, 75)]
+    beta = 6.0
+    s = x[0] @ x[2].transpose(-1, -2) - tau(64, 8, beta)[:, None]
+    nz = ((s > 0) & torch.ones(64, 64, dtype=torch.bool).tril()).sum().item()
+    assert 0 < nz * 20 < 2 * 64 * 64  # the sparse branch runs, with weights to sum
+    full = tda(*x, beta, torch.tensor(0.4, dtype=torch.float64), p, False)
+    assert full.abs().max() > 0
+    ch = tda_chunked(*x, beta, 0.4, p, False, block=16, dtype=torch.float64)
+    torch.testing.assert_close(ch, full, rtol=1e-12, atol=1e-12)
+    q_off = tda_chunked(x[0][:, :, 40:], None, x[2], None, x[4], beta, 0.0, p, False, branches=1,
+                        block=5, dtype=torch.float64, q_offset=40)
+    torch.testing.assert_close(q_off, tra(x[0], x[2], x[4], beta, p, False)[:, :, 40:], rtol=1e-12, atol=1e-12)
+
+
 # ---------------------------------------------------------------- gradients
 @pytest.mark.parametrize("p", [2.0, 1.5, 3.0])
 def test_gradcheck_tda(p):

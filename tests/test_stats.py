@@ -28,13 +28,14 @@ def test_argument_checks():
         tile_sparsity(x, x, x, 1.0, q2=x)
 
 
-def _tile_map(q, k, n, d, beta, normalize):
+def _tile_map(q, k, n, d, beta, normalize, floor=0.0):
+    """Tiles holding a weight with x > floor (floor > 0: weights clear of rounding ties)."""
     qf, kf = q.double().cpu(), k.double().cpu()
     if normalize:
         qf = torch.nn.functional.normalize(qf, dim=-1)
         kf = torch.nn.functional.normalize(kf, dim=-1)
     s = qf @ kf.transpose(-1, -2) - tau(n, d, beta)[:, None]
-    nz = (s > 0) & torch.ones(n, n, dtype=torch.bool).tril()
+    nz = (s > floor) & torch.ones(n, n, dtype=torch.bool).tril()
     t = (n + 31) // 32
     pad = torch.zeros(*nz.shape[:-2], 32 * t, 32 * t, dtype=torch.bool)
     pad[..., :n, :n] = nz
@@ -58,6 +59,9 @@ def test_tile_sparsity_tda(dtype):
     want = torch.stack([_tile_map(q1, k1, 700, 128, 1.0, True), _tile_map(q2, k2, 700, 128, 1.0, True)])
     mism = (st.occupancy.cpu() != want).sum().item()
     assert mism <= 4, mism  # threshold ties within rounding only
+    # one-sided: every tile with a weight clear of rounding ties is in the map
+    strong = torch.stack([_tile_map(q1, k1, 700, 128, 1.0, True, 4e-6), _tile_map(q2, k2, 700, 128, 1.0, True, 4e-6)])
+    assert not (strong & ~st.occupancy.cpu()).any()
     assert 0.0 < st.skipped_fraction < 1.0
     assert st.density.shape == (2,)
     if dtype == torch.bfloat16:
@@ -74,4 +78,6 @@ def test_tile_sparsity_tra_unnormalized():
     assert torch.equal(out, threshold_rela_triton(q, k, v, 25.0, 1.0))
     want = _tile_map(q, k, 300, 64, 25.0, False).unsqueeze(0)
     assert (st.occupancy.cpu() != want).sum().item() <= 4
+    strong = _tile_map(q, k, 300, 64, 25.0, False, 1e-4).unsqueeze(0)
+    assert not (strong & ~st.occupancy.cpu()).any()
     assert st.tiles_nonzero == int(st.occupancy.sum())
