@@ -33,7 +33,8 @@
  *   - Every pointer in the argument structs is a device pointer, except the
  *     struct itself.  The caller allocates everything (outputs and the
  *     workspace of each pass); the library never allocates or frees device
- *     memory and keeps no per-call state.
+ *     memory and keeps no per-call state.  The one exception is tda_fwd_noalloc,
+ *     whose workspace is a fixed device array of the library (see there).
  *   - Strides are in elements, for the (B, H, N, d) axes.  stride[3] must be 1;
  *     the other strides and every base pointer must keep 16-byte alignment;
  *     the sequence stride is at most 2^25 elements.
@@ -77,7 +78,12 @@ extern "C" {
 #define TDA_ERR_NORMS        -11   /* normalize set but the norms buffer is missing */
 #define TDA_ERR_OFFSET       -12   /* q_offset negative, or seq_len_kv / q_offset + seq_len
                                       beyond 2^30 - 64 */
+#define TDA_ERR_SCRATCH      -13   /* tda_fwd_noalloc: the call needs more workspace than
+                                      TDA_NOALLOC_SCRATCH_BYTES */
 #define TDA_ERR_HIP         -100   /* a HIP launch failed; see tda_last_hip_error() */
+
+/* Size of the device array that tda_fwd_noalloc uses as its workspace (per GPU). */
+#define TDA_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
 
 /* One (B, H, N, d) tensor: data pointer plus strides in elements. */
 typedef struct tda_tensor {
@@ -183,6 +189,20 @@ size_t tda_pair_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t bra
 /* Enqueue the forward / backward pass on `stream` (a hipStream_t). */
 int32_t tda_fwd(const tda_fwd_args* args, void* stream);
 int32_t tda_bwd(const tda_bwd_args* args, void* stream);
+
+/* tda_fwd without a caller workspace, and without any allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments, results and errors
+ * as tda_fwd, except that args->workspace and args->workspace_bytes are ignored: the workspace
+ * is a device array of the library, TDA_NOALLOC_SCRATCH_BYTES (16 MiB) per GPU, held from the
+ * first call on that GPU until the process ends.  A call whose workspace
+ * (tda_fwd_workspace_bytes_kv) exceeds it returns TDA_ERR_SCRATCH before touching the GPU
+ * (e.g. B*H = 64 at seq_len 4096 needs 2.4 MiB; one query against B*H = 64 heads of 16384 keys
+ * 0.5 MiB).  Every call on one GPU shares that GPU's array, which keeps the last call's
+ * contents: calls that overlap on one GPU (other streams, unordered host threads) race and
+ * must be serialised by the caller.  The outputs (out, norms, occupancy, pairs, stats) are
+ * the caller's as for tda_fwd. */
+int32_t tda_fwd_noalloc(const tda_fwd_args* args, void* stream);
 
 #ifdef __cplusplus
 }

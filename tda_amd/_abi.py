@@ -30,7 +30,9 @@ ERR_ABI = -9
 ERR_CAUSAL = -10
 ERR_NORMS = -11
 ERR_OFFSET = -12
+ERR_SCRATCH = -13
 ERR_HIP = -100
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 
 class TdaTensor(ctypes.Structure):
@@ -96,6 +98,7 @@ SIGNATURES = {
     "tda_pair_words": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
     "tda_fwd": (ctypes.c_int32, [ctypes.POINTER(TdaFwdArgs), ctypes.c_void_p]),
     "tda_bwd": (ctypes.c_int32, [ctypes.POINTER(TdaBwdArgs), ctypes.c_void_p]),
+    "tda_fwd_noalloc": (ctypes.c_int32, [ctypes.POINTER(TdaFwdArgs), ctypes.c_void_p]),
 }
 
 _lock = threading.Lock()

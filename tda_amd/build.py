@@ -28,7 +28,8 @@ HIP_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 
-HIP_SOURCES = ["tda_fwd.hip", "tda_fwd_sparse.hip", "tda_fwd_decode.hip", "tda_bwd.hip", "tda_bwd_fast.hip"]
+HIP_SOURCES = ["tda_fwd.hip", "tda_fwd_sparse.hip", "tda_fwd_decode.hip", "tda_bwd.hip", "tda_bwd_fast.hip",
+               "tda_noalloc.hip"]
 HOST_SOURCES = ["tda_host.cpp"]
 
 

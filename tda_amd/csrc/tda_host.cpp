@@ -116,6 +116,10 @@ void copy_strides(int64_t dst[3], const tda_tensor& t) {
 
 }  // namespace
 
+namespace tda {
+void record_hip_error(int e) { g_last_hip_error = e; }
+}  // namespace tda
+
 extern "C" {
 
 int32_t tda_abi_version(void) { return TDA_ABI_VERSION; }
@@ -139,6 +143,9 @@ const char* tda_error_string(int32_t code) {
     case TDA_ERR_CAUSAL: return "only the causal form is implemented (causal must be 1)";
     case TDA_ERR_NORMS: return "normalize requires the norms buffer (forward: output, backward: the forward's output)";
     case TDA_ERR_OFFSET: return "q_offset must be >= 0, and seq_len_kv and q_offset + seq_len at most 2^30 - 64";
+    case TDA_ERR_SCRATCH:
+      return "tda_fwd_noalloc: the call needs more workspace than the library's device array "
+             "(TDA_NOALLOC_SCRATCH_BYTES, 16 MiB); use tda_fwd with a caller workspace";
     case TDA_ERR_HIP: return "HIP kernel launch failed";
     default: return "unknown error";
   }

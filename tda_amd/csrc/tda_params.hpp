@@ -103,5 +103,7 @@ int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream);
 // Sum the (dbeta, dlambda) partial pairs ws[2 * item], item < items, in a fixed order.
 int launch_bwd_finish(const BwdParams& p, int branches, int64_t items, void* stream);
+// Record a hipError_t for tda_last_hip_error() (this thread).
+void record_hip_error(int e);
 
 }  // namespace tda

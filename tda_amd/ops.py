@@ -106,16 +106,23 @@ def _common(args, t: torch.Tensor, branches: int, normalize: bool, relu_power: f
 
 
 def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, branches: int,
-            norms=None, occupancy=None, stats=None, q_offset: int = 0, pairs=None) -> torch.Tensor:
+            norms=None, occupancy=None, stats=None, q_offset: int = 0, pairs=None,
+            out=None, no_alloc: bool = False) -> torch.Tensor:
     """One forward launch.  Tensors must already be in a native dtype (float32 / bfloat16)
     on one device; beta (and lam) are 0-dim float32 tensors on that device.  q1 (q2) have Nq
     rows at positions q_offset.., k1 (k2) and v have Nk rows.  The optional norms /
-    occupancy / stats / pairs buffers receive the side outputs described in include/tda.h."""
+    occupancy / stats / pairs buffers receive the side outputs described in include/tda.h.
+    no_alloc: call tda_fwd_noalloc, whose workspace is the library's own device array (no
+    workspace tensor here); with `out` (and `norms` when normalize) given, the call then
+    allocates nothing."""
     lib = _abi.load()
     q1, k1, v = _usable(q1), _usable(k1), _usable(v)
     if branches == 2:
         q2, k2 = _usable(q2), _usable(k2)
-    out = _empty_like_layout(q1)
+    if out is None:
+        out = _empty_like_layout(q1)
+    elif out.shape != q1.shape or out.dtype != q1.dtype or out.device != q1.device:
+        raise ValueError("out must match q1's shape, dtype and device")
     a = _abi.TdaFwdArgs()
     nk = k1.shape[2]
     _common(a, q1, branches, normalize, relu_power, nk, q_offset)
@@ -130,6 +137,10 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
     if stats is not None and (stats.dtype != torch.int64 or stats.numel() < 3 or stats.device != q1.device):
         raise ValueError("stats must be an int64 tensor of at least 3 elements on the inputs' device")
     a.norms, a.occupancy, a.stats, a.pairs = _ptr(norms), _ptr(occupancy), _ptr(stats), _ptr(pairs)
+    if no_alloc:
+        with torch.cuda.device(q1.device):
+            _abi.check(lib.tda_fwd_noalloc(ctypes.byref(a), _stream(q1.device)), "tda_fwd_noalloc")
+        return out
     ws = torch.empty((lib.tda_fwd_workspace_bytes_kv(*q1.shape[:3], nk, branches) + 3) // 4,
                      dtype=torch.float32, device=q1.device)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4

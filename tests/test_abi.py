@@ -287,3 +287,36 @@ def test_error_code_mapping():
     with pytest.raises(RuntimeError, match="launch failed"):
         _abi.check(_abi.ERR_HIP, "tda_fwd")
     _abi.check(_abi.OK, "tda_fwd")
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (lambda a: setattr(a, "abi_version", 99), _abi.ERR_ABI),
+    (lambda a: setattr(a, "head_dim", 96), _abi.ERR_HEAD_DIM),
+    (lambda a: setattr(a, "beta", None), _abi.ERR_NULL_POINTER),
+    (lambda a: setattr(a.q1, "data", FAKE + 2), _abi.ERR_LAYOUT),
+    (lambda a: setattr(a, "norms", None), _abi.ERR_NORMS),
+    (lambda a: setattr(a, "q_offset", -1), _abi.ERR_OFFSET),
+    # its workspace is the library's own: the caller's workspace fields are not read
+    (lambda a: setattr(a, "workspace", None), _abi.OK),
+])
+def test_fwd_noalloc_validates_like_tda_fwd(mutate, code):
+    lib = _lib()
+    a = _fwd_args()
+    mutate(a)
+    if code == _abi.OK:
+        a.head_dim = 100  # stop at the validator anyway: no GPU here
+        assert lib.tda_fwd_noalloc(ctypes.byref(a), None) == _abi.ERR_HEAD_DIM
+    else:
+        assert lib.tda_fwd_noalloc(ctypes.byref(a), None) == code
+
+
+def test_fwd_noalloc_rejects_workspace_beyond_its_array():
+    """A call needing more workspace than TDA_NOALLOC_SCRATCH_BYTES fails with ERR_SCRATCH
+    before touching a GPU; the limit in the header matches the binding's."""
+    lib = _lib()
+    assert f"TDA_NOALLOC_SCRATCH_BYTES ((size_t){_abi.NOALLOC_SCRATCH_BYTES >> 20} << 20)" in open(HEADER).read()
+    shape = (8, 64, 8192, 128)
+    assert lib.tda_fwd_workspace_bytes(*shape[:3], 2) > _abi.NOALLOC_SCRATCH_BYTES
+    a = _fwd_args(shape)
+    assert lib.tda_fwd_noalloc(ctypes.byref(a), None) == _abi.ERR_SCRATCH
+    assert b"16 MiB" in lib.tda_error_string(_abi.ERR_SCRATCH)
