@@ -204,6 +204,20 @@ int32_t tda_bwd(const tda_bwd_args* args, void* stream);
  * the caller's as for tda_fwd. */
 int32_t tda_fwd_noalloc(const tda_fwd_args* args, void* stream);
 
+/* Per-launch timing of one call: no counterpart in the reference (whose Triton launches are
+ * timed from outside); for benchmarks that need each kernel's duration without a tracer.
+ * Arms the calling thread: its next tda_fwd, tda_fwd_noalloc or tda_bwd call that passes
+ * validation records events[0] (hipEvent_t, created by the caller) on its stream before its
+ * first kernel launch and events[k] right after its k-th launch, k = 1 .. n - 1 (later launches
+ * are not bracketed), then disarms.  n = 0 (or events == NULL) disarms.  Returns TDA_OK, or
+ * TDA_ERR_NULL_POINTER for events == NULL with n > 0.  A failed event record fails the call
+ * with TDA_ERR_HIP. */
+int32_t tda_time_next_call(void* const* events, int32_t n);
+/* Kernel launches of the last timed call on this thread, and the name of launch k (0-based;
+ * NULL past the end).  Names are the kernel families: "key_norms", "fwd_screen", ... */
+int32_t     tda_timed_launches(void);
+const char* tda_timed_launch_name(int32_t k);
+
 #ifdef __cplusplus
 }
 #endif

@@ -99,6 +99,9 @@ SIGNATURES = {
     "tda_fwd": (ctypes.c_int32, [ctypes.POINTER(TdaFwdArgs), ctypes.c_void_p]),
     "tda_bwd": (ctypes.c_int32, [ctypes.POINTER(TdaBwdArgs), ctypes.c_void_p]),
     "tda_fwd_noalloc": (ctypes.c_int32, [ctypes.POINTER(TdaFwdArgs), ctypes.c_void_p]),
+    "tda_time_next_call": (ctypes.c_int32, [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int32]),
+    "tda_timed_launches": (ctypes.c_int32, []),
+    "tda_timed_launch_name": (ctypes.c_char_p, [ctypes.c_int32]),
 }
 
 _lock = threading.Lock()

@@ -31,6 +31,9 @@ HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 HIP_SOURCES = ["tda_fwd.hip", "tda_fwd_sparse.hip", "tda_fwd_decode.hip", "tda_bwd.hip", "tda_bwd_fast.hip",
                "tda_noalloc.hip"]
 HOST_SOURCES = ["tda_host.cpp"]
+# host-only code that calls the HIP runtime API (no device code): g++ against the ROCm headers
+HIP_HOST_SOURCES = ["tda_timing.cpp"]
+HIP_HOST_FLAGS = [f"-I{ROCM}/include", "-D__HIP_PLATFORM_AMD__"]
 
 
 def _run(cmd, verbose):
@@ -58,6 +61,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     for src in HOST_SOURCES:
         obj = os.path.join(BUILD_DIR, src + ".o")
         cmds.append([CXX, *HOST_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        objs.append(obj)
+    for src in HIP_HOST_SOURCES:
+        obj = os.path.join(BUILD_DIR, src + ".o")
+        cmds.append([CXX, *HOST_FLAGS, *HIP_HOST_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
     jobs = jobs or min(len(cmds), os.cpu_count() or 1)
     with ThreadPoolExecutor(max_workers=jobs) as ex:

@@ -474,7 +474,9 @@ static int launch_bwd_t(const BwdParams& p, void* stream) {
   const int64_t qitems = (int64_t)p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL((bwd_dq<Pol, D, BR, PK, NORM>), dim3((unsigned)((qitems + 3) / 4)), dim3(256), 0, s, p);
+  launched(s, "bwd_dq");
   hipLaunchKernelGGL((bwd_dkv<Pol, D, BR, PK, NORM>), dim3((unsigned)((kitems + 3) / 4)), dim3(256), 0, s, p);
+  launched(s, "bwd_dkv");
   const int e = (int)hipGetLastError();
   return e ? e : launch_bwd_finish(p, BR, (int64_t)p.B * p.H * p.nqt, stream);
 }
@@ -503,6 +505,7 @@ static int bsel_d(const BwdParams& p, const KernelKey& k, void* s) {
 int launch_bwd_finish(const BwdParams& p, int branches, int64_t items, void* stream) {
   hipLaunchKernelGGL(bwd_finish, dim3(1), dim3(kFinThreads), 0, (hipStream_t)stream, (const float*)p.ws, items, p.lam,
                      p.dbeta, p.dlam, branches);
+  launched(stream, "bwd_finish");
   return (int)hipGetLastError();
 }
 

@@ -1168,11 +1168,18 @@ template <int D, int BR, int PK, bool NORM>
 static int launch_t(const BwdParams& p, void* stream) {
   const int64_t qitems = (int64_t)BR * p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
-  if (p.pairs) hipLaunchKernelGGL((bwd_dq_pairs<D, BR, PK, NORM>), dim3((unsigned)qitems), dim3(64), 0, s, p);
+  if (p.pairs) {
+    hipLaunchKernelGGL((bwd_dq_pairs<D, BR, PK, NORM>), dim3((unsigned)qitems), dim3(64), 0, s, p);
+    launched(s, "bwd_dq_pairs");
+  }
   const int dq_per_wave = p.pairs ? 8 : 1;  // with pair lists most items exit at once
   hipLaunchKernelGGL((bwd_dq_fast<D, BR, PK, NORM>), dim3((unsigned)((qitems + dq_per_wave - 1) / dq_per_wave)),
                      dim3(64), 0, s, p, dq_per_wave);
-  if (p.pairs) hipLaunchKernelGGL((bwd_dkv_pairs<D, BR, PK, NORM>), dim3((unsigned)kitems), dim3(64), 0, s, p);
+  launched(s, "bwd_dq_fast");
+  if (p.pairs) {
+    hipLaunchKernelGGL((bwd_dkv_pairs<D, BR, PK, NORM>), dim3((unsigned)kitems), dim3(64), 0, s, p);
+    launched(s, "bwd_dkv_pairs");
+  }
   if (p.dkvq) {  // the key tiles the pair pass could not take, from its queue: one wave per SIMD
     hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3((unsigned)(kitems < 1024 ? kitems : 1024)), dim3(64), 0, s,
                        p, 0);
@@ -1181,6 +1188,7 @@ static int launch_t(const BwdParams& p, void* stream) {
     hipLaunchKernelGGL((bwd_dkv_fast<D, BR, PK, NORM>), dim3((unsigned)((kitems + dkv_per_wave - 1) / dkv_per_wave)),
                        dim3(64), 0, s, p, dkv_per_wave);
   }
+  launched(s, "bwd_dkv_fast");
   const int e = (int)hipGetLastError();
   return e ? e : launch_bwd_finish(p, BR, qitems, stream);
 }

@@ -237,6 +237,7 @@ static int launch_fwd_t(const FwdParams& p, void* stream) {
   const int64_t items = (int64_t)p.B * p.H * p.nqt;
   const unsigned grid = (unsigned)((items + 3) / 4);
   hipLaunchKernelGGL((fwd_wave<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, (hipStream_t)stream, p);
+  launched(stream, "fwd_wave");
   return (int)hipGetLastError();
 }
 

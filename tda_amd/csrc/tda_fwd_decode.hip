@@ -199,8 +199,10 @@ int launch_decode_t(const FwdParams& p, float* part, hipStream_t s) {
   const int BH = p.B * p.H;
   const int nch = (p.nkt + 31) / 32;
   hipLaunchKernelGGL((fwd_decode<D, BR, PK, NORM>), dim3((unsigned)(BH * nch)), dim3(64 * kDecWaves), 0, s, p, part);
+  launched(s, "fwd_decode");
   const int64_t n = (int64_t)BH * p.Nq * D;
   hipLaunchKernelGGL((fwd_decode_sum<D>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, (const float*)part);
+  launched(s, "fwd_decode_sum");
   return (int)hipGetLastError();
 }
 template <int D, int BR, int PK>

@@ -873,18 +873,23 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
     constexpr int rows = (64 / (D / 8)) * KN_GROUPS;  // rows per wave
     const int64_t waves = (int64_t)BR * BH * ((p.Nk + rows - 1) / rows);
     hipLaunchKernelGGL(key_norms<D>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, BR);
+    launched(s, "key_norms");
   }
   const unsigned nqb = (unsigned)((p.Nq + 255) / 256);
   constexpr int QPW = 2, TPB = 1;
   hipLaunchKernelGGL((fwd_screen<D, NORM, QPW, TPB>), dim3((unsigned)(BR * BH) * nqb), dim3(512 / QPW), 0, s, p, BR);
-  if (NORM && p.cand)
+  launched(s, "fwd_screen");
+  if (NORM && p.cand) {
     hipLaunchKernelGGL((fwd_pv_cand<D, BR, PK>), dim3((unsigned)(BH * p.nqt)), dim3(64), 0, s, p);
+    launched(s, "fwd_pv_cand");
+  }
   if (NORM && p.cand) {  // the query tiles the candidate pass could not take, from its queue
     const int items = BH * p.nqt;
     hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)(items < 2048 ? items : 2048)), dim3(64), 0, s, p, 0);
   } else {
     hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)(BH * p.nqt)), dim3(64), 0, s, p, 1);
   }
+  launched(s, "fwd_pv");
   return (int)hipGetLastError();
 }
 

@@ -274,7 +274,10 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
   p.pairs = a->pairs;
   p.nbr = a->branches;
   const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};
-  const int e = tda::launch_fwd(p, key, stream);
+  tda::timing_begin(stream);
+  int e = tda::launch_fwd(p, key, stream);
+  const int te = tda::timing_end();
+  if (e == 0) e = te;
   if (e != 0) {
     g_last_hip_error = e;
     return TDA_ERR_HIP;
@@ -328,7 +331,10 @@ int32_t tda_bwd(const tda_bwd_args* a, void* stream) {
   if (p.pairs && (int64_t)a->batch * a->heads * p.nkt <= lists * tda::kPairCap)
     p.dkvq = reinterpret_cast<uint32_t*>(p.pws + lists * tda::kPairCap);
   const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};
-  const int e = tda::launch_bwd(p, key, stream);
+  tda::timing_begin(stream);
+  int e = tda::launch_bwd(p, key, stream);
+  const int te = tda::timing_end();
+  if (e == 0) e = te;
   if (e != 0) {
     g_last_hip_error = e;
     return TDA_ERR_HIP;

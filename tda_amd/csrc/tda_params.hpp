@@ -105,5 +105,11 @@ int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_finish(const BwdParams& p, int branches, int64_t items, void* stream);
 // Record a hipError_t for tda_last_hip_error() (this thread).
 void record_hip_error(int e);
+// Per-launch timing of one call (tda_time_next_call; tda_timing.cpp): the C-ABI entry points
+// bracket their launches with timing_begin / timing_end (which returns the first failed event
+// record, 0 if none) and every launcher reports each kernel launch, in stream order.
+void timing_begin(void* stream);
+void launched(void* stream, const char* name);
+int timing_end();
 
 }  // namespace tda

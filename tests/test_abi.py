@@ -320,3 +320,20 @@ def test_fwd_noalloc_rejects_workspace_beyond_its_array():
     a = _fwd_args(shape)
     assert lib.tda_fwd_noalloc(ctypes.byref(a), None) == _abi.ERR_SCRATCH
     assert b"16 MiB" in lib.tda_error_string(_abi.ERR_SCRATCH)
+
+
+def test_launch_timing_arming_without_a_device():
+    """tda_time_next_call only records the caller's events: NULL events with n > 0 are an
+    error, n = 0 disarms, and a thread that made no timed call reports no launches."""
+    lib = _lib()
+    assert lib.tda_time_next_call(None, 3) == _abi.ERR_NULL_POINTER
+    assert lib.tda_time_next_call(None, 0) == _abi.OK
+    assert lib.tda_timed_launches() == 0
+    assert lib.tda_timed_launch_name(0) is None
+    assert lib.tda_timed_launch_name(-1) is None
+    # an armed call that fails validation records nothing and stays armed for the next one
+    evs = (ctypes.c_void_p * 2)(None, None)
+    assert lib.tda_time_next_call(evs, 2) == _abi.OK
+    assert lib.tda_fwd(None, None) == _abi.ERR_NULL_POINTER
+    assert lib.tda_timed_launches() == 0
+    assert lib.tda_time_next_call(None, 0) == _abi.OK
