@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define TDA_ABI_VERSION 5
+#define TDA_ABI_VERSION 6
 
 /* element types of q, k, v, out and gradients */
 #define TDA_DTYPE_F32  0
@@ -132,6 +132,14 @@ typedef struct tda_fwd_args {
                                non-zero weights (key index, row, exact threshold margin), which
                                lets the backward read only the rows they name; bf16 only (the
                                f32 forward leaves it alone) */
+  void*    zero;            /* optional (may be NULL with zero_bytes == 0): a device range the
+                               call sets to zero, 16-byte aligned, zero_bytes a multiple of 16.
+                               For training: the buffer of the backward's gradients, zeroed while
+                               the forward's matrix-core pass runs (its HBM is mostly idle), so
+                               the backward (grads_zeroed = 1) writes only the non-zero rows.  It
+                               must not overlap any other buffer of the call.  No counterpart in
+                               the reference. */
+  uint64_t zero_bytes;
 } tda_fwd_args;
 
 typedef struct tda_bwd_args {
@@ -160,6 +168,10 @@ typedef struct tda_bwd_args {
   int64_t q_offset;
   const uint32_t* pairs;    /* the forward's pair lists, or NULL; used only with occupancy
                                (bf16): lists that did not fit fall back to the bitmask tiles */
+  int32_t grads_zeroed;     /* 1: dq1, dk1, (dq2, dk2,) dv hold zeros already (e.g. the forward's
+                               zero range); the call then stores only the gradient rows that a
+                               non-zero weight reaches.  0: every row is stored.  No counterpart
+                               in the reference. */
 } tda_bwd_args;
 
 int32_t     tda_abi_version(void);

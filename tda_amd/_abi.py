@@ -13,7 +13,7 @@ import threading
 HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(HERE, "libtda_hip.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
@@ -62,6 +62,7 @@ class TdaFwdArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("seq_len_kv", ctypes.c_int64), ("q_offset", ctypes.c_int64),
         ("pairs", ctypes.c_void_p),
+        ("zero", ctypes.c_void_p), ("zero_bytes", ctypes.c_uint64),
     ]
 
 
@@ -78,6 +79,7 @@ class TdaBwdArgs(ctypes.Structure):
         ("stats", ctypes.c_void_p),
         ("seq_len_kv", ctypes.c_int64), ("q_offset", ctypes.c_int64),
         ("pairs", ctypes.c_void_p),
+        ("grads_zeroed", ctypes.c_int32),
     ]
 
 

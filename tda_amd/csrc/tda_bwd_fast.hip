@@ -506,7 +506,7 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
     last_kt = kt;
   }
   const int q0 = 32 * qt;
-  zero_rows<D>(gb + (int64_t)q0 * sg, sg, min(32, P.Nq - q0), used);
+  if (!P.grads_zeroed) zero_rows<D>(gb + (int64_t)q0 * sg, sg, min(32, P.Nq - q0), used);
 
   // The pairs sorted by query row, then list order: lane s gets the pair of rank s (lanes past
   // the count keep their own slot, so the ranks form a permutation of the lanes).
@@ -781,11 +781,13 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
   const uint32_t uall = BR == 2 ? used[0] | used[BR - 1] : used[0];
   bf16* dvb = gbase(B_DV, 4);
   const int64_t sdv = P.s[B_DV][2];
-  zero_rows<D>(dvb + (int64_t)(32 * kt) * sdv, sdv, nrows, uall);
+  if (!P.grads_zeroed) {
+    zero_rows<D>(dvb + (int64_t)(32 * kt) * sdv, sdv, nrows, uall);
 #pragma unroll
-  for (int br = 0; br < BR; ++br) {
-    const int gslot = br == 0 ? B_DK1 : B_DK2;
-    zero_rows<D>(gbase(gslot, br == 0 ? 1 : 3) + (int64_t)(32 * kt) * P.s[gslot][2], P.s[gslot][2], nrows, used[br]);
+    for (int br = 0; br < BR; ++br) {
+      const int gslot = br == 0 ? B_DK1 : B_DK2;
+      zero_rows<D>(gbase(gslot, br == 0 ? 1 : 3) + (int64_t)(32 * kt) * P.s[gslot][2], P.s[gslot][2], nrows, used[br]);
+    }
   }
   const bf16* dob = base(B_DO);
   const int64_t sdo = P.s[B_DO][2];

@@ -262,11 +262,30 @@ static int sel_d(const FwdParams& p, const KernelKey& k, void* s) {
   return k.d == 128 ? sel_br<Pol, 128>(p, k, s) : sel_br<Pol, 64>(p, k, s);
 }
 
+// The zero range of a call whose path has no screen (which clears it otherwise): 16 bytes per
+// lane, streaming stores.
+__global__ void __launch_bounds__(256) zero_range(void* z, int64_t units) {
+  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256)
+    __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u}, reinterpret_cast<u32x4*>(z) + u);
+}
+int launch_zero(const FwdParams& p, void* stream) {
+  if (!p.zero || p.zero_units <= 0) return 0;
+  const int64_t blocks = (p.zero_units + 255) / 256;
+  hipLaunchKernelGGL(zero_range, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, (hipStream_t)stream,
+                     p.zero, p.zero_units);
+  launched(stream, "zero_range");
+  return (int)hipGetLastError();
+}
+
 // bf16 runs the screen + sparse A.V kernels (tda_fwd_sparse.hip), or with a single query tile
-// the split-key decode kernels (tda_fwd_decode.hip); fp32 runs fwd_wave.
+// the split-key decode kernels (tda_fwd_decode.hip); fp32 runs fwd_wave.  The screen clears the
+// call's zero range; the other paths launch zero_range.
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream) {
-  if (k.dtype == 1) return p.nqt == 1 && p.part ? launch_fwd_decode(p, k, p.part, stream) : launch_fwd_sparse(p, k, stream);
-  return sel_d<PolF32>(p, k, stream);
+  int e;
+  if (k.dtype == 1 && !(p.nqt == 1 && p.part)) return launch_fwd_sparse(p, k, stream);
+  if (k.dtype == 1) e = launch_fwd_decode(p, k, p.part, stream);
+  else e = sel_d<PolF32>(p, k, stream);
+  return e ? e : launch_zero(p, stream);
 }
 
 }  // namespace tda

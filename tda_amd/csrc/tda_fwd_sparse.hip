@@ -288,6 +288,30 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     }
   }
 
+  // ---- the call's zero range (the backward's gradients in training), spread over the steps of
+  // every workgroup: workgroup (stream, block) clears zero_per_it units per key tile it walks,
+  // from the sum of the steps of the workgroups before it in (stream, block) order
+  int64_t z0 = 0, zend = 0;
+  if (P.zero) {
+    int64_t before = 0, per_stream = 0;
+    for (int q = 0; q < (Nq + 255) / 256; ++q) {
+      const int n = kt_last(min(8 * q + 7, nqt - 1), qoff, P.nkt) + 1;
+      before += q < qb ? n : 0;
+      per_stream += n;
+    }
+    z0 = ((int64_t)sidx * per_stream + before) * P.zero_per_it;
+    zend = min(z0 + (int64_t)nkt * P.zero_per_it, P.zero_units);
+  }
+  // buffer stores over the workgroup's slice: the hardware drops those past its end (a slice
+  // is below 1 MiB, so 32-bit offsets); streaming (nt): the backward reads them much later
+  const __amdgpu_buffer_rsrc_t rzero =
+      make_rsrc(P.zero ? reinterpret_cast<u32x4*>(P.zero) + z0 : nullptr, (uint32_t)(zend > z0 ? (zend - z0) * 16 : 0));
+  auto clear = [&](int kt) {
+    const uint32_t step = (uint32_t)kt * (uint32_t)P.zero_per_it * 16u;
+    for (int u = tid; u < P.zero_per_it; u += NTHR)
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rzero, (uint32_t)u * 16u, step, 2);
+  };
+
   uint32_t* occ0 = P.occ + ((int64_t)sidx * nqt + qt0) * P.occ_w;  // bitmask row of qt0 (then qt0 + 1)
   // Per lane and query tile: bit kt % 32 set when the lane's test passed for key tile kt.  The
   // wave ORs them when a 32-tile word is complete (cheaper than a ballot per tile).
@@ -392,6 +416,7 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     for (int j = 0; j < TPB; ++j) {
       const int kt = TPB * it + j;
       if (kt >= nkt) break;
+      if (P.zero) clear(kt);
       process(kt, TPB * (it & 1) + j);
       flush(kt);
     }

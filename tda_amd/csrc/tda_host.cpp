@@ -212,6 +212,8 @@ int32_t tda_validate_fwd(const tda_fwd_args* a) {
     return TDA_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0) return TDA_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(a->pairs) % 16 != 0) return TDA_ERR_LAYOUT;
+  if (a->zero_bytes % 16 != 0 || reinterpret_cast<uintptr_t>(a->zero) % 16 != 0) return TDA_ERR_LAYOUT;
+  if (a->zero_bytes && !a->zero) return TDA_ERR_NULL_POINTER;
   return TDA_OK;
 }
 
@@ -273,6 +275,21 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
   p.stats = a->stats;
   p.pairs = a->pairs;
   p.nbr = a->branches;
+  if (a->zero_bytes) {
+    p.zero = a->zero;
+    p.zero_units = (int64_t)(a->zero_bytes / 16);
+    // the screen's workgroups walk sum over (branch, head, 256-row block) of its key tiles:
+    // spread the units evenly over those steps
+    int64_t steps = 0;
+    for (int qb = 0; qb < (p.Nq + 255) / 256; ++qb) {
+      const int qt = qb * 8 + 7 < p.nqt - 1 ? qb * 8 + 7 : p.nqt - 1;
+      const int64_t last = (int64_t)p.qoff + 32 * qt + 31;  // last position of the block
+      const int64_t klast = last / 32 < p.nkt - 1 ? last / 32 : p.nkt - 1;
+      steps += klast + 1;
+    }
+    steps *= (int64_t)a->branches * a->batch * a->heads;
+    p.zero_per_it = (int)((p.zero_units + steps - 1) / steps);
+  }
   const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};
   tda::timing_begin(stream);
   int e = tda::launch_fwd(p, key, stream);
@@ -327,6 +344,7 @@ int32_t tda_bwd(const tda_bwd_args* a, void* stream) {
   p.pws = p.ws + 2 * lists;  // after the partial pairs
   p.stats = a->stats;
   p.pairs = a->occupancy ? a->pairs : nullptr;  // the key-major pass finds the lists through the bitmask
+  p.grads_zeroed = a->grads_zeroed ? 1 : 0;
   // the key-tile queue, when it holds every key tile
   if (p.pairs && (int64_t)a->batch * a->heads * p.nkt <= lists * tda::kPairCap)
     p.dkvq = reinterpret_cast<uint32_t*>(p.pws + lists * tda::kPairCap);

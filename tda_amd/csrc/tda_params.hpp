@@ -62,6 +62,9 @@ struct FwdParams {
   uint32_t* cand;            // candidate keys (workspace; null for a single query tile)
   uint32_t* pvq;             // with cand: query tiles for the tile pass ([0] count, then bh nqt + qt),
                              // zeroed by the screen, filled by the candidate pass (workspace)
+  void* zero;                // may be null: 16-byte units [0, zero_units) the call sets to zero
+  int64_t zero_units;
+  int zero_per_it;           // units each screen workgroup clears per key tile it walks
 };
 
 struct BwdParams {
@@ -85,6 +88,7 @@ struct BwdParams {
   uint32_t* dkvq;            // may be null: key tiles for the key-major tile pass ([0] count, then
                              // items), zeroed by the query-major pair pass, filled by the key-major
                              // pair pass (workspace)
+  int grads_zeroed;          // the gradient rows hold zeros: the pair passes store named rows only
 };
 
 // Kernel-family launchers (return a hipError_t value).  Template selection happens inside.
@@ -101,6 +105,8 @@ int launch_fwd_sparse(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_fwd_decode(const FwdParams& p, const KernelKey& k, float* part, void* stream);
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream);
+// Set the forward's zero range to zero (paths without the screen, which clears it otherwise).
+int launch_zero(const FwdParams& p, void* stream);
 // Sum the (dbeta, dlambda) partial pairs ws[2 * item], item < items, in a fixed order.
 int launch_bwd_finish(const BwdParams& p, int branches, int64_t items, void* stream);
 // Record a hipError_t for tda_last_hip_error() (this thread).

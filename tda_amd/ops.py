@@ -107,14 +107,15 @@ def _common(args, t: torch.Tensor, branches: int, normalize: bool, relu_power: f
 
 def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, branches: int,
             norms=None, occupancy=None, stats=None, q_offset: int = 0, pairs=None,
-            out=None, no_alloc: bool = False) -> torch.Tensor:
+            out=None, no_alloc: bool = False, zero=None) -> torch.Tensor:
     """One forward launch.  Tensors must already be in a native dtype (float32 / bfloat16)
     on one device; beta (and lam) are 0-dim float32 tensors on that device.  q1 (q2) have Nq
     rows at positions q_offset.., k1 (k2) and v have Nk rows.  The optional norms /
     occupancy / stats / pairs buffers receive the side outputs described in include/tda.h.
     no_alloc: call tda_fwd_noalloc, whose workspace is the library's own device array (no
     workspace tensor here); with `out` (and `norms` when normalize) given, the call then
-    allocates nothing."""
+    allocates nothing.  zero: a contiguous tensor the call sets to zero (the gradient buffer
+    of grad_buffers, cleared while the forward runs)."""
     lib = _abi.load()
     q1, k1, v = _usable(q1), _usable(k1), _usable(v)
     if branches == 2:
@@ -137,6 +138,10 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
     if stats is not None and (stats.dtype != torch.int64 or stats.numel() < 3 or stats.device != q1.device):
         raise ValueError("stats must be an int64 tensor of at least 3 elements on the inputs' device")
     a.norms, a.occupancy, a.stats, a.pairs = _ptr(norms), _ptr(occupancy), _ptr(stats), _ptr(pairs)
+    if zero is not None:
+        if not zero.is_contiguous() or zero.device != q1.device:
+            raise ValueError("zero must be a contiguous tensor on the inputs' device")
+        a.zero, a.zero_bytes = zero.data_ptr(), zero.numel() * zero.element_size()
     if no_alloc:
         with torch.cuda.device(q1.device):
             _abi.check(lib.tda_fwd_noalloc(ctypes.byref(a), _stream(q1.device)), "tda_fwd_noalloc")
@@ -149,20 +154,51 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
     return out
 
 
+def grad_buffers(q1, k1, q2, k2, v, branches: int):
+    """One allocation holding the backward's gradient tensors: returns (buffer, [dq1, dk1,
+    dq2, dk2, dv]) with the branch-2 entries None when branches == 1.  Each gradient has its
+    input's shape and dtype, in the memory order _empty_like_layout would give it; the forward
+    can clear the whole buffer (its `zero` argument) and the backward then stores only the
+    non-zero rows (grads=)."""
+    srcs = [q1, k1, q2, k2, v] if branches == 2 else [q1, k1, None, None, v]
+    sizes = [0 if t is None else t.numel() for t in srcs]
+    buf = torch.empty(sum(sizes), dtype=q1.dtype, device=q1.device)
+    views, off = [], 0
+    for t, n in zip(srcs, sizes):
+        if t is None:
+            views.append(None)
+            continue
+        flat = buf[off:off + n]
+        off += n
+        b, h, s, d = t.shape
+        if h > 1 and s > 1 and t.stride(1) < t.stride(2):
+            views.append(flat.view(b, s, h, d).transpose(1, 2))
+        else:
+            views.append(flat.view(b, h, s, d))
+    return buf, views
+
+
 def backward(q1, k1, q2, k2, v, dout, beta, lam, relu_power: float, normalize: bool,
-             branches: int, norms=None, occupancy=None, stats=None, q_offset: int = 0, pairs=None):
+             branches: int, norms=None, occupancy=None, stats=None, q_offset: int = 0, pairs=None,
+             grads=None):
     """One backward launch: returns (dq1, dk1, dq2, dk2, dv, dbeta, dlambda); the branch-2
     entries and dlambda are None when branches == 1.  pairs: the forward's pair lists (bf16,
-    with occupancy), or None for the bitmask tiles alone."""
+    with occupancy), or None for the bitmask tiles alone.  grads: the [dq1, dk1, dq2, dk2, dv]
+    of grad_buffers whose buffer the forward cleared; the call then stores only the gradient
+    rows some non-zero weight reaches."""
     lib = _abi.load()
     q1, k1, v, dout = _usable(q1), _usable(k1), _usable(v), _usable(dout)
     if branches == 2:
         q2, k2 = _usable(q2), _usable(k2)
     dev = q1.device
-    dq1, dk1, dv = _empty_like_layout(q1), _empty_like_layout(k1), _empty_like_layout(v)
     dq2 = dk2 = dlam = None
+    if grads is not None:
+        dq1, dk1, dq2, dk2, dv = grads
+    else:
+        dq1, dk1, dv = _empty_like_layout(q1), _empty_like_layout(k1), _empty_like_layout(v)
+        if branches == 2:
+            dq2, dk2 = _empty_like_layout(q2), _empty_like_layout(k2)
     if branches == 2:
-        dq2, dk2 = _empty_like_layout(q2), _empty_like_layout(k2)
         dlam = torch.empty((), dtype=torch.float32, device=dev)
     dbeta = torch.empty((), dtype=torch.float32, device=dev)
     b, h, n, d = q1.shape
@@ -180,6 +216,7 @@ def backward(q1, k1, q2, k2, v, dout, beta, lam, relu_power: float, normalize: b
     a.norms, a.occupancy, a.pairs = _ptr(norms), _ptr(occupancy), _ptr(pairs)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
     a.stats = _ptr(stats)
+    a.grads_zeroed = 1 if grads is not None else 0
     with torch.cuda.device(dev):
         _abi.check(lib.tda_bwd(ctypes.byref(a), _stream(dev)), "tda_bwd")
     return dq1, dk1, dq2, dk2, dv, dbeta, dlam
@@ -213,25 +250,29 @@ class TDAFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches, q_offset=0):
         need = any(ctx.needs_input_grad[:7])
-        norms = occ = pairs = None
+        norms = occ = pairs = gbuf = None
+        grads = [None] * 5
         if need:
             norms, occ = side_buffers(q1.shape, branches, normalize, q1.device, k1.shape[2])
             if q1.dtype == torch.bfloat16:
                 pairs = pair_buffer(q1.shape, branches, q1.device)
+                # the gradients, cleared by this forward while its matrix-core pass runs: the
+                # pair backward then stores only the rows a non-zero weight reaches
+                gbuf, grads = grad_buffers(q1, k1, q2, k2, v, branches)
         out = forward(q1, k1, q2, k2, v, beta, lam, relu_power, normalize, branches, norms, occ,
-                      q_offset=q_offset, pairs=pairs)
-        ctx.save_for_backward(q1, k1, q2, k2, v, beta, lam, norms, occ, pairs)
-        ctx.cfg = (float(relu_power), bool(normalize), int(branches), int(q_offset))
+                      q_offset=q_offset, pairs=pairs, zero=gbuf)
+        ctx.save_for_backward(q1, k1, q2, k2, v, beta, lam, norms, occ, pairs, *grads)
+        ctx.cfg = (float(relu_power), bool(normalize), int(branches), int(q_offset), gbuf is not None)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q1, k1, q2, k2, v, beta, lam, norms, occ, pairs = ctx.saved_tensors
-        relu_power, normalize, branches, q_offset = ctx.cfg
+        q1, k1, q2, k2, v, beta, lam, norms, occ, pairs, *grads = ctx.saved_tensors
+        relu_power, normalize, branches, q_offset, zeroed = ctx.cfg
         dout = dout.to(q1.dtype)
         dq1, dk1, dq2, dk2, dv, dbeta, dlam = backward(
             q1, k1, q2, k2, v, dout, beta, lam, relu_power, normalize, branches, norms, occ,
-            q_offset=q_offset, pairs=pairs)
+            q_offset=q_offset, pairs=pairs, grads=grads if zeroed else None)
         ng = ctx.needs_input_grad
         return (dq1 if ng[0] else None, dk1 if ng[1] else None,
                 dq2 if ng[2] else None, dk2 if ng[3] else None,

@@ -148,6 +148,10 @@ def test_valid_args_pass():
     (lambda a: setattr(a, "seq_len_kv", -5), _abi.ERR_OFFSET),
     # more key rows need a wider bitmask than the workspace holds
     (lambda a: setattr(a, "seq_len_kv", 5000), _abi.ERR_WORKSPACE),
+    # the zero range: 16-byte aligned, a multiple of 16 bytes, present when its size is not 0
+    (lambda a: (setattr(a, "zero", FAKE), setattr(a, "zero_bytes", 40)), _abi.ERR_LAYOUT),
+    (lambda a: (setattr(a, "zero", FAKE + 8), setattr(a, "zero_bytes", 64)), _abi.ERR_LAYOUT),
+    (lambda a: (setattr(a, "zero", None), setattr(a, "zero_bytes", 64)), _abi.ERR_NULL_POINTER),
 ])
 def test_fwd_validator_rejects(mutate, code):
     lib = _lib()
@@ -155,6 +159,18 @@ def test_fwd_validator_rejects(mutate, code):
     mutate(a)
     assert lib.tda_validate_fwd(ctypes.byref(a)) == code
     assert lib.tda_fwd(ctypes.byref(a), None) == code  # rejected before any launch
+
+
+def test_zero_range_args_pass():
+    lib = _lib()
+    a = _fwd_args()
+    a.zero, a.zero_bytes = FAKE, 1 << 20
+    assert lib.tda_validate_fwd(ctypes.byref(a)) == _abi.OK
+    a.zero, a.zero_bytes = None, 0
+    assert lib.tda_validate_fwd(ctypes.byref(a)) == _abi.OK
+    b = _bwd_args()
+    b.grads_zeroed = 1
+    assert lib.tda_validate_bwd(ctypes.byref(b)) == _abi.OK
 
 
 def test_offset_args_pass():
