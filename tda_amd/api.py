@@ -108,10 +108,54 @@ def differential_threshold_rela_triton(q1, q2, k1, k2, v, beta, lambda_param, re
                 relu_power, normalize, 2, q_offset)
 
 
-class ThresholdRelaFunction:
-    """Name-compatible stand-in for the reference's autograd Function (TTA:327-469):
-    ThresholdRelaFunction.apply(q, k, v, beta, relu_power) == threshold_rela_triton(...)."""
+class ThresholdRelaFunction(torch.autograd.Function):
+    """The reference's autograd Function (TTA:327-469) with its interface:
+    forward(ctx, q, k, v, beta, relu_power) -> out and backward(ctx, dout) -> (dq, dk, dv,
+    None, None), single branch, no normalisation, causal.  Like the reference it gives beta and
+    relu_power no gradient (TTA:469); threshold_rela_triton above gives beta one.  Runs the same
+    kernels as TDAFunction (ops.py) through the C ABI."""
 
     @staticmethod
-    def apply(q, k, v, beta, relu_power):
-        return threshold_rela_triton(q, k, v, beta, relu_power)
+    def forward(ctx, q, k, v, beta, relu_power):
+        ops._check_inputs((q, k, v), ("q", "k", "v"), kv_from=1)
+        if q.shape[-1] not in (64, 128):
+            raise ValueError(f"head_dim must be 64 or 128, got {q.shape[-1]}")
+        p = _power(relu_power)
+        cdt = _COMPUTE.get(q.dtype)
+        if cdt is None:
+            raise ValueError(f"unsupported dtype {q.dtype}")
+        off = _offset(None, q.shape[2], k.shape[2])
+        beta_t = _scalar(beta, q.device, "beta").detach()
+        qc, kc, vc = (t if t.dtype == cdt else t.to(cdt) for t in (q, k, v))
+        ctx.dtype = q.dtype
+        ctx.cfg = (p, off)
+        if any(t.numel() == 0 for t in (q, k, v)):  # no query rows or no keys: the output is 0
+            ctx.empty = True
+            return torch.zeros_like(q)
+        ctx.empty = False
+        need = any(ctx.needs_input_grad[:3])
+        occ = pairs = gbuf = None
+        grads = [None] * 5
+        if need:
+            _, occ = ops.side_buffers(qc.shape, 1, False, qc.device, kc.shape[2])
+            if cdt == torch.bfloat16:
+                pairs = ops.pair_buffer(qc.shape, 1, qc.device)
+                gbuf, grads = ops.grad_buffers(qc, kc, None, None, vc, 1)
+        out = ops.forward(qc, kc, None, None, vc, beta_t, None, p, False, 1, None, occ, q_offset=off,
+                          pairs=pairs, zero=gbuf)
+        ctx.save_for_backward(qc, kc, vc, beta_t, occ, pairs, *grads)
+        ctx.zeroed = gbuf is not None
+        return out if out.dtype == q.dtype else out.to(q.dtype)
+
+    @staticmethod
+    def backward(ctx, dout):
+        if ctx.empty:
+            return None, None, None, None, None
+        qc, kc, vc, beta_t, occ, pairs, *grads = ctx.saved_tensors
+        p, off = ctx.cfg
+        dq, dk, _, _, dv, _, _ = ops.backward(qc, kc, None, None, vc, dout.to(qc.dtype), beta_t, None, p, False, 1,
+                                              None, occ, q_offset=off, pairs=pairs,
+                                              grads=grads if ctx.zeroed else None)
+        dq, dk, dv = (g if g.dtype == ctx.dtype else g.to(ctx.dtype) for g in (dq, dk, dv))
+        ng = ctx.needs_input_grad
+        return dq if ng[0] else None, dk if ng[1] else None, dv if ng[2] else None, None, None
