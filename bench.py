@@ -339,7 +339,7 @@ def main(argv=None) -> int:
     lam = torch.tensor(LAM, device=dev)
     stream = torch.cuda.current_stream(dev)
 
-    # ---- forward only (key_norms, fwd_screen, fwd_pv_cand, fwd_pv per call), events around the calls
+    # ---- forward only (key_prep, fwd_screen, fwd_pv_cand, fwd_pv per call), events around the calls
     fwd = lambda: ops.forward(q1, k1, q2, k2, v, beta, lam, POWER, True, 2)  # noqa: E731
     with torch.no_grad():
         fwd_ms = time_calls(stream, fwd, args.steps, args.warmup)

@@ -118,11 +118,14 @@ typedef struct tda_fwd_args {
                                weight tile (A.V issued), [2] += those whose exact weights
                                were evaluated (bf16: the tiles the screen kept, a superset
                                of [1]; f32 leaves [2] alone); tiles are 32x32 */
-  void*  workspace;         /* device scratch of tda_fwd_workspace_bytes_kv() bytes,
-                               16-byte aligned: holds the tile bitmask when occupancy is NULL
-                               and, when seq_len <= 32, the fp32 per-chunk partial outputs of
-                               the single-query-tile (decode) kernels, else the screen's
-                               candidate keys per (branch, head, query tile) */
+  void*  workspace;         /* device scratch of tda_fwd_workspace_bytes_for(args) bytes (or
+                               the larger tda_fwd_workspace_bytes_kv()), 16-byte aligned: holds
+                               the tile bitmask when occupancy is NULL and, when seq_len <= 32,
+                               the fp32 per-chunk partial outputs of the single-query-tile
+                               (decode) kernels, else the screen's candidate keys per (branch,
+                               head, query tile) and, for bf16 with normalize, the key rows
+                               quantised to int8 for the screen (head_dim + 8 bytes per key row
+                               and branch) */
   size_t workspace_bytes;
   int64_t seq_len_kv;       /* Nk, the key/value rows; 0 means Nk = seq_len */
   int64_t q_offset;         /* position of query row 0 (>= 0); 0 with Nk = Nq is the
@@ -184,7 +187,10 @@ int32_t tda_validate_fwd(const tda_fwd_args* args);
 int32_t tda_validate_bwd(const tda_bwd_args* args);
 
 /* Buffer sizes for the optional forward outputs and the backward workspace (0 for invalid
-   arguments).  The _kv forms take the key rows Nk; the others are the Nk = Nq case. */
+   arguments).  The _kv forms take the key rows Nk; the others are the Nk = Nq case.  The forward
+   workspace functions without a tda_fwd_args return the largest any call of that shape needs
+   (bf16 with normalize, head_dim 128); tda_fwd_workspace_bytes_for gives the exact need of one
+   call (its dtype, normalize and head_dim; the workspace fields are not read). */
 size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 size_t tda_norms_floats(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 size_t tda_fwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
@@ -194,6 +200,7 @@ size_t tda_norms_floats_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_
                            int32_t branches);
 size_t tda_fwd_workspace_bytes_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv,
                                   int32_t branches);
+size_t tda_fwd_workspace_bytes_for(const tda_fwd_args* args);
 size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim);
 /* Words of the pair-list output (queries seq_len; no dependence on the key rows). */
 size_t tda_pair_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);

@@ -96,6 +96,7 @@ SIGNATURES = {
     "tda_occupancy_words_kv": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int32]),
     "tda_norms_floats_kv": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int32]),
     "tda_fwd_workspace_bytes_kv": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int32]),
+    "tda_fwd_workspace_bytes_for": (ctypes.c_size_t, [ctypes.POINTER(TdaFwdArgs)]),
     "tda_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4),
     "tda_pair_words": (ctypes.c_size_t, [ctypes.c_int64] * 3 + [ctypes.c_int32]),
     "tda_fwd": (ctypes.c_int32, [ctypes.POINTER(TdaFwdArgs), ctypes.c_void_p]),

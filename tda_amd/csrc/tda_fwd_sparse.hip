@@ -7,17 +7,17 @@
 // out = A1 V - clamp(lambda, 0, 1) A2 V (TTA:489-519).
 //
 // Launches, in stream order:
-//   key_norms   inverse L2 norms rk_j of the key rows, into the norms table (normalize only).
+//   key_prep    (normalize) inverse L2 norms rk_j of the key rows into the norms table, and the
+//               normalised key rows quantised to int8 with a per-row scale and residual bound.
 //   fwd_screen  for every causal (query tile, key tile) pair of a branch, a score tile on the
 //               matrix cores and a test that keeps every tile holding a non-zero weight
 //               (x_ij = fma(s_ij rk_j, rq_i, -tau_i) > 0 for some pair).  Without normalisation
-//               the test is exact; with it, the queries enter pre-scaled by their inverse norms
-//               and the test carries a margin bounded per query tile from the bf16 rounding
-//               residuals of its rows (screen_tlo), so it may keep a few tiles whose weights
-//               are all zero.  No V and no output accumulators: the kernel
-//               holds only Q fragments and two score tiles per wave, so MFMA results stay in
-//               ordinary VGPRs and several waves share a SIMD.  With normalisation it also
-//               lists each query tile's candidate keys (the keys of its passing lanes).
+//               (fwd_screen) the test is exact on the bf16 scores; with it (fwd_screen_i8) the
+//               scores are int8 products of the quantised normalised rows and the test carries a
+//               bound on the quantisation residuals, so it may keep tiles and keys whose weights
+//               are all zero, never drop a non-zero one.  No V and no output accumulators, so
+//               several waves share a SIMD.  With normalisation it also lists each query
+//               tile's candidate keys (the keys of its passing lanes).
 //   fwd_pv_cand (normalize) one wave per query tile whose candidate lists fit: the score tile
 //               of its rows against the candidate keys (the same MFMA sequence and operand
 //               values as fwd_pv, so the same scores), the exact weights and out += coef A V
@@ -76,30 +76,6 @@ __device__ __forceinline__ float maximum16(const f32x16& v) {
   return m3(m3(a, b, c), m3(d, e, v[15]), v[15]);
 }
 
-// Threshold of the normalised screen for one query tile, in cosine units.
-//
-// The exact pass keeps weight (i, j) iff x_ij = fma(fl(S_ij rk_j), rq_i, -tau_i) > 0, with S_ij
-// the fp32 MFMA sum of q_i . k_j; the screen tests fl(sh_ij rk_j) > tlo with sh_ij the fp32 MFMA
-// sum of qh_i . k_j and qh_i = bf16(fl(q_i rq_i)) (rq_i, rk_j: the same fp32 inverse norms on
-// both sides).  Write qh_i = rq_i q_i + r_i + f_i, r_i = qh_i - fl(q_i rq_i) the bf16 rounding
-// residual (exact in fp32) and |f_i| <= 2^-24 rq_i |q_i| the fp32 product's.  Then
-//   |sh_ij - rq_i S_ij| <= (|r_i| + 2^-24 + 2^-17 |qh_i| + 2^-17 rq_i |q_i|) |k_j|
-// (each 128-term fp32 accumulation errs by at most 128 * 2^-24 = 2^-17 of |a||b|, Cauchy-
-// Schwarz), and with rq_i |q_i|, rk_j |k_j| <= 1 + 2^-16 and |qh_i| <= 1.01 the difference
-// after the factor rk_j stays below |r_i| (1 + 2^-16) + 2^-15.  The two fp32 products of the
-// tests add a relative 2^-24 each on values of magnitude <= 1.02.  So with
-//   tlo = min_i tau_i - |min_i tau_i| 2^-19 - (max_i |r_i| (1 + 2^-14) + 2^-14)
-// every kept weight passes the screen: max_i |r_i| is computed per query tile where qh is
-// formed (fp32 sum of squares and square root: relative error below 2^-16, covered by the
-// 2^-14 factor), and 2^-14 covers the 2^-15 of the accumulations plus the products' 2^-22.
-// tau_i, evaluated in fp32 with a few ulps of error, is monotone in i up to a relative 2^-20;
-// the 2^-19 term covers that and the products' relative error on tau.  A bf16 residual is
-// at most 2^-8 of each element (unit roundoff of an 8-bit significand), so |r_i| <= 2^-8 |qh_i|;
-// on N(0,1) rows it is about 0.0016.
-__device__ __forceinline__ float screen_tlo(float tmin, float rmax) {
-  return tmin - fabsf(tmin) * 0x1p-19f - (rmax * (1.f + 0x1p-14f) + 0x1p-14f);
-}
-
 // XCD-aware order of the (stream, block) work items of a grid: consecutive workgroup ids go to
 // the 8 XCDs in turn, so all blocks of a stream (one head of one branch) run on one XCD and
 // share its L2.  Blocks are handed out from the last (the longest causal row range) down.
@@ -119,13 +95,210 @@ __device__ __forceinline__ WorkItem xcd_order(int bid, int nstreams, int nblocks
   return w;
 }
 
-// ------------------------------------------------------------------ key_norms
-// Inverse L2 norms of the key rows of every branch.  A group of D/8 lanes reads one row (16
-// bytes per lane, whole rows per load instruction); each wave covers KN_ROWS consecutive rows
-// of one (branch, head) with all its loads issued before the first reduction.
+// Work item of the screens: key tiles [k0, k1) of one 256-row block of one stream (branch,
+// head).  A block's causal key range (key tiles 0 .. nkt - 1) is cut into chunks of screen_kc
+// tiles (whole bitmask words), so that small problems have enough items and no item is much
+// longer than the others; items are numbered per stream in (block, chunk) order and handed out
+// from the last (the longest block's).  tiles_before / per_stream: key-tile steps of the stream's
+// earlier items / of all of them (they place the item's slice of the zero range).
+struct ScreenItem {
+  int sidx, qb, chunk, nkt, k0, k1;
+  int64_t tiles_before, per_stream;
+};
+__device__ __forceinline__ ScreenItem screen_item(const FwdParams& P, int BR) {
+  const int nqt = P.nqt, qoff = P.qoff;
+  const WorkItem wi = xcd_order(blockIdx.x, BR * P.B * P.H, P.screen_items);
+  const int KC = P.screen_kc;
+  ScreenItem it{wi.stream, 0, 0, 1, 0, 1, 0, 0};
+  int t = wi.block;
+  bool found = false;
+  for (int q = 0; q < (P.Nq + 255) / 256; ++q) {
+    const int n = kt_last(min(8 * q + 7, nqt - 1), qoff, P.nkt) + 1;
+    const int c = (n + KC - 1) / KC;
+    if (!found && t < c) {
+      it.qb = q;
+      it.chunk = t;
+      it.nkt = n;
+      it.tiles_before += (int64_t)t * KC;
+      found = true;
+    } else if (!found) {
+      t -= c;
+      it.tiles_before += n;
+    }
+    it.per_stream += n;
+  }
+  it.k0 = it.chunk * KC;
+  it.k1 = min(it.k0 + KC, it.nkt);
+  return it;
+}
+
+// The item's slice of the call's zero range (the backward's gradients in training): an item
+// clears zero_per_it 16-byte units per key tile it walks, from the steps of the items before it
+// in (stream, block, chunk) order.  Buffer stores over the slice: the hardware drops those past
+// its end (a slice is below 1 MiB, so 32-bit offsets); streaming (nt): the backward reads them
+// much later.
+struct ZeroSlice {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ void init(const FwdParams& P, const ScreenItem& it) {
+    int64_t z0 = 0, zend = 0;
+    if (P.zero) {
+      z0 = ((int64_t)it.sidx * it.per_stream + it.tiles_before) * P.zero_per_it;
+      zend = min(z0 + (int64_t)(it.k1 - it.k0) * P.zero_per_it, P.zero_units);
+    }
+    r = make_rsrc(P.zero ? reinterpret_cast<u32x4*>(P.zero) + z0 : nullptr,
+                  (uint32_t)(zend > z0 ? (zend - z0) * 16 : 0));
+  }
+  template <int NTHR>
+  __device__ __forceinline__ void clear(const FwdParams& P, int step, int tid) const {
+    const uint32_t base = (uint32_t)step * (uint32_t)P.zero_per_it * 16u;
+    for (int u = tid; u < P.zero_per_it; u += NTHR)
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, r, (uint32_t)u * 16u, base, 2);
+  }
+};
+
+// Bitmask words (and, with candidate lists, the candidate keys) of one wave's query tiles after
+// key tile kt, when a 32-tile word is complete or the item ends.  hb[s]: per lane, bit kt % 32
+// set when the lane's test passed for key tile kt (lane n32 of either half: key n32 of the tile
+// when CAND, the lane's query row otherwise).  The item owns whole words of each row.
+// Candidate slots: an item that covers its block's whole key range is the lists' only producer
+// and counts in cn[s] (stored at the end, screen_counts); the items of a split block take their
+// slots with one atomic add per word on the count (zeroed by key_prep).
+template <int QPW, bool CAND>
+__device__ __forceinline__ void screen_flush(const FwdParams& P, int BR, const ScreenItem& it, int qt0,
+                                             const bool (&live)[QPW], uint32_t (&hb)[QPW], uint32_t (&cn)[QPW],
+                                             int kt) {
+  const int l = lane_id(), n32 = l & 31;
+  const int BH = P.B * P.H, nqt = P.nqt, Nk = P.Nk;
+  if (!(live[0] && ((kt & 31) == 31 || kt == it.k1 - 1))) return;
+  uint32_t* occ0 = P.occ + ((int64_t)it.sidx * nqt + qt0) * P.occ_w;
+  const int kpad = P.nkt - 1;  // the key tile that may hold padding keys
+#pragma unroll
+  for (int s = 0; s < QPW; ++s) {
+    uint32_t w = hb[s];
+    if constexpr (CAND) {
+      // a padding key (past Nk, in the last key tile) scores 0 and passes a threshold below 0
+      // (the query tile at position 0, beta <= 0): it holds no weight and must not be listed
+      if ((kt >> 5) == (kpad >> 5) && n32 >= Nk - 32 * kpad) w &= ~(1u << (kpad & 31));
+    }
+    const uint32_t hm = w | (uint32_t)__shfl_xor((int)w, 32);  // lane n32: tiles its key passed
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) w |= (uint32_t)__shfl_xor((int)w, o);
+    hb[s] = 0u;
+    if constexpr (CAND) {
+      // candidate keys of the word's tiles: per tile with a passing lane (a few per cent), the
+      // keys of its passing lanes in increasing order, appended to the query tile's list
+      const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)w);
+      if (P.cand && m0) {
+        const int64_t list = (int64_t)it.sidx * nqt + qt0 + s;
+        uint32_t* clist = P.cand + list * kCandCap;
+        uint32_t run = cn[s];
+        if (!(it.k0 == 0 && it.k1 == it.nkt)) {  // a split block: slots by atomic add
+          uint32_t total = 0u;
+          for (uint32_t m = m0; m; m &= m - 1u)
+            total += (uint32_t)__builtin_popcountll(wave_ballot(l < 32 && ((hm >> __builtin_ctz(m)) & 1u)));
+          uint32_t base = 0u;
+          if (l == 0) base = atomicAdd(P.cand + pair_lists(BR, BH, nqt) * kCandCap + list, total);
+          run = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+        }
+        for (uint32_t m = m0; m; m &= m - 1u) {
+          const int b = __builtin_ctz(m);
+          const uint32_t keys = (uint32_t)wave_ballot(l < 32 && ((hm >> b) & 1u));
+          const uint32_t slot = run + (uint32_t)__builtin_popcount(keys & ((1u << n32) - 1u));
+          if (l < 32 && ((keys >> l) & 1u) && slot < (uint32_t)kCandCap)
+            clist[slot] = (uint32_t)(32 * (32 * (kt >> 5) + b) + l);
+          run += (uint32_t)__builtin_popcount(keys);
+        }
+        cn[s] = run;
+      }
+    }
+    if (l == 0 && live[s]) {
+      uint32_t* row = occ0 + s * P.occ_w;
+      row[kt >> 5] = w;
+      if (kt == it.nkt - 1)  // words of key tiles no item of the block reaches
+        for (int x = (kt >> 5) + 1; x < P.occ_w; ++x) row[x] = 0u;
+    }
+  }
+}
+
+// The candidate counts of an item that is its lists' only producer (see screen_flush).
+template <int QPW>
+__device__ __forceinline__ void screen_counts(const FwdParams& P, int BR, const ScreenItem& it, int qt0,
+                                              const bool (&live)[QPW], const uint32_t (&cn)[QPW]) {
+  if (!P.cand || lane_id() != 0 || !(it.k0 == 0 && it.k1 == it.nkt)) return;
+  const int64_t base = pair_lists(BR, P.B * P.H, P.nqt) * kCandCap + (int64_t)it.sidx * P.nqt + qt0;
+#pragma unroll
+  for (int s = 0; s < QPW; ++s)
+    if (live[s]) P.cand[base + s] = cn[s];
+}
+
+// Causal (query tile, key tile) pairs of one wave's query tiles in the item, for the counters.
+template <int QPW>
+__device__ __forceinline__ void screen_count(const FwdParams& P, const ScreenItem& it, const bool (&live)[QPW],
+                                             const int (&ktl)[QPW]) {
+  if (!P.stats || lane_id() != 0) return;
+  unsigned visited = 0;
+#pragma unroll
+  for (int s = 0; s < QPW; ++s) visited += live[s] ? (unsigned)max(0, min(it.k1 - 1, ktl[s]) - it.k0 + 1) : 0u;
+  if (visited) atomicAdd(P.stats + 0, (unsigned long long)visited);
+}
+
+// ------------------------------------------------------------------ int8 screening bound
+// The normalised screen (fwd_screen_i8) tests int8 scores.  The exact pass keeps weight (i, j)
+// iff x_ij = fma(fl(S_ij rk_j), rq_i, -tau_i) > 0, S_ij the fp32 MFMA sum of the bf16 products
+// q_i . k_j (rq, rk: fp32 inverse row norms, the same values on both sides).  With qt = rq q_i
+// and kt = rk k_j (real), x > 0 implies
+//   qt . kt > tau_i (1 - 2^-24) - 2^-17 (1 + 2^-20)
+// (the fp32 product and fma roundings, and 128 * 2^-24 = 2^-17 of |q||k| for the accumulation).
+// The screen forms qh = fl(q rq) and kh = fl(k rk) (each within 2^-24 of qt, kt per element) and
+// quantises them: qh = sq a + rq_res with one scale sq per 32-row query tile (sq = max |qh| /
+// 127 over the tile, a = rint(qh / sq) in [-127, 127]) and kh = s_j b + rk_res per key row (s_j
+// = max |kh_j| / 127); the residuals are computed exactly (fma) and eq >= |rq_res|, ek_j >=
+// |rk_res| bound their norms (fp32 sums of squares and square roots, times 1 + 2^-12).  With
+// A_ij = a . b_j (exact int32) and |qh|, |kh| <= 1 + 2^-20:
+//   qt . kt <= sq s_j A_ij + (eq + ek_j)(1 + 2^-20) + 3 eq ek_j + 2^-22.
+// So with tmin the tile's smallest tau (tau is monotone in the position up to a relative
+// 2^-20) every kept weight passes
+//   fl(fl(float(max_i A_ij) * fl(sq s_j))) > thr_j = tmin - |tmin| 2^-19 - 2^-14
+//                                                   - eq (1 + 2^-10) - ek_j (1 + 2^-10 + 4 eq):
+// 2^-14 covers 2^-17 + 2^-22 and the fp32 roundings of the test (relative 2^-23 on values below
+// 1.02), |tmin| 2^-19 the threshold's, and the (1 + 2^-10) factors and 4 eq ek_j the rest.  On
+// N(0, 1) rows eq is about 0.009 and ek_j about 0.006 (against a bf16-residual margin of 0.002),
+// so the screen keeps about twice the candidate keys of an exact test; the exact pass drops them.
+__device__ __forceinline__ float i8_tmin(float tmin, float eq) {
+  return tmin - fabsf(tmin) * 0x1p-19f - 0x1p-14f - eq * (1.f + 0x1p-10f);
+}
+__device__ __forceinline__ float i8_ekcoef(float eq) { return 1.f + 0x1p-10f + 4.f * eq; }
+__device__ __forceinline__ float res_bound(float sumsq) { return sqrtf(sumsq) * (1.f + 0x1p-12f); }
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// Signed byte j of an int8 lane value packed 4 per int (two's complement).
+__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
+  return (a & 255) | ((b & 255) << 8) | ((c & 255) << 16) | ((d & 255) << 24);
+}
+__device__ __forceinline__ int quant(float x, float inv) {
+  return min(127, max(-127, (int)__builtin_rintf(x * inv)));
+}
+
+__device__ __forceinline__ int max16i(const i32x16& v) {
+  const int a = max(max(v[0], v[1]), v[2]), b = max(max(v[3], v[4]), v[5]), c = max(max(v[6], v[7]), v[8]);
+  const int d = max(max(v[9], v[10]), v[11]), e = max(max(v[12], v[13]), v[14]);
+  return max(max(max(a, b), max(c, d)), max(e, v[15]));
+}
+
+// ------------------------------------------------------------------ key_prep
+// Per key row of every branch: the inverse L2 norm rk_j into the norms table and, for the int8
+// screen (P.k8 set), the row kh_j = fl(k_j rk_j) quantised to int8 (P.k8, [stream][Nk][D] bytes)
+// with its scale s_j and residual bound ek_j (P.ksc, [stream][Nk] {s_j, ek_j}).  Non-finite
+// elements quantise as 0 (such a key's exact weights are 0).  A group of D/8 lanes reads one row
+// (16 bytes per lane, whole rows per load instruction); each wave covers KN_ROWS consecutive rows
+// of one (branch, head) with all its loads issued before the first reduction.  It also zeroes the
+// screen's candidate counts and the tile-pass queue count.
 constexpr int KN_GROUPS = 4;  // row groups per wave
 template <int D>
-__global__ void __launch_bounds__(256) key_norms(FwdParams P, int BR) {
+__global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
   constexpr int LPR = D / 8;        // lanes per row
   constexpr int RPG = 64 / LPR;     // rows per load instruction
   constexpr int ROWS = RPG * KN_GROUPS;
@@ -133,6 +306,12 @@ __global__ void __launch_bounds__(256) key_norms(FwdParams P, int BR) {
   const int BH = P.B * P.H, N = P.Nk;     // key rows
   const int wpr = (N + ROWS - 1) / ROWS;  // waves per (branch, head)
   const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (P.cand) {  // the screen's candidate counts (it appends with atomic adds) and the queue count
+    const int64_t lists = pair_lists(BR, BH, P.nqt), nthr = (int64_t)gridDim.x * 256;
+    uint32_t* counts = P.cand + lists * kCandCap;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < lists; i += nthr) counts[i] = 0u;
+    if (blockIdx.x == 0 && threadIdx.x == 0) P.pvq[0] = 0u;
+  }
   if (wid >= (int64_t)BR * BH * wpr) return;  // whole wave, no barriers
   const int sidx = (int)(wid / wpr), br = sidx / BH, bh = sidx % BH;
   const int t0 = (int)(wid % wpr) * ROWS + l / LPR;
@@ -152,26 +331,48 @@ __global__ void __launch_bounds__(256) key_norms(FwdParams P, int BR) {
 #pragma unroll
     for (int o = LPR / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
     const int t = t0 + RPG * u;
-    if (sub == 0 && t < N) out[t] = inv_norm(ss);
+    const float rk = inv_norm(ss);
+    if (sub == 0 && t < N) out[t] = rk;
+    if (P.k8) {
+      float kh[8], m = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = (float)x[u][j] * rk;
+        kh[j] = __builtin_isfinite(v) ? v : 0.f;
+        m = fmaxf(m, fabsf(kh[j]));
+      }
+#pragma unroll
+      for (int o = LPR / 2; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+      const float sc = m * (1.f / 127.f), inv = m > 0.f ? 127.f / m : 0.f;
+      int b[8];
+      float e2 = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        b[j] = quant(kh[j], inv);
+        const float r = __builtin_fmaf(-sc, (float)b[j], kh[j]);
+        e2 = __builtin_fmaf(r, r, e2);
+      }
+#pragma unroll
+      for (int o = LPR / 2; o >= 1; o >>= 1) e2 += __shfl_xor(e2, o);
+      if (t < N) {
+        int8_t* krow = P.k8 + ((int64_t)sidx * N + t) * D;
+        *reinterpret_cast<i32x2*>(krow + 8 * sub) = i32x2{pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7])};
+        if (sub == 0) *reinterpret_cast<float2*>(P.ksc + 2 * ((int64_t)sidx * N + t)) = float2{sc, res_bound(e2)};
+      }
+    }
   }
 }
 
-// ------------------------------------------------------------------ fwd_screen
-// Workgroup = 256 query rows of one branch of one head, QPW 32-row query tiles per wave
-// (8 / QPW waves); grid = branches x heads x ceil(N / 256).  Key tiles stream through LDS in
-// groups of TPB tiles ("super-stages", two of them in a ring): buffer loads into VGPRs one
-// iteration ahead, LDS writes of the next group while the current one is read, one barrier per
-// group.
-// Without normalisation, score tiles are computed transposed, S^T = K Q^T: each lane holds one
-// query i and 16 of its keys, so "max_j s_ij > tau_i" is the exact test with one compare per
-// lane.  With normalisation the weight test is s_ij rk_j rq_i > tau_i; the queries enter
-// pre-scaled, qh_i = bf16(q_i rq_i), and the tile is computed as S = Qh K^T, so each lane holds
-// one key j (and 16 queries): the per-lane test "max_i sh_ij * rk_j > tlo" needs one multiply
-// per lane instead of one per score, with tlo = the tile's smallest tau minus screen_margin.
-// Dispatch uses QPW = 2 (three waves per SIMD) and TPB = 1: one query tile per wave (twice the
-// LDS fragment reads per MFMA) and larger groups (fewer waves) both measured slower at the
-// headline shape.
-template <int D, bool NORM, int QPW, int TPB>
+// ------------------------------------------------------------------ fwd_screen (unnormalised)
+// The exact screen of dot-product scores.  Workgroup = one work item (ScreenItem): 256 query rows
+// of one branch of one head against key tiles [k0, k1), QPW 32-row query tiles per wave (8 / QPW
+// waves).  Key tiles stream through LDS in groups of TPB tiles ("super-stages", two of them in a
+// ring): buffer loads into VGPRs one iteration ahead, LDS writes of the next group while the
+// current one is read, one barrier per group.  Score tiles are computed transposed, S^T = K Q^T:
+// each lane holds one query i and 16 of its keys, so "max_j s_ij > tau_i" is the exact test with
+// one compare per lane (the exact pass computes the same scores with the same MFMA sequence).
+// Dispatch uses QPW = 2 (three waves per SIMD) and TPB = 1.
+template <int D, int QPW, int TPB>
 __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) {
   constexpr int NT = D / 16;                // MFMA steps over d
   constexpr int KS = D + 8;                 // LDS row stride (elements): conflict-free fragment reads
@@ -180,21 +381,18 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
   constexpr int TPR = CPR < NTHR / 32 ? CPR : NTHR / 32;  // staging threads per row
   constexpr int CPT = CPR / TPR;            // chunks per staging thread
   __shared__ __attribute__((aligned(16))) bf16 kst[2 * TPB][32 * KS];
-  __shared__ __attribute__((aligned(16))) float krk[2 * TPB][32];  // inverse key norms of each tile
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5, tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
-  if (NORM && P.pvq && blockIdx.x == 0 && tid == 0) P.pvq[0] = 0u;  // the candidate pass fills it
-  const WorkItem wi = xcd_order(blockIdx.x, BR * BH, (Nq + 255) / 256);
-  const int sidx = wi.stream, qb = wi.block;
-  const int br = sidx / BH, bh = sidx % BH;
+  const ScreenItem it = screen_item(P, BR);
+  const int k0 = it.k0, k1 = it.k1;
+  const int br = it.sidx / BH, bh = it.sidx % BH;
   const int b = bh / P.H, h = bh % P.H;
   const int qslot = br ? F_Q2 : F_Q1, kslot = br ? F_K2 : F_K1;
-  const int q0w = qb * 256 + 32 * QPW * wv;  // first row of this wave
-  const int qt0 = q0w >> 5;                  // this wave's query tiles: qt0 .. qt0 + QPW - 1
-  const int nkt = kt_last(min(8 * qb + 7, nqt - 1), qoff, P.nkt) + 1;  // key tiles of the workgroup
-  const int nit = (nkt + TPB - 1) / TPB;
+  const int q0w = it.qb * 256 + 32 * QPW * wv;  // first row of this wave
+  const int qt0 = q0w >> 5;                     // this wave's query tiles: qt0 .. qt0 + QPW - 1
+  const int nit = (k1 - k0 + TPB - 1) / TPB;
   bool live[QPW];
   int ktl[QPW];  // last key tile each query tile sees
 #pragma unroll
@@ -209,45 +407,37 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
   const int srow = tid / TPR, sch = tid % TPR;
   const bool stager = tid < 32 * TPR;
   const uint32_t soff = (uint32_t)((srow * sk + 8 * sch) * 2);
-  // key norms: threads 0..7 stage four rows each (rows past N read as 0, never used)
-  const __amdgpu_buffer_rsrc_t rnorm =
-      make_rsrc(NORM ? P.norms + norm_base(P, br ? N_K2 : N_K1, bh) : nullptr, NORM ? (uint32_t)Nk * 4 : 0u);
-  u32x4 R[TPB][CPT], RN[TPB];
-  auto fetch = [&](int it) {  // tiles of group it into registers
+  u32x4 R[TPB][CPT];
+  auto fetch = [&](int i) {  // tiles of group i into registers
 #pragma unroll
     for (int j = 0; j < TPB; ++j) {
-      const int kt = TPB * it + j;
-      if (kt >= nkt) break;
+      const int kt = k0 + TPB * i + j;
+      if (kt >= k1) break;
       if (stager) {
-        const __amdgpu_buffer_rsrc_t rs = tile_rsrc<D>(khead, sk, kt, Nk);
+        const __amdgpu_buffer_rsrc_t rs = tile_rsrc<D>(khead, sk, kt, Nk);  // rows past Nk read 0
 #pragma unroll
         for (int c = 0; c < CPT; ++c) R[j][c] = buf_load16(rs, soff + 16 * TPR * c);
       }
-      if constexpr (NORM)
-        if (tid < 8) RN[j] = buf_load16(rnorm, (uint32_t)(32 * kt + 4 * tid) * 4);
     }
   };
-  auto commit = [&](int it) {  // group it into its super-stage
+  auto commit = [&](int i) {  // group i into its super-stage
 #pragma unroll
     for (int j = 0; j < TPB; ++j) {
-      const int kt = TPB * it + j;
-      if (kt >= nkt) break;
-      const int st = TPB * (it & 1) + j;
+      const int kt = k0 + TPB * i + j;
+      if (kt >= k1) break;
       if (stager) {
-        bf16* k = &kst[st][srow * KS + 8 * sch];
+        bf16* k = &kst[TPB * (i & 1) + j][srow * KS + 8 * sch];
 #pragma unroll
         for (int c = 0; c < CPT; ++c) *reinterpret_cast<u32x4*>(k + 8 * TPR * c) = R[j][c];
       }
-      if constexpr (NORM)
-        if (tid < 8) *reinterpret_cast<u32x4*>(&krk[st][4 * tid]) = RN[j];
     }
   };
 
-  // ---- resident query fragments, inverse norms, thresholds
+  // ---- resident query fragments and thresholds
   const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
   const float beta = *P.beta;
   bf16x8 Q[QPW][NT];
-  float tau[QPW];  // without normalisation tau_i of the lane's query; with it the tile's tlo
+  float tau[QPW];  // tau_i of the lane's query
   bool valid[QPW];
 #pragma unroll
   for (int s = 0; s < QPW; ++s) {
@@ -256,67 +446,12 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     const bf16* row = qhead + (int64_t)min(iq, Nq - 1) * P.s[qslot][2];  // rows >= Nq: never vote
 #pragma unroll
     for (int t = 0; t < NT; ++t) Q[s][t] = *reinterpret_cast<const bf16x8*>(row + 16 * t + 8 * g);
-    if constexpr (NORM) {
-      const float rq = inv_norm(row_sumsq<PolBF16, NT>(Q[s]));
-      if (g == 0 && valid[s]) P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + iq] = rq;
-      // rows past Nq score 0; so do non-finite elements (NaN/Inf inputs), whose exact weights
-      // are 0 (x > 0 fails on NaN), so a NaN score can only come from a non-finite key row:
-      // it poisons the maximum of that key's lane alone, whose weights are 0 as well
-      const float sc = valid[s] ? rq : 0.f;
-      float r2 = 0.f;  // squared norm of the row's bf16 rounding residual (this lane's half)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float x0 = (float)Q[s][t][j] * sc;
-          const float x = __builtin_isfinite(x0) ? x0 : 0.f;
-          const bf16 xb = (bf16)x;
-          const float r = (float)xb - x;  // exact: xb and x are within a factor of two
-          r2 = __builtin_fmaf(r, r, r2);
-          Q[s][t][j] = xb;
-        }
-      r2 += __shfl_xor(r2, 32);
-#pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) r2 = fmaxf(r2, __shfl_xor(r2, o));  // largest of the tile
-      // tau is monotone in the position: its smallest value over the tile's rows is at one of
-      // the ends
-      const int i0 = q0w + 32 * s, i1 = max(i0, min(i0 + 31, Nq - 1));
-      tau[s] = screen_tlo(fminf(beta * tau_coeff(qoff + i0, P.inv_d), beta * tau_coeff(qoff + i1, P.inv_d)),
-                          sqrtf(r2));
-    } else {
-      tau[s] = beta * tau_coeff(qoff + iq, P.inv_d);
-    }
+    tau[s] = beta * tau_coeff(qoff + iq, P.inv_d);
   }
+  ZeroSlice zs;
+  zs.init(P, it);
 
-  // ---- the call's zero range (the backward's gradients in training), spread over the steps of
-  // every workgroup: workgroup (stream, block) clears zero_per_it units per key tile it walks,
-  // from the sum of the steps of the workgroups before it in (stream, block) order
-  int64_t z0 = 0, zend = 0;
-  if (P.zero) {
-    int64_t before = 0, per_stream = 0;
-    for (int q = 0; q < (Nq + 255) / 256; ++q) {
-      const int n = kt_last(min(8 * q + 7, nqt - 1), qoff, P.nkt) + 1;
-      before += q < qb ? n : 0;
-      per_stream += n;
-    }
-    z0 = ((int64_t)sidx * per_stream + before) * P.zero_per_it;
-    zend = min(z0 + (int64_t)nkt * P.zero_per_it, P.zero_units);
-  }
-  // buffer stores over the workgroup's slice: the hardware drops those past its end (a slice
-  // is below 1 MiB, so 32-bit offsets); streaming (nt): the backward reads them much later
-  const __amdgpu_buffer_rsrc_t rzero =
-      make_rsrc(P.zero ? reinterpret_cast<u32x4*>(P.zero) + z0 : nullptr, (uint32_t)(zend > z0 ? (zend - z0) * 16 : 0));
-  auto clear = [&](int kt) {
-    const uint32_t step = (uint32_t)kt * (uint32_t)P.zero_per_it * 16u;
-    for (int u = tid; u < P.zero_per_it; u += NTHR)
-      __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rzero, (uint32_t)u * 16u, step, 2);
-  };
-
-  uint32_t* occ0 = P.occ + ((int64_t)sidx * nqt + qt0) * P.occ_w;  // bitmask row of qt0 (then qt0 + 1)
-  // Per lane and query tile: bit kt % 32 set when the lane's test passed for key tile kt.  The
-  // wave ORs them when a 32-tile word is complete (cheaper than a ballot per tile).
-  uint32_t hb[QPW];
-  uint32_t cn[QPW];  // candidate keys met per query tile (may pass the cap)
+  uint32_t hb[QPW], cn[QPW];  // hit bits; candidate keys met per query tile (may pass the cap)
 #pragma unroll
   for (int s = 0; s < QPW; ++s) hb[s] = cn[s] = 0u;
   const int koff = n32 * KS + 8 * g;
@@ -331,79 +466,25 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
       fk[t] = *reinterpret_cast<const bf16x8*>(kp + 16 * t);
       __builtin_amdgcn_sched_barrier(0);
     }
-    float rk = 1.f;
-    if constexpr (NORM) rk = krk[st][n32];  // the lane's key (0 past N)
-    __builtin_amdgcn_sched_barrier(0);  // all fragment reads in flight before the first MFMA
     f32x16 S[QPW];
 #pragma unroll
     for (int s = 0; s < QPW; ++s) S[s] = f32x16{};
     // One query tile's chain at a time: dependent MFMAs back to back on the same accumulator
-    // take the accumulate fast path; alternating two VGPR accumulators measured ~20 % slower.
+    // take the accumulate fast path.
 #pragma unroll
     for (int s = 0; s < QPW; ++s) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        if constexpr (NORM) S[s] = PolBF16::mma(Q[s][t], fk[t], S[s]);  // S = Qh K^T
-        else S[s] = PolBF16::mma(fk[t], Q[s][t], S[s]);                 // S^T = K Q^T
-      }
+      for (int t = 0; t < NT; ++t) S[s] = PolBF16::mma(fk[t], Q[s][t], S[s]);  // S^T = K Q^T
       __builtin_amdgcn_sched_barrier(0);  // keep the chains apart
     }
     const uint32_t bit = 1u << (kt & 31);
     // Both tests run on every path, masked by selects: the MFMA results are read only in
     // straight-line code after the chains, where the compiler counts the wait states the
-    // hardware needs between an MFMA writing a register and a VALU reading it.  (With a branch
-    // skipping the first test, the compiler placed the second test's reads too early on the
-    // branch path: 7 wait states where 12 are needed, so the test could read scores that were
-    // not yet written.)
+    // hardware needs between an MFMA writing a register and a VALU reading it.
 #pragma unroll
     for (int s = 0; s < QPW; ++s) {
-      bool hit;
-      if constexpr (NORM) hit = maximum16(S[s]) * rk > tau[s];  // largest score of the lane's key
-      else hit = valid[s] && max16(S[s]) > tau[s];          // largest score of the lane's query
-      // key tiles after the query tile's last position hold no causal pair; a query tile past
-      // the last row (the wave's second, at the end of the sequence) has no list
-      const bool lh = live[s] && hit && kt <= ktl[s];
-      hb[s] |= lh ? bit : 0u;
-    }
-  };
-  // bitmask words of this wave's rows: word kt/32 is complete after key tile kt
-  const int kpad = P.nkt - 1;  // the key tile that may hold padding keys
-  auto flush = [&](int kt) {
-    if (live[0] && ((kt & 31) == 31 || kt == nkt - 1)) {
-#pragma unroll
-      for (int s = 0; s < QPW; ++s) {
-        uint32_t w = hb[s];
-        if constexpr (NORM) {
-          // a padding key (past Nk, in the last key tile) scores 0 and passes a threshold below 0
-          // (the query tile at position 0, beta <= 0): it holds no weight and must not be listed
-          if ((kt >> 5) == (kpad >> 5) && n32 >= Nk - 32 * kpad) w &= ~(1u << (kpad & 31));
-        }
-        const uint32_t hm = w | (uint32_t)__shfl_xor((int)w, 32);  // lane n32: tiles its key passed
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) w |= (uint32_t)__shfl_xor((int)w, o);
-        hb[s] = 0u;
-        if constexpr (NORM) {
-          // candidate keys of the word's tiles: per tile with a passing lane (a few per cent),
-          // the keys of its passing lanes in increasing order, appended to the query tile's list
-          if (P.cand) {
-            uint32_t* clist = P.cand + ((int64_t)sidx * nqt + qt0 + s) * kCandCap;
-            for (uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)w); m; m &= m - 1u) {
-              const int b = __builtin_ctz(m);
-              const uint32_t keys = (uint32_t)wave_ballot(l < 32 && ((hm >> b) & 1u));
-              const uint32_t slot = cn[s] + (uint32_t)__builtin_popcount(keys & ((1u << n32) - 1u));
-              if (l < 32 && ((keys >> l) & 1u) && slot < (uint32_t)kCandCap)
-                clist[slot] = (uint32_t)(32 * (32 * (kt >> 5) + b) + l);
-              cn[s] += (uint32_t)__builtin_popcount(keys);
-            }
-          }
-        }
-        if (l == 0 && live[s]) {
-          uint32_t* row = occ0 + s * P.occ_w;
-          row[kt >> 5] = w;
-          if (kt == nkt - 1)  // words of key tiles this workgroup never reaches
-            for (int x = (kt >> 5) + 1; x < P.occ_w; ++x) row[x] = 0u;
-        }
-      }
+      const bool hit = valid[s] && max16(S[s]) > tau[s];  // largest score of the lane's query
+      hb[s] |= live[s] && hit && kt <= ktl[s] ? bit : 0u;
     }
   };
 
@@ -411,32 +492,223 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
   commit(0);
   if (nit > 1) fetch(1);
   __syncthreads();
-  for (int it = 0; it < nit; ++it) {
+  for (int i = 0; i < nit; ++i) {
 #pragma unroll
     for (int j = 0; j < TPB; ++j) {
-      const int kt = TPB * it + j;
-      if (kt >= nkt) break;
-      if (P.zero) clear(kt);
-      process(kt, TPB * (it & 1) + j);
-      flush(kt);
+      const int kt = k0 + TPB * i + j;
+      if (kt >= k1) break;
+      if (P.zero) zs.clear<NTHR>(P, kt - k0, tid);
+      process(kt, TPB * (i & 1) + j);
+      screen_flush<QPW, false>(P, BR, it, qt0, live, hb, cn, kt);
     }
     // the other super-stage was last read before the previous barrier
-    if (it + 1 < nit) commit(it + 1);
-    if (it + 2 < nit) fetch(it + 2);
+    if (i + 1 < nit) commit(i + 1);
+    if (i + 2 < nit) fetch(i + 2);
     __syncthreads();
   }
-  if (NORM && P.cand && l == 0) {
+  screen_count<QPW>(P, it, live, ktl);
+}
+
+// ------------------------------------------------------------------ fwd_screen_i8 (normalised)
+// The normalised screen on int8 matrix cores (v_mfma_i32_32x32x32_i8, twice the bf16 rate, half
+// the operand bytes).  Workgroup = one work item (as fwd_screen), four waves of two 32-row query
+// tiles.  Per wave the query rows are normalised (their inverse norms rq go to the norms table),
+// quantised to int8 with one scale per query tile and held as A fragments; the int8 key tiles of
+// key_prep (32 x D bytes, contiguous) and their {s_j, ek_j} stream through a two-stage LDS ring
+// (buffer loads into VGPRs one iteration ahead, rows past Nk read 0, one barrier per tile).  The
+// tile is S = A B^T: each lane holds one key j and 16 query rows, and the test (the int8 bound
+// above) is "float(max_i A_ij) * (sq s_j) > thr_j", a few operations per lane and query tile.
+// Hit bits give the bitmask words and the candidate keys (screen_flush).
+template <int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) fwd_screen_i8(FwdParams P, int BR) {
+  constexpr int QPW = 2, NTHR = 256;
+  constexpr int NK = D / 32;                // int8 MFMA steps over d
+  constexpr int KS8 = D + 16;               // LDS row stride (bytes): conflict-free fragment reads
+  constexpr int CPR = D / 16;               // 16-byte chunks per int8 key row
+  constexpr int STAGERS = 32 * CPR;         // threads loading a tile, one chunk each
+  __shared__ __attribute__((aligned(16))) int8_t kst[2][32 * KS8];
+  __shared__ __attribute__((aligned(16))) float2 ksc[2][32];  // {s_j, ek_j} of each tile's keys
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5, tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
+  const ScreenItem it = screen_item(P, BR);
+  const int k0 = it.k0, k1 = it.k1, nit = k1 - k0;
+  const int br = it.sidx / BH, bh = it.sidx % BH;
+  const int b = bh / P.H, h = bh % P.H;
+  const int qslot = br ? F_Q2 : F_Q1;
+  const int q0w = it.qb * 256 + 32 * QPW * wv;  // first row of this wave
+  const int qt0 = q0w >> 5;                     // this wave's query tiles: qt0, qt0 + 1
+  bool live[QPW];
+  int ktl[QPW];  // last key tile each query tile sees
 #pragma unroll
-    for (int s = 0; s < QPW; ++s)
-      if (live[s]) P.cand[pair_lists(BR, BH, nqt) * kCandCap + (int64_t)sidx * nqt + qt0 + s] = cn[s];
+  for (int s = 0; s < QPW; ++s) {
+    live[s] = qt0 + s < nqt;
+    ktl[s] = kt_last(qt0 + s, qoff, P.nkt);
   }
-  if (P.stats && l == 0) {
-    // causal (query tile, key tile) pairs of this wave: key tiles 0 .. qt of each live query tile
-    unsigned visited = 0;
+
+  // ---- staging: tile kt is the stream's int8 key rows 32 kt .. 32 kt + 31 (contiguous, D bytes
+  // each) and their {s_j, ek_j}; rows past Nk read 0
+  const int8_t* k8head = P.k8 + (int64_t)it.sidx * Nk * D;
+  const float* schead = P.ksc + 2 * (int64_t)it.sidx * Nk;
+  const bool stager = tid < STAGERS;
+  const int srow = tid / CPR, sch = tid % CPR;
+  u32x4 R = {}, RS = {};
+  auto fetch = [&](int i) {
+    const int kt = k0 + i;
+    if (kt >= k1) return;
+    const uint32_t rows = (uint32_t)min(32, Nk - 32 * kt);
+    if (stager) R = buf_load16(make_rsrc(k8head + (int64_t)(32 * kt) * D, rows * D), (uint32_t)(16 * tid));
+    if (tid < 16) RS = buf_load16(make_rsrc(schead + (int64_t)(64 * kt), rows * 8), (uint32_t)(16 * tid));
+  };
+  auto commit = [&](int i) {
+    const int kt = k0 + i;
+    if (kt >= k1) return;
+    if (stager) *reinterpret_cast<u32x4*>(&kst[i & 1][srow * KS8 + 16 * sch]) = R;
+    if (tid < 16) *reinterpret_cast<u32x4*>(&ksc[i & 1][2 * tid]) = RS;
+  };
+
+  // ---- resident int8 query fragments and the per-tile constants of the test
+  const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
+  const float beta = *P.beta;
+  i32x4 A8[QPW][NK];
+  float sq[QPW], tq[QPW], cq[QPW];  // scale, thr part of the tile, coefficient of ek_j
 #pragma unroll
-    for (int s = 0; s < QPW; ++s) visited += live[s] ? (unsigned)(ktl[s] + 1) : 0u;
-    if (visited) atomicAdd(P.stats + 0, (unsigned long long)visited);
+  for (int s = 0; s < QPW; ++s) {
+    const int iq = q0w + 32 * s + n32;
+    const bool valid = iq < Nq;
+    const bf16* row = qhead + (int64_t)min(iq, Nq - 1) * P.s[qslot][2];  // rows >= Nq: never vote
+    bf16x8 qv[NK][2];  // lane (m, g): elements 32 t + 16 g .. + 16 of row m
+#pragma unroll
+    for (int t = 0; t < NK; ++t) {
+      qv[t][0] = *reinterpret_cast<const bf16x8*>(row + 32 * t + 16 * g);
+      qv[t][1] = *reinterpret_cast<const bf16x8*>(row + 32 * t + 16 * g + 8);
+    }
+    // the row's sum of squares, and the largest finite |q| from the raw bits (magnitude bits of a
+    // finite bf16 order like its value)
+    float ss = 0.f;
+    uint32_t mb = 0u;
+#pragma unroll
+    for (int t = 0; t < NK; ++t)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        ss += PolBF16::sumsq(qv[t][c]);
+        const u32x4 w = __builtin_bit_cast(u32x4, qv[t][c]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t lo = w[k] & 0x7fffu, hi = (w[k] >> 16) & 0x7fffu;
+          mb = max(mb, (lo & 0x7f80u) != 0x7f80u ? lo : 0u);
+          mb = max(mb, (hi & 0x7f80u) != 0x7f80u ? hi : 0u);
+        }
+      }
+    float mq = __builtin_bit_cast(float, mb << 16);
+    // the row values are converted again below, not kept as fp32 (register pressure)
+#pragma unroll
+    for (int t = 0; t < NK; ++t)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        u32x4 w = __builtin_bit_cast(u32x4, qv[t][c]);
+        asm volatile("" : "+v"(w));
+        qv[t][c] = __builtin_bit_cast(bf16x8, w);
+      }
+    const float rq = inv_norm(ss + __shfl_xor(ss, 32));
+    if (g == 0 && valid && it.chunk == 0) P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + iq] = rq;
+    const float sc = valid ? rq : 0.f;
+    // the scale, one per query tile: sq = m / 127 with m the tile's largest |qh| = max over its
+    // rows of rq_i max |q_i| (any m works: the residuals are taken against the sq the test uses,
+    // and rint past +-127 is clamped)
+    mq = fmaxf(mq, __shfl_xor(mq, 32));  // the row's largest |q|
+    float m = mq * sc;
+    m = __builtin_isfinite(m) ? m : 0.f;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));  // over the tile's rows
+    sq[s] = m * (1.f / 127.f);
+    const float inv = m > 0.f ? 127.f / m : 0.f;
+    float r2 = 0.f;  // squared norm of the row's quantisation residual (this lane's half)
+#pragma unroll
+    for (int t = 0; t < NK; ++t) {
+      int w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        int a[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 4 * u + e;
+          const float x0 = (float)qv[t][j >> 3][j & 7] * sc;
+          const float x = __builtin_isfinite(x0) ? x0 : 0.f;
+          a[e] = quant(x, inv);
+          const float r = __builtin_fmaf(-sq[s], (float)a[e], x);
+          r2 = __builtin_fmaf(r, r, r2);
+        }
+        w[u] = pack4(a[0], a[1], a[2], a[3]);
+      }
+      A8[s][t] = i32x4{w[0], w[1], w[2], w[3]};
+      __builtin_amdgcn_sched_barrier(0);  // one step's values live at a time
+    }
+    r2 += __shfl_xor(r2, 32);
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) r2 = fmaxf(r2, __shfl_xor(r2, o));  // largest row of the tile
+    const float eq = res_bound(r2);
+    // tau is monotone in the position: its smallest value over the tile's rows is at one end
+    const int i0 = q0w + 32 * s, i1 = max(i0, min(i0 + 31, Nq - 1));
+    tq[s] = i8_tmin(fminf(beta * tau_coeff(qoff + i0, P.inv_d), beta * tau_coeff(qoff + i1, P.inv_d)), eq);
+    cq[s] = i8_ekcoef(eq);
+    __builtin_amdgcn_sched_barrier(0);  // one query tile's rows live at a time
   }
+  ZeroSlice zs;
+  zs.init(P, it);
+
+  uint32_t hb[QPW], cn[QPW];  // hit bits; candidate keys met per query tile (may pass the cap)
+#pragma unroll
+  for (int s = 0; s < QPW; ++s) hb[s] = cn[s] = 0u;
+  const int koff = n32 * KS8 + 16 * g;
+
+  auto process = [&](int kt, int st) {
+    if (!(live[0] && kt <= ktl[QPW - 1])) return;
+    const int8_t* kp = &kst[st][koff];
+    i32x4 fk[NK];
+#pragma unroll
+    for (int t = 0; t < NK; ++t) {  // in MFMA order
+      fk[t] = *reinterpret_cast<const i32x4*>(kp + 32 * t);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const float2 kq = ksc[st][n32];  // the lane's key: {s_j, ek_j} (0 past Nk)
+    __builtin_amdgcn_sched_barrier(0);
+    i32x16 S[QPW];
+#pragma unroll
+    for (int s = 0; s < QPW; ++s) S[s] = i32x16{};
+#pragma unroll
+    for (int s = 0; s < QPW; ++s) {
+#pragma unroll
+      for (int t = 0; t < NK; ++t) S[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A8[s][t], fk[t], S[s], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);  // keep the chains apart
+    }
+    const uint32_t bit = 1u << (kt & 31);
+    // straight-line tests on every path (see fwd_screen)
+#pragma unroll
+    for (int s = 0; s < QPW; ++s) {
+      const float thr = __builtin_fmaf(-kq.y, cq[s], tq[s]);
+      const bool hit = (float)max16i(S[s]) * (sq[s] * kq.x) > thr;
+      hb[s] |= live[s] && hit && kt <= ktl[s] ? bit : 0u;
+    }
+  };
+
+  fetch(0);
+  commit(0);
+  if (nit > 1) fetch(1);
+  __syncthreads();
+  for (int i = 0; i < nit; ++i) {
+    const int kt = k0 + i;
+    if (P.zero) zs.clear<NTHR>(P, i, tid);
+    process(kt, i & 1);
+    screen_flush<QPW, true>(P, BR, it, qt0, live, hb, cn, kt);
+    // the other stage was last read before the previous barrier
+    if (i + 1 < nit) commit(i + 1);
+    if (i + 2 < nit) fetch(i + 2);
+    __syncthreads();
+  }
+  screen_counts<QPW>(P, BR, it, qt0, live, cn);
+  screen_count<QPW>(P, it, live, ktl);
 }
 
 // ------------------------------------------------------------------ fwd_pv
@@ -720,13 +992,28 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
   uint32_t nc[BR];
 #pragma unroll
   for (int br = 0; br < BR; ++br) nc[br] = counts[((int64_t)br * BH + bh) * nqt + qt];
-  const int kraw = (int)P.cand[(((int64_t)(BR == 2 ? (l >> 5) : 0) * BH + bh) * nqt + qt) * kCandCap + (l & 31)];
+  int kraw = (int)P.cand[(((int64_t)(BR == 2 ? (l >> 5) : 0) * BH + bh) * nqt + qt) * kCandCap + (l & 31)];
   bool fit = true;
 #pragma unroll
   for (int br = 0; br < BR; ++br) fit = fit && nc[br] <= (uint32_t)kCandCap;
   if (!fit) {  // fwd_pv walks the bitmask tiles
     if (l == 0) P.pvq[1 + atomicAdd(P.pvq, 1u)] = (uint32_t)(bh * nqt + qt);
     return;
+  }
+  if (P.screen_items > (Nq + 255) / 256) {
+    // the screen split some key ranges over several items, which append in any order: sort each
+    // list (lanes 0-31: branch 0, lanes 32-63: branch 1; its keys are distinct) by rank
+    const int half = BR == 2 ? (l >> 5) : 0;
+    const uint32_t nh = nc[BR == 2 ? half : 0];
+    int rank = l & 31;
+    if ((uint32_t)(l & 31) < nh) {
+      rank = 0;
+      for (int f = 0; f < 32; ++f) {
+        const int a = __builtin_amdgcn_readlane(kraw, f), c = __builtin_amdgcn_readlane(kraw, 32 + f);
+        rank += ((uint32_t)f < nh && (half ? c : a) < kraw) ? 1 : 0;
+      }
+    }
+    kraw = __builtin_amdgcn_ds_permute(4 * ((l & 32) + rank), kraw);
   }
 
   const int b = bh / P.H, h = bh % P.H;
@@ -897,12 +1184,16 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   if constexpr (NORM) {
     constexpr int rows = (64 / (D / 8)) * KN_GROUPS;  // rows per wave
     const int64_t waves = (int64_t)BR * BH * ((p.Nk + rows - 1) / rows);
-    hipLaunchKernelGGL(key_norms<D>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, BR);
-    launched(s, "key_norms");
+    hipLaunchKernelGGL(key_prep<D>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, BR);
+    launched(s, "key_prep");
   }
-  const unsigned nqb = (unsigned)((p.Nq + 255) / 256);
-  constexpr int QPW = 2, TPB = 1;
-  hipLaunchKernelGGL((fwd_screen<D, NORM, QPW, TPB>), dim3((unsigned)(BR * BH) * nqb), dim3(512 / QPW), 0, s, p, BR);
+  const dim3 grid((unsigned)(BR * BH) * (unsigned)p.screen_items);
+  if constexpr (NORM) {
+    hipLaunchKernelGGL(fwd_screen_i8<D>, grid, dim3(256), 0, s, p, BR);
+  } else {
+    constexpr int QPW = 2, TPB = 1;
+    hipLaunchKernelGGL((fwd_screen<D, QPW, TPB>), grid, dim3(512 / QPW), 0, s, p, BR);
+  }
   launched(s, "fwd_screen");
   if (NORM && p.cand) {
     hipLaunchKernelGGL((fwd_pv_cand<D, BR, PK>), dim3((unsigned)(BH * p.nqt)), dim3(64), 0, s, p);

@@ -91,10 +91,21 @@ int64_t fwd_cand_bytes(int64_t bh, int64_t seq_len, int64_t branches) {
   return fwd_cand_list_bytes(bh, seq_len, branches) +
          round256((64 + bh * ceil_div(seq_len, 32)) * (int64_t)sizeof(uint32_t));
 }
-int64_t fwd_ws_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t branches) {
-  return fwd_occ_bytes(bh, seq_len, seq_len_kv, branches) + fwd_part_bytes(bh, seq_len, seq_len_kv) +
-         fwd_cand_bytes(bh, seq_len, branches);
+// ... and, for the int8 screen (bf16 with normalisation, more than one query tile), the
+// quantised key rows (kd bytes each, kd = head_dim) and their {scale, residual bound}.
+int64_t fwd_k8_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t branches, int64_t kd) {
+  if (seq_len <= 32 || kd == 0) return 0;
+  return round256(branches * bh * seq_len_kv * kd) + round256(branches * bh * seq_len_kv * 8);
 }
+int64_t fwd_ws_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t branches, int64_t kd) {
+  return fwd_occ_bytes(bh, seq_len, seq_len_kv, branches) + fwd_part_bytes(bh, seq_len, seq_len_kv) +
+         fwd_cand_bytes(bh, seq_len, branches) + fwd_k8_bytes(bh, seq_len, seq_len_kv, branches, kd);
+}
+// Row bytes of the int8 keys a call needs (0: it uses none).
+int64_t k8_row_bytes(const tda_fwd_args& a) {
+  return a.dtype == TDA_DTYPE_BF16 && a.normalize ? a.head_dim : 0;
+}
+constexpr int64_t kMaxHeadDim = 128;  // the size functions without head_dim assume the largest
 bool size_args_ok(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv, int32_t branches) {
   return batch >= 1 && heads >= 1 && seq_len >= 1 && seq_len_kv >= 1 && (branches == 1 || branches == 2);
 }
@@ -166,7 +177,13 @@ size_t tda_norms_floats_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_
 size_t tda_fwd_workspace_bytes_kv(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv,
                                   int32_t branches) {
   if (!size_args_ok(batch, heads, seq_len, seq_len_kv, branches)) return 0;
-  return (size_t)fwd_ws_bytes(batch * heads, seq_len, seq_len_kv, branches);
+  return (size_t)fwd_ws_bytes(batch * heads, seq_len, seq_len_kv, branches, kMaxHeadDim);
+}
+
+size_t tda_fwd_workspace_bytes_for(const tda_fwd_args* a) {
+  if (!a || check_common(common_of(*a)) != TDA_OK) return 0;
+  const Common c = common_of(*a);
+  return (size_t)fwd_ws_bytes(a->batch * a->heads, a->seq_len, c.seq_len_kv, a->branches, k8_row_bytes(*a));
 }
 
 size_t tda_pair_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches) {
@@ -206,10 +223,7 @@ int32_t tda_validate_fwd(const tda_fwd_args* a) {
   for (int k = 0; k < n; ++k)
     if ((rc = check_tensor(*ts[k], eb))) return rc;
   if (a->normalize && !a->norms) return TDA_ERR_NORMS;
-  const Common c = common_of(*a);
-  if (!a->workspace ||
-      a->workspace_bytes < tda_fwd_workspace_bytes_kv(a->batch, a->heads, a->seq_len, c.seq_len_kv, a->branches))
-    return TDA_ERR_WORKSPACE;
+  if (!a->workspace || a->workspace_bytes < tda_fwd_workspace_bytes_for(a)) return TDA_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0) return TDA_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(a->pairs) % 16 != 0) return TDA_ERR_LAYOUT;
   if (a->zero_bytes % 16 != 0 || reinterpret_cast<uintptr_t>(a->zero) % 16 != 0) return TDA_ERR_LAYOUT;
@@ -269,12 +283,42 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
                    fwd_occ_bytes(a->batch * a->heads, a->seq_len, c.seq_len_kv, a->branches);
   if (a->seq_len <= 32) p.part = reinterpret_cast<float*>(after_occ);
   else {
+    const int64_t bh = a->batch * a->heads;
     p.cand = reinterpret_cast<uint32_t*>(after_occ);
-    p.pvq = reinterpret_cast<uint32_t*>(after_occ + fwd_cand_list_bytes(a->batch * a->heads, a->seq_len, a->branches));
+    p.pvq = reinterpret_cast<uint32_t*>(after_occ + fwd_cand_list_bytes(bh, a->seq_len, a->branches));
+    const int64_t kd = k8_row_bytes(*a);
+    if (kd) {
+      char* k8 = after_occ + fwd_cand_bytes(bh, a->seq_len, a->branches);
+      p.k8 = reinterpret_cast<int8_t*>(k8);
+      p.ksc = reinterpret_cast<float*>(k8 + round256(a->branches * bh * c.seq_len_kv * kd));
+    }
   }
   p.stats = a->stats;
   p.pairs = a->pairs;
   p.nbr = a->branches;
+  {
+    // screen work items: a 256-row block's key tiles 0 .. n - 1 (n grows with the block) cut
+    // into chunks of kc tiles; kc is the largest multiple of 32 (whole bitmask words) that still
+    // gives at least kMinItems items, so that small problems spread over the whole GPU and no
+    // item's chain of key tiles is much longer than the rest
+    constexpr int64_t kMinItems = 1536;
+    const int nqb = (p.Nq + 255) / 256;
+    auto blk_tiles = [&](int qb) {
+      const int qt = qb * 8 + 7 < p.nqt - 1 ? qb * 8 + 7 : p.nqt - 1;
+      const int64_t t = ((int64_t)p.qoff + 32 * qt + 31) / 32;
+      return (int)(t < p.nkt - 1 ? t : p.nkt - 1) + 1;
+    };
+    auto items = [&](int kc) {
+      int64_t t = 0;
+      for (int qb = 0; qb < nqb; ++qb) t += (blk_tiles(qb) + kc - 1) / kc;
+      return t;
+    };
+    const int64_t streams = (int64_t)a->branches * a->batch * a->heads;
+    int kc = (blk_tiles(nqb - 1) + 31) / 32 * 32;
+    while (kc > 32 && streams * items(kc) < kMinItems) kc -= 32;
+    p.screen_kc = kc;
+    p.screen_items = (int)items(kc);
+  }
   if (a->zero_bytes) {
     p.zero = a->zero;
     p.zero_units = (int64_t)(a->zero_bytes / 16);

@@ -62,8 +62,7 @@ int32_t current_scratch(void** out) {
 extern "C" int32_t tda_fwd_noalloc(const tda_fwd_args* a, void* stream) {
   if (!a) return TDA_ERR_NULL_POINTER;
   tda_fwd_args b = *a;
-  const int64_t nk = a->seq_len_kv ? a->seq_len_kv : a->seq_len;
-  const size_t need = tda_fwd_workspace_bytes_kv(a->batch, a->heads, a->seq_len, nk, a->branches);
+  const size_t need = tda_fwd_workspace_bytes_for(a);
   // every other argument is checked first, against a stand-in workspace that is never touched
   b.workspace = reinterpret_cast<void*>(uintptr_t(256));
   b.workspace_bytes = need;

@@ -32,9 +32,11 @@ constexpr uint32_t kPairOverflow = 0xffffffffu;  // count of a list the forward 
 // tile) the keys j whose screen lane passed (max over its query rows of the screen score above
 // the tile's threshold minus the screen's rounding margin), a superset of the keys with a non-zero
 // weight in the query tile; the exact pass gathers only these rows.  Layout: the keys,
-// kCandCap u32 per list, in the order the screen met them (increasing); then the counts, u32 per
-// list.  A count above kCandCap marks a list that did not fit: the exact pass then walks the
-// bitmask tiles of that query tile.
+// kCandCap u32 per list, each distinct (increasing when the list has one producer; a query tile
+// whose key range the screen splits over several work items gets its keys in any order, which the
+// exact pass sorts); then the counts, u32 per list (zeroed by key_norms, raised by the screen's
+// atomic adds).  A count above kCandCap marks a list that did not fit: the exact pass then walks
+// the bitmask tiles of that query tile.
 constexpr int kCandCap = 32;
 constexpr int64_t cand_words(int64_t lists) { return lists * (1 + kCandCap); }
 
@@ -65,6 +67,12 @@ struct FwdParams {
   void* zero;                // may be null: 16-byte units [0, zero_units) the call sets to zero
   int64_t zero_units;
   int zero_per_it;           // units each screen workgroup clears per key tile it walks
+  int screen_kc;             // key tiles per screen work item (a multiple of 32): a 256-row block
+                             // whose causal key range is longer is split into several items
+  int screen_items;          // screen work items per (branch, head)
+  int8_t* k8;                // int8 screen (bf16, normalised): key rows quantised by key_prep,
+                             // [branch * B*H + bh][Nk][D] (workspace)
+  float* ksc;                // their {scale s_j, residual bound ek_j}, [branch * B*H + bh][Nk][2]
 };
 
 struct BwdParams {

@@ -2,8 +2,8 @@
 
 On CDNA3/CDNA4 the hardware does not interlock a VALU (or LDS/memory store) use of a VGPR
 written by an MFMA: the compiler must place enough independent instructions or s_nop wait
-states between them (for v_mfma_f32_32x32x16_bf16, an 8-pass op on gfx950: 12; for the
-16-pass v_mfma_f32_32x32x2f32: 20).  hipcc was seen to count them on the fall-through path
+states between them (for v_mfma_f32_32x32x16_bf16 and v_mfma_i32_32x32x32_i8, 8-pass ops on
+gfx950: 12; for the 16-pass v_mfma_f32_32x32x2f32: 20).  hipcc was seen to count them on the fall-through path
 only, leaving a read 7 wait states after the MFMA on a branch path that skipped a block.
 This module compiles each kernel source to assembly and walks every control-flow path from
 each MFMA for that many wait states, reporting:
@@ -73,6 +73,7 @@ def _functions(asm: str) -> dict:
 
 
 def _window(op: str) -> int:
+    # 16-pass fp32 32x32x2: 20; 8-pass bf16 32x32x16 and int8 32x32x32: 12
     return 20 if op.endswith("x2f32") else 12
 
 

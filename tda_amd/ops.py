@@ -146,7 +146,7 @@ def forward(q1, k1, q2, k2, v, beta, lam, relu_power: float, normalize: bool, br
         with torch.cuda.device(q1.device):
             _abi.check(lib.tda_fwd_noalloc(ctypes.byref(a), _stream(q1.device)), "tda_fwd_noalloc")
         return out
-    ws = torch.empty((lib.tda_fwd_workspace_bytes_kv(*q1.shape[:3], nk, branches) + 3) // 4,
+    ws = torch.empty((lib.tda_fwd_workspace_bytes_for(ctypes.byref(a)) + 3) // 4,
                      dtype=torch.float32, device=q1.device)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
     with torch.cuda.device(q1.device):

@@ -108,6 +108,10 @@ int main() {
     CHECK(p.B == 4 && p.H == 16 && p.Nq == 4096 && p.Nk == 4096 && p.qoff == 0);
     CHECK(p.nqt == 128 && p.nkt == 128 && p.occ_w == 4);
     CHECK(p.norms != nullptr && p.cand != nullptr && p.part == nullptr);
+    CHECK(p.k8 != nullptr && p.ksc != nullptr);  // the int8 screen's keys, after the candidate lists
+    CHECK((char*)p.k8 - (char*)p.cand >= (int64_t)2 * 64 * 128 * 33 * 4);
+    CHECK((char*)p.ksc - (char*)p.k8 == (int64_t)2 * 64 * 4096 * 128);
+    CHECK(tda_fwd_workspace_bytes_for(&a) <= a.workspace_bytes);
     CHECK(stub::last_key.d == 128 && stub::last_key.branches == 2 && stub::last_key.pkind == 2);
     // the screen's steps: per (branch, head) sum over the 16 blocks of 8 (qb + 1) key tiles
     const int64_t steps = (int64_t)2 * 64 * 8 * (16 * 17 / 2);
@@ -124,7 +128,16 @@ int main() {
     CHECK(tda_fwd(&a, nullptr) == TDA_OK);
     CHECK(stub::last_fwd.part != nullptr && stub::last_fwd.cand == nullptr);
     CHECK(stub::last_fwd.Nk == 900 && stub::last_fwd.nkt == 29 && stub::last_key.pkind == 0);
-    CHECK(stub::last_fwd.zero == nullptr);
+    CHECK(stub::last_fwd.zero == nullptr && stub::last_fwd.k8 == nullptr);
+    a.normalize = 0;  // one query tile and no normalisation: no int8 keys either way
+    CHECK(tda_fwd_workspace_bytes_for(&a) == tda_fwd_workspace_bytes_kv(1, 2, 5, 900, 1));
+  }
+  {
+    tda_fwd_args a = fwd_args(1, 2, 100, 64, 2);
+    a.dtype = TDA_DTYPE_F32;
+    a.workspace_bytes = tda_fwd_workspace_bytes_for(&a);
+    CHECK(tda_fwd(&a, nullptr) == TDA_OK);
+    CHECK(stub::last_fwd.k8 == nullptr && stub::last_fwd.screen_items >= 1 && stub::last_fwd.screen_kc % 32 == 0);
   }
   {
     tda_bwd_args a = bwd_args();

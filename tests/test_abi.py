@@ -161,6 +161,28 @@ def test_fwd_validator_rejects(mutate, code):
     assert lib.tda_fwd(ctypes.byref(a), None) == code  # rejected before any launch
 
 
+def test_workspace_for_one_call():
+    """tda_fwd_workspace_bytes_for: the int8 keys only for bf16 with normalize and more than one
+    query tile, at the call's head_dim; never above the shape-only bound."""
+    lib = _lib()
+    r256 = lambda b: 256 * ((b + 255) // 256)  # noqa: E731
+    a = _fwd_args()  # bf16, normalize, (2, 3, 100, 128), two branches
+    full = lib.tda_fwd_workspace_bytes_for(ctypes.byref(a))
+    assert full == lib.tda_fwd_workspace_bytes(2, 3, 100, 2)
+    a.normalize = 0
+    assert full - lib.tda_fwd_workspace_bytes_for(ctypes.byref(a)) == r256(2 * 6 * 100 * 128) + r256(2 * 6 * 100 * 8)
+    a.normalize, a.dtype = 1, _abi.DTYPE_F32
+    assert lib.tda_fwd_workspace_bytes_for(ctypes.byref(a)) == lib.tda_fwd_workspace_bytes_for(
+        ctypes.byref(_fwd_args(dtype=_abi.DTYPE_F32))) < full
+    b = _fwd_args(shape=(2, 3, 100, 64))
+    assert full - lib.tda_fwd_workspace_bytes_for(ctypes.byref(b)) == r256(2 * 6 * 100 * 128) - r256(2 * 6 * 100 * 64)
+    b.seq_len, b.seq_len_kv, b.q_offset = 20, 300, 280  # one query tile: decode partials, no int8 keys
+    assert lib.tda_fwd_workspace_bytes_for(ctypes.byref(b)) == lib.tda_fwd_workspace_bytes_kv(2, 3, 20, 300, 2)
+    b.head_dim = 96
+    assert lib.tda_fwd_workspace_bytes_for(ctypes.byref(b)) == 0
+    assert lib.tda_fwd_workspace_bytes_for(None) == 0
+
+
 def test_zero_range_args_pass():
     lib = _lib()
     a = _fwd_args()
@@ -249,7 +271,10 @@ def test_buffer_sizes():
     # tiles (a count block of 64 words and one item per head and query tile)
     r256 = lambda b: 256 * ((b + 255) // 256)  # noqa: E731
     cand = lambda lists, tiles: r256(lists * (1 + 32) * 4) + r256((64 + tiles) * 4)  # noqa: E731
-    assert lib.tda_fwd_workspace_bytes_kv(1, 1, 33, 5000, 1) == 256 * ((2 * 5 * 4 + 255) // 256) + cand(2, 2)
+    # + the int8 screen's keys (head_dim 128 bytes per row and branch) and their {scale, bound}
+    k8 = lambda rows, d=128: r256(rows * d) + r256(rows * 8)  # noqa: E731
+    assert lib.tda_fwd_workspace_bytes_kv(1, 1, 33, 5000, 1) == (256 * ((2 * 5 * 4 + 255) // 256) + cand(2, 2)
+                                                              + k8(5000))
     assert lib.tda_occupancy_words_kv(1, 1, 33, 0, 2) == 0
     assert lib.tda_occupancy_words(1, 1, 33, 3) == 0
     assert lib.tda_norms_floats(4, 16, 4096, 2) == 4 * 64 * 4096
@@ -259,8 +284,9 @@ def test_buffer_sizes():
     lists = 2 * 64 * 128
     assert lib.tda_bwd_workspace_bytes(4, 16, 4096, 128) == (lists * (2 + 32) + 64 + lists * 32) * 4
     # bitmask scratch, rounded up to 256 bytes, then the candidate lists
-    assert lib.tda_fwd_workspace_bytes(4, 16, 4096, 2) == 2 * 64 * 128 * 4 * 4 + cand(2 * 64 * 128, 64 * 128)
-    assert lib.tda_fwd_workspace_bytes(1, 1, 33, 1) == 256 + cand(2, 2)
+    assert lib.tda_fwd_workspace_bytes(4, 16, 4096, 2) == (2 * 64 * 128 * 4 * 4 + cand(2 * 64 * 128, 64 * 128)
+                                                           + k8(2 * 64 * 4096))
+    assert lib.tda_fwd_workspace_bytes(1, 1, 33, 1) == 256 + cand(2, 2) + k8(33)
     assert lib.tda_fwd_workspace_bytes(1, 1, 33, 3) == 0
     assert lib.tda_occupancy_words(0, 1, 1, 1) == 0
 

@@ -177,11 +177,12 @@ def test_occupancy_and_norms_match_oracle(shape, heads):
             strong = nz.view(nqt, 32, nqt, 32).any(3).any(1)
             assert not (strong & ~got).any(), (bh, br, int((strong & ~got).sum()))
     assert mism <= 4, mism  # only threshold ties within rounding may differ
-    # the screen keeps a superset of the non-zero tiles (its margin covers the bf16 rounding of
-    # the pre-scaled queries); the exact pass clears the rest, and the margin costs little
+    # the screen keeps a superset of the non-zero tiles (its margin covers the int8 quantisation
+    # residuals of the normalised rows, about 0.015 in cosine units on N(0, 1) rows, which keeps
+    # about twice the non-zero tiles); the exact pass clears the rest
     visited, computed, checked = (int(x) for x in stats.tolist())
     assert computed == int(bits.sum())
-    assert computed <= checked <= 1.5 * computed
+    assert computed <= checked <= 2.5 * computed
 
 
 def test_backward_with_and_without_bitmask_identical():

@@ -1,9 +1,10 @@
 """GPU parity at edge cases of the reference's formula (TTA:59-109, :505-517), through the
 public entry points, against the CPU oracle on the same values:
 
-* an adversarial query/key pair for the normalised bf16 screen: a weight the reference keeps
-  (cosine 1e-4 above tau) whose screen score falls below a constant margin of 2^-9 + 2^-13
-  (tests/screen_emulation.py builds it); at p < 1 a dropped weight is a large error;
+* an adversarial query/key pair for the normalised int8 screen: a weight the reference keeps
+  (cosine 1e-4 above tau) whose int8 score falls below tau by more than the bound's constant
+  terms, i.e. a test without the residual terms would drop it (tests/screen_emulation.py builds
+  it); at p < 1 a dropped weight is a large error;
 * key rows shorter than the query rows with lists that fit (padding keys past Nk in the last
   key tile), and beta <= 0 with a ragged key count;
 * powers below 1 (p = 0.5 and p = 0: x^0 = 1 for x > 0, zero gradient through the scores);
@@ -14,7 +15,9 @@ import pytest
 import torch
 
 from tests.helpers import TOL, host, make_inputs, oracle_out, rel_err, tda_grads
-from tests.screen_emulation import MARGIN_FIXED_OLD, adversarial_key, adversarial_row, prescale, tlo
+import numpy as np
+
+from tests.screen_emulation import adversarial_key, bf16, quant_tile, thr
 
 pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
@@ -31,14 +34,16 @@ def _tda(*a, **kw):
 
 
 def _adversarial_head(seed=0, d=128, n=64):
-    """q, k (n, d) float32 holding bf16 values: query rows 32..63 are copies of a row with a
-    large bf16 rounding residual once pre-scaled, key 5 has cosine tau + [8e-5, 1.3e-4] with
-    it (tau = 0 at beta = 0) and the screen score the search makes lowest, every other key of
-    key tiles 0 and 1 points against that row (cosine -1); query rows 0..31 are N(0, 1)."""
-    qa = adversarial_row(d, seed, steps=8000)
-    k5, cos, sv = adversarial_key(qa, 0.0, lo=8e-5, hi=1.3e-4, seed=seed)
-    _, _, r = prescale(qa)
-    assert sv <= tlo(0.0, MARGIN_FIXED_OLD)  # a constant 2^-9 + 2^-13 margin would drop it
+    """q, k (n, d) float32 holding bf16 values: query rows 32..63 are copies of one row (their
+    query tile quantises to one int8 row), key 5 has cosine tau + [8e-5, 1.3e-4] with it (tau = 0
+    at beta = 0) and the int8 screen score the search makes lowest, every other key of key tiles 0
+    and 1 points against that row (cosine -1); query rows 0..31 are N(0, 1)."""
+    qa = bf16(np.random.default_rng(seed).standard_normal(d).astype(np.float32))
+    tile = np.repeat(qa[None], 32, 0)
+    k5, cos, sv, _, ek = adversarial_key(qa, tile, 0.0, lo=8e-5, hi=1.3e-4, seed=seed, tries=3000, climb=2000,
+                                         score=lambda sv, eq, ek: sv)
+    _, _, eq, _ = quant_tile(tile)
+    assert sv <= thr(0.0, eq, ek, ("tau", "const"))  # a test without the residual terms drops it
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(n, d, generator=g).to(BF).float()
     q[32:] = torch.from_numpy(qa)
