@@ -140,6 +140,33 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ unsigned long long wave_ballot(bool b) { return __ballot(b); }
 
+// Sum / maximum over aligned groups of W lanes (W = 2, 4, 8 or 16) by DPP moves within a 16-lane
+// row (no LDS round trip): quad_perm [1,0,3,2] and [2,3,0,1] pair lanes within quads, then
+// row_half_mirror (lane i <- 7 - i) and row_mirror (i <- 15 - i) pair quads and half-rows.  Each
+// step adds two values in either order, so every lane of a group ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+template <int W>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(W == 2 || W == 4 || W == 8 || W == 16, "group of 2..16 lanes");
+  x += dpp_mov<0xB1>(x);
+  if constexpr (W >= 4) x += dpp_mov<0x4E>(x);
+  if constexpr (W >= 8) x += dpp_mov<0x141>(x);
+  if constexpr (W >= 16) x += dpp_mov<0x140>(x);
+  return x;
+}
+template <int W>
+__device__ __forceinline__ float group_max(float x) {
+  static_assert(W == 2 || W == 4 || W == 8 || W == 16, "group of 2..16 lanes");
+  x = fmaxf(x, dpp_mov<0xB1>(x));
+  if constexpr (W >= 4) x = fmaxf(x, dpp_mov<0x4E>(x));
+  if constexpr (W >= 8) x = fmaxf(x, dpp_mov<0x141>(x));
+  if constexpr (W >= 16) x = fmaxf(x, dpp_mov<0x140>(x));
+  return x;
+}
+
 // ------------------------------------------------------------------ transposed tiles
 // A 32-row x D tile used as the A operand of a contraction over its rows.
 // bf16: staged in (wave-private) LDS as T[d][pos(row)], pos() swapping bits 2 and 3 of the

@@ -32,6 +32,8 @@
 // (and, without normalisation, padding keys past Nk): it may keep a tile the mask empties, never
 // drop a non-zero one.  With normalisation padding keys are cleared from the hit bits, so no
 // candidate list names a key row past Nk.
+#include <type_traits>
+
 #include "tda_common.hpp"
 #include "tda_params.hpp"
 #include "tda_pos.hpp"
@@ -148,11 +150,15 @@ struct ZeroSlice {
     r = make_rsrc(P.zero ? reinterpret_cast<u32x4*>(P.zero) + z0 : nullptr,
                   (uint32_t)(zend > z0 ? (zend - z0) * 16 : 0));
   }
+  // The slices of key-tile steps step .. step + n - 1.  The whole offset is the per-lane one:
+  // the descriptor's range check (which drops the stores past the slice) does not cover the
+  // scalar offset.
   template <int NTHR>
-  __device__ __forceinline__ void clear(const FwdParams& P, int step, int tid) const {
+  __device__ __forceinline__ void clear(const FwdParams& P, int step, int tid, int n = 1) const {
     const uint32_t base = (uint32_t)step * (uint32_t)P.zero_per_it * 16u;
-    for (int u = tid; u < P.zero_per_it; u += NTHR)
-      __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, r, (uint32_t)u * 16u, base, 2);
+    const int units = n * P.zero_per_it;
+    for (int u = tid; u < units; u += NTHR)
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, r, base + (uint32_t)u * 16u, 0, 2);
   }
 };
 
@@ -292,11 +298,16 @@ __device__ __forceinline__ int max16i(const i32x16& v) {
 // Per key row of every branch: the inverse L2 norm rk_j into the norms table and, for the int8
 // screen (P.k8 set), the row kh_j = fl(k_j rk_j) quantised to int8 (P.k8, [stream][Nk][D] bytes)
 // with its scale s_j and residual bound ek_j (P.ksc, [stream][Nk] {s_j, ek_j}).  Non-finite
-// elements quantise as 0 (such a key's exact weights are 0).  A group of D/8 lanes reads one row
-// (16 bytes per lane, whole rows per load instruction); each wave covers KN_ROWS consecutive rows
-// of one (branch, head) with all its loads issued before the first reduction.  It also zeroes the
-// screen's candidate counts and the tile-pass queue count.
-constexpr int KN_GROUPS = 4;  // row groups per wave
+// elements quantise as 0 (such a key's exact weights are 0); a row whose sum of squares is finite
+// has none.  A group of D/8 lanes reads one row (16 bytes per lane, whole rows per load
+// instruction), and the row sums and maxima are DPP reductions within the group; each wave covers
+// KN_ROWS consecutive rows of one (branch, head) with all its loads issued before the first
+// reduction and its stores after the last.  It also zeroes the screen's candidate counts and the
+// tile-pass queue count.
+#ifndef TDA_KN_GROUPS
+#define TDA_KN_GROUPS 4
+#endif
+constexpr int KN_GROUPS = TDA_KN_GROUPS;  // row groups per wave
 template <int D>
 __global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
   constexpr int LPR = D / 8;        // lanes per row
@@ -304,60 +315,82 @@ __global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
   constexpr int ROWS = RPG * KN_GROUPS;
   const int l = lane_id(), sub = l % LPR;
   const int BH = P.B * P.H, N = P.Nk;     // key rows
-  const int wpr = (N + ROWS - 1) / ROWS;  // waves per (branch, head)
-  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const uint32_t wpr = (uint32_t)(N + ROWS - 1) / ROWS;  // waves per (branch, head)
+  const uint32_t wid = blockIdx.x * 4u + (threadIdx.x >> 6);  // below the grid's 2^32 waves
   if (P.cand) {  // the screen's candidate counts (it appends with atomic adds) and the queue count
     const int64_t lists = pair_lists(BR, BH, P.nqt), nthr = (int64_t)gridDim.x * 256;
     uint32_t* counts = P.cand + lists * kCandCap;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < lists; i += nthr) counts[i] = 0u;
     if (blockIdx.x == 0 && threadIdx.x == 0) P.pvq[0] = 0u;
   }
-  if (wid >= (int64_t)BR * BH * wpr) return;  // whole wave, no barriers
+  if ((int64_t)wid >= (int64_t)BR * BH * wpr) return;  // whole wave, no barriers
   const int sidx = (int)(wid / wpr), br = sidx / BH, bh = sidx % BH;
   const int t0 = (int)(wid % wpr) * ROWS + l / LPR;
-  const int slot = br ? F_K2 : F_K1;
-  const int64_t st = P.s[slot][2];
-  const bf16* head = (const bf16*)P.in[slot] + (int64_t)(bh / P.H) * P.s[slot][0] + (int64_t)(bh % P.H) * P.s[slot][1];
+  // the branch's key tensor and strides, selected without indexing the parameter block by a
+  // run-time slot (that index makes the compiler load the block from memory)
+  const bf16* kin = (const bf16*)(br ? P.in[F_K2] : P.in[F_K1]);
+  const int64_t sb = br ? P.s[F_K2][0] : P.s[F_K1][0], sh = br ? P.s[F_K2][1] : P.s[F_K1][1];
+  const int64_t st = br ? P.s[F_K2][2] : P.s[F_K1][2];
+  const bf16* head = kin + (int64_t)(bh / P.H) * sb + (int64_t)(bh % P.H) * sh;
   bf16x8 x[KN_GROUPS];
 #pragma unroll
   for (int u = 0; u < KN_GROUPS; ++u) {
     const int t = min(t0 + RPG * u, N - 1);
+#ifdef TDA_KP_NT
+    x[u] = __builtin_bit_cast(bf16x8, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(head + (int64_t)t * st + 8 * sub)));
+#else
     x[u] = *reinterpret_cast<const bf16x8*>(head + (int64_t)t * st + 8 * sub);
+#endif
   }
-  float* out = P.norms + norm_base(P, br ? N_K2 : N_K1, bh);
+  float ss[KN_GROUPS], rk[KN_GROUPS];
 #pragma unroll
   for (int u = 0; u < KN_GROUPS; ++u) {
-    float ss = PolBF16::sumsq(x[u]);
+    ss[u] = group_sum<LPR>(PolBF16::sumsq(x[u]));
+    rk[u] = inv_norm(ss[u]);
+  }
+  float* out = P.norms + norm_base(P, br ? N_K2 : N_K1, bh);
+  if (!P.k8) {
 #pragma unroll
-    for (int o = LPR / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    for (int u = 0; u < KN_GROUPS; ++u) {
+      const int t = t0 + RPG * u;
+      if (sub == 0 && t < N) out[t] = rk[u];
+    }
+    return;
+  }
+  i32x2 packed[KN_GROUPS];
+  float2 se[KN_GROUPS];
+#pragma unroll
+  for (int u = 0; u < KN_GROUPS; ++u) {
+    float kh[8], m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kh[j] = (float)x[u][j] * rk[u];
+    if (!__builtin_isfinite(ss[u])) {  // a finite sum of squares: every |kh| <= 1 + 2^-20
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kh[j] = __builtin_isfinite(kh[j]) ? kh[j] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(kh[j]));
+    m = group_max<LPR>(m);
+    const float sc = m * (1.f / 127.f), inv = m > 0.f ? 127.f / m : 0.f;
+    int b[8];
+    float e2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      b[j] = quant(kh[j], inv);
+      const float r = __builtin_fmaf(-sc, (float)b[j], kh[j]);
+      e2 = __builtin_fmaf(r, r, e2);
+    }
+    packed[u] = i32x2{pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7])};
+    se[u] = float2{sc, res_bound(group_sum<LPR>(e2))};
+  }
+#pragma unroll
+  for (int u = 0; u < KN_GROUPS; ++u) {
     const int t = t0 + RPG * u;
-    const float rk = inv_norm(ss);
-    if (sub == 0 && t < N) out[t] = rk;
-    if (P.k8) {
-      float kh[8], m = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float v = (float)x[u][j] * rk;
-        kh[j] = __builtin_isfinite(v) ? v : 0.f;
-        m = fmaxf(m, fabsf(kh[j]));
-      }
-#pragma unroll
-      for (int o = LPR / 2; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-      const float sc = m * (1.f / 127.f), inv = m > 0.f ? 127.f / m : 0.f;
-      int b[8];
-      float e2 = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        b[j] = quant(kh[j], inv);
-        const float r = __builtin_fmaf(-sc, (float)b[j], kh[j]);
-        e2 = __builtin_fmaf(r, r, e2);
-      }
-#pragma unroll
-      for (int o = LPR / 2; o >= 1; o >>= 1) e2 += __shfl_xor(e2, o);
-      if (t < N) {
-        int8_t* krow = P.k8 + ((int64_t)sidx * N + t) * D;
-        *reinterpret_cast<i32x2*>(krow + 8 * sub) = i32x2{pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7])};
-        if (sub == 0) *reinterpret_cast<float2*>(P.ksc + 2 * ((int64_t)sidx * N + t)) = float2{sc, res_bound(e2)};
+    if (t < N) {
+      *reinterpret_cast<i32x2*>(P.k8 + ((int64_t)sidx * N + t) * D + 8 * sub) = packed[u];
+      if (sub == 0) {
+        out[t] = rk[u];
+        *reinterpret_cast<float2*>(P.ksc + 2 * ((int64_t)sidx * N + t)) = se[u];
       }
     }
   }
@@ -513,30 +546,62 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
 // The normalised screen on int8 matrix cores (v_mfma_i32_32x32x32_i8, twice the bf16 rate, half
 // the operand bytes).  Workgroup = one work item (as fwd_screen), four waves of two 32-row query
 // tiles.  Per wave the query rows are normalised (their inverse norms rq go to the norms table),
-// quantised to int8 with one scale per query tile and held as A fragments; the int8 key tiles of
-// key_prep (32 x D bytes, contiguous) and their {s_j, ek_j} stream through a two-stage LDS ring
-// (buffer loads into VGPRs one iteration ahead, rows past Nk read 0, one barrier per tile).  The
+// quantised to int8 with one scale per query tile and held as A fragments.  The int8 key tiles
+// of key_prep (32 x D bytes, contiguous) and their {s_j, ek_j} stream through a ring of
+// I8_STAGES LDS stages of I8_TPI tiles by direct buffer->LDS loads issued I8_STAGES - 1 stages
+// ahead (rows past Nk read 0; one wait on the wave's own loads and one barrier per stage).  The
 // tile is S = A B^T: each lane holds one key j and 16 query rows, and the test (the int8 bound
 // above) is "float(max_i A_ij) * (sq s_j) > thr_j", a few operations per lane and query tile.
 // Hit bits give the bitmask words and the candidate keys (screen_flush).
+#ifndef TDA_I8_STAGES
+#define TDA_I8_STAGES 4
+#endif
+#ifndef TDA_I8_TPI
+#define TDA_I8_TPI 2
+#endif
+constexpr int I8_STAGES = TDA_I8_STAGES;
+constexpr int I8_TPI = TDA_I8_TPI;       // key tiles per stage (a divisor of 32)
+constexpr int I8_AHEAD = I8_STAGES - 1;  // stages in flight past the one being tested
+static_assert(32 % I8_TPI == 0 && I8_TPI <= 4, "stages of whole parts of a bitmask word");
+// Chunk swizzle of an int8 key tile row (16-byte chunks): conflict-free fragment reads, where
+// lane (m, g) reads chunk 2 t + g of row m.
+template <int D>
+__device__ __forceinline__ int i8swz(int r) {
+  if constexpr (D == 128) return (r ^ (r >> 3)) & 7;
+  else return ((r >> 1) ^ (r >> 3)) & 3;
+}
+// 32-bit LDS address of a __shared__ object (for inline-asm LDS instructions).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {  // vmcnt(N) with the other counters left alone
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+// rint(x) for |x| < 2^22 by the float adder: x + 1.5 * 2^23 rounds to an integer (ties to even)
+// whose low bits are that integer's two's complement; returns the sum.
+constexpr float kRintMagic = 12582912.0f;
+__device__ __forceinline__ float rint_sum(float x) { return x + kRintMagic; }
+
 template <int D>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) fwd_screen_i8(FwdParams P, int BR) {
-  constexpr int QPW = 2, NTHR = 256;
-  constexpr int NK = D / 32;                // int8 MFMA steps over d
-  constexpr int KS8 = D + 16;               // LDS row stride (bytes): conflict-free fragment reads
-  constexpr int CPR = D / 16;               // 16-byte chunks per int8 key row
-  constexpr int STAGERS = 32 * CPR;         // threads loading a tile, one chunk each
-  __shared__ __attribute__((aligned(16))) int8_t kst[2][32 * KS8];
-  __shared__ __attribute__((aligned(16))) float2 ksc[2][32];  // {s_j, ek_j} of each tile's keys
+  constexpr int QPW = 2, NTHR = 256, TPI = I8_TPI;
+  constexpr int NK = D / 32;                     // int8 MFMA steps over d
+  constexpr int CPR = D / 16;                    // 16-byte chunks per int8 key row
+  constexpr int RPI = 64 / CPR;                  // key rows per load instruction
+  constexpr int KI = TPI * 32 / RPI;             // key load instructions per stage
+  constexpr int TB = 32 * D;                     // bytes of one int8 key tile
+  __shared__ __attribute__((aligned(16))) int8_t kst[I8_STAGES][TPI * TB];
+  __shared__ __attribute__((aligned(16))) float2 ksc[I8_STAGES][TPI * 32];  // {s_j, ek_j} per key
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5, tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
   const ScreenItem it = screen_item(P, BR);
-  const int k0 = it.k0, k1 = it.k1, nit = k1 - k0;
+  const int k0 = it.k0, k1 = it.k1, nit = k1 - k0, nst = (nit + TPI - 1) / TPI;
   const int br = it.sidx / BH, bh = it.sidx % BH;
   const int b = bh / P.H, h = bh % P.H;
-  const int qslot = br ? F_Q2 : F_Q1;
   const int q0w = it.qb * 256 + 32 * QPW * wv;  // first row of this wave
   const int qt0 = q0w >> 5;                     // this wave's query tiles: qt0, qt0 + 1
   bool live[QPW];
@@ -547,29 +612,58 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
     ktl[s] = kt_last(qt0 + s, qoff, P.nkt);
   }
 
-  // ---- staging: tile kt is the stream's int8 key rows 32 kt .. 32 kt + 31 (contiguous, D bytes
-  // each) and their {s_j, ek_j}; rows past Nk read 0
-  const int8_t* k8head = P.k8 + (int64_t)it.sidx * Nk * D;
-  const float* schead = P.ksc + 2 * (int64_t)it.sidx * Nk;
-  const bool stager = tid < STAGERS;
-  const int srow = tid / CPR, sch = tid % CPR;
-  u32x4 R = {}, RS = {};
-  auto fetch = [&](int i) {
-    const int kt = k0 + i;
-    if (kt >= k1) return;
-    const uint32_t rows = (uint32_t)min(32, Nk - 32 * kt);
-    if (stager) R = buf_load16(make_rsrc(k8head + (int64_t)(32 * kt) * D, rows * D), (uint32_t)(16 * tid));
-    if (tid < 16) RS = buf_load16(make_rsrc(schead + (int64_t)(64 * kt), rows * 8), (uint32_t)(16 * tid));
+  // ---- staging: stage j holds tiles k0 + TPI j .. + TPI - 1 (the stream's int8 key rows,
+  // contiguous, D bytes each) and their {s_j, ek_j}.  The buffer descriptors start at the item's
+  // first key row (host: an item spans under 2^30 bytes); rows past Nk read 0.  Every wave issues
+  // the same loads per stage: key load instructions wv, wv + 4, .. (1 KiB: RPI rows each; lane L
+  // moves stage row R = RPI k + L / CPR, chunk (L % CPR) ^ swz(R % 32)) and a quarter of the
+  // stage's {s_j, ek_j} (4 TPI lanes of 16 bytes).
+  static_assert(KI % 4 == 0, "key load instructions spread evenly over the four waves");
+  constexpr int LK = KI / 4;      // key load instructions per wave and stage
+  constexpr int LW = LK + 1;      // loads per wave and stage
+  const int64_t rows_left = (int64_t)Nk - 32 * (int64_t)k0;
+  const int8_t* k8base = P.k8 + ((int64_t)it.sidx * Nk + 32 * (int64_t)k0) * D;
+  const float* scbase = P.ksc + 2 * ((int64_t)it.sidx * Nk + 32 * (int64_t)k0);
+  const uint32_t k8bytes = (uint32_t)(rows_left * D < 0xffffff00ll ? rows_left * D : 0xffffff00ll);
+  const uint32_t scbytes = (uint32_t)(rows_left * 8 < 0xffffff00ll ? rows_left * 8 : 0xffffff00ll);
+  uint32_t loff[LK];
+#pragma unroll
+  for (int u = 0; u < LK; ++u) {
+    const int R = RPI * (4 * u + wv) + l / CPR;
+    loff[u] = (uint32_t)(R * D + 16 * ((l % CPR) ^ i8swz<D>(R & 31)));
+  }
+  const uint32_t soff = (uint32_t)(16 * (4 * TPI * wv + l));  // this lane's {s_j, ek_j} chunk
+  // The stage offset goes into the per-lane offset, which the descriptor's range check covers
+  // (rows past Nk must read 0), not into the scalar offset.
+  auto issue = [&](int j) {  // stage j into ring slot j % I8_STAGES
+    const int st = j % I8_STAGES;
+    const uint32_t so = (uint32_t)j * (uint32_t)(TPI * TB);
+#pragma unroll
+    for (int u = 0; u < LK; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(k8base, k8bytes), LDS_PTR(void, &kst[st][1024 * (4 * u + wv)]), 16,
+                                               (uint32_t)(loff[u] + so), 0, 0, 0);
+    if (l < 4 * TPI)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(scbase, scbytes), LDS_PTR(void, &ksc[st][8 * TPI * wv]), 16,
+                                               (uint32_t)(soff + (uint32_t)j * (uint32_t)(TPI * 256)), 0, 0, 0);
   };
-  auto commit = [&](int i) {
-    const int kt = k0 + i;
-    if (kt >= k1) return;
-    if (stager) *reinterpret_cast<u32x4*>(&kst[i & 1][srow * KS8 + 16 * sch]) = R;
-    if (tid < 16) *reinterpret_cast<u32x4*>(&ksc[i & 1][2 * tid]) = RS;
+  // Wait for this wave's loads of stage j: the loads of later stages may stay in flight (loads
+  // complete in order; stores or atomics issued since only lengthen the wait).
+  auto wait_stage = [&](int j) {
+    if (j + I8_AHEAD <= nst) wait_vm<LW * (I8_AHEAD - 1)>();  // stages j + 1 .. j + I8_AHEAD - 1 issued
+    else wait_vm<0>();
   };
+  // issued before the query setup, whose loads and latency they overlap
+#pragma unroll
+  for (int j = 0; j < I8_AHEAD; ++j)
+    if (j < nst) issue(j);
 
   // ---- resident int8 query fragments and the per-tile constants of the test
-  const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
+  const int qslot = br ? F_Q2 : F_Q1;
+  const bf16* qin = (const bf16*)(br ? P.in[F_Q2] : P.in[F_Q1]);
+  const int64_t qsb = br ? P.s[F_Q2][0] : P.s[F_Q1][0], qsh = br ? P.s[F_Q2][1] : P.s[F_Q1][1];
+  const int64_t qst = br ? P.s[F_Q2][2] : P.s[F_Q1][2];
+  (void)qslot;
+  const bf16* qhead = qin + (int64_t)b * qsb + (int64_t)h * qsh;
   const float beta = *P.beta;
   i32x4 A8[QPW][NK];
   float sq[QPW], tq[QPW], cq[QPW];  // scale, thr part of the tile, coefficient of ek_j
@@ -577,31 +671,44 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
   for (int s = 0; s < QPW; ++s) {
     const int iq = q0w + 32 * s + n32;
     const bool valid = iq < Nq;
-    const bf16* row = qhead + (int64_t)min(iq, Nq - 1) * P.s[qslot][2];  // rows >= Nq: never vote
+    const bf16* row = qhead + (int64_t)min(iq, Nq - 1) * qst;  // rows >= Nq: never vote
     bf16x8 qv[NK][2];  // lane (m, g): elements 32 t + 16 g .. + 16 of row m
 #pragma unroll
     for (int t = 0; t < NK; ++t) {
       qv[t][0] = *reinterpret_cast<const bf16x8*>(row + 32 * t + 16 * g);
       qv[t][1] = *reinterpret_cast<const bf16x8*>(row + 32 * t + 16 * g + 8);
     }
-    // the row's sum of squares, and the largest finite |q| from the raw bits (magnitude bits of a
-    // finite bf16 order like its value)
-    float ss = 0.f;
-    uint32_t mb = 0u;
+    // the row's sum of squares and largest |q|; a row with a finite sum of squares has only
+    // finite elements, and every element of it then scales to |x| <= m below
+    float ss = 0.f, mq = 0.f;
 #pragma unroll
     for (int t = 0; t < NK; ++t)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        ss += PolBF16::sumsq(qv[t][c]);
-        const u32x4 w = __builtin_bit_cast(u32x4, qv[t][c]);
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t lo = w[k] & 0x7fffu, hi = (w[k] >> 16) & 0x7fffu;
-          mb = max(mb, (lo & 0x7f80u) != 0x7f80u ? lo : 0u);
-          mb = max(mb, (hi & 0x7f80u) != 0x7f80u ? hi : 0u);
+        for (int j = 0; j < 8; ++j) {
+          const float x = (float)qv[t][c][j];
+          ss = __builtin_fmaf(x, x, ss);
+          mq = fmaxf(mq, fabsf(x));
         }
-      }
-    float mq = __builtin_bit_cast(float, mb << 16);
+    ss += __shfl_xor(ss, 32);
+    const bool finite_row = __builtin_isfinite(ss);
+    if (!finite_row) {  // the largest finite |q| (non-finite elements quantise as 0)
+      uint32_t mb = 0u;
+#pragma unroll
+      for (int t = 0; t < NK; ++t)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const u32x4 w = __builtin_bit_cast(u32x4, qv[t][c]);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = w[k] & 0x7fffu, hi = (w[k] >> 16) & 0x7fffu;
+            mb = max(mb, (lo & 0x7f80u) != 0x7f80u ? lo : 0u);
+            mb = max(mb, (hi & 0x7f80u) != 0x7f80u ? hi : 0u);
+          }
+        }
+      mq = __builtin_bit_cast(float, mb << 16);
+    }
     // the row values are converted again below, not kept as fp32 (register pressure)
 #pragma unroll
     for (int t = 0; t < NK; ++t)
@@ -611,19 +718,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
         asm volatile("" : "+v"(w));
         qv[t][c] = __builtin_bit_cast(bf16x8, w);
       }
-    const float rq = inv_norm(ss + __shfl_xor(ss, 32));
+    const float rq = inv_norm(ss);
     if (g == 0 && valid && it.chunk == 0) P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + iq] = rq;
     const float sc = valid ? rq : 0.f;
     // the scale, one per query tile: sq = m / 127 with m the tile's largest |qh| = max over its
-    // rows of rq_i max |q_i| (any m works: the residuals are taken against the sq the test uses,
-    // and rint past +-127 is clamped)
+    // rows of rq_i max |q_i|; every |x| <= m, so x 127 / m rounds into [-127, 127]
     mq = fmaxf(mq, __shfl_xor(mq, 32));  // the row's largest |q|
     float m = mq * sc;
     m = __builtin_isfinite(m) ? m : 0.f;
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));  // over the tile's rows
+    m = group_max<16>(m);
+    m = fmaxf(m, __shfl_xor(m, 16));  // over the tile's rows
     sq[s] = m * (1.f / 127.f);
     const float inv = m > 0.f ? 127.f / m : 0.f;
+    const bool any_nonfinite = wave_ballot(!finite_row) != 0ull;
     float r2 = 0.f;  // squared norm of the row's quantisation residual (this lane's half)
 #pragma unroll
     for (int t = 0; t < NK; ++t) {
@@ -634,10 +741,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int j = 4 * u + e;
-          const float x0 = (float)qv[t][j >> 3][j & 7] * sc;
-          const float x = __builtin_isfinite(x0) ? x0 : 0.f;
-          a[e] = quant(x, inv);
-          const float r = __builtin_fmaf(-sq[s], (float)a[e], x);
+          float x = (float)qv[t][j >> 3][j & 7] * sc;
+          if (any_nonfinite) x = __builtin_isfinite(x) ? x : 0.f;
+          const float rs = rint_sum(x * inv);  // rint(x inv), |x inv| <= 127 (1 + 2^-22)
+          a[e] = __builtin_bit_cast(int, rs);  // low byte: the int8 value
+          const float r = __builtin_fmaf(-sq[s], rs - kRintMagic, x);
           r2 = __builtin_fmaf(r, r, r2);
         }
         w[u] = pack4(a[0], a[1], a[2], a[3]);
@@ -646,8 +754,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
       __builtin_amdgcn_sched_barrier(0);  // one step's values live at a time
     }
     r2 += __shfl_xor(r2, 32);
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) r2 = fmaxf(r2, __shfl_xor(r2, o));  // largest row of the tile
+    r2 = group_max<16>(r2);
+    r2 = fmaxf(r2, __shfl_xor(r2, 16));  // largest row of the tile
     const float eq = res_bound(r2);
     // tau is monotone in the position: its smallest value over the tile's rows is at one end
     const int i0 = q0w + 32 * s, i1 = max(i0, min(i0 + 31, Nq - 1));
@@ -661,26 +769,32 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
   uint32_t hb[QPW], cn[QPW];  // hit bits; candidate keys met per query tile (may pass the cap)
 #pragma unroll
   for (int s = 0; s < QPW; ++s) hb[s] = cn[s] = 0u;
-  const int koff = n32 * KS8 + 16 * g;
+  uint32_t koff[NK];  // this lane's fragment chunks in a tile: row n32, chunk 2 t + g
+#pragma unroll
+  for (int t = 0; t < NK; ++t) koff[t] = (uint32_t)(n32 * D + 16 * ((2 * t + g) ^ i8swz<D>(n32)));
 
-  auto process = [&](int kt, int st) {
-    if (!(live[0] && kt <= ktl[QPW - 1])) return;
-    const int8_t* kp = &kst[st][koff];
+  // One tile: the fragment reads are inline asm (the compiler orders every LDS read after all
+  // outstanding direct-to-LDS loads, vmcnt(0), which would drain the ring each tile, while
+  // wait_stage and the barrier already order this stage's loads before them); the wait that ends
+  // them takes the fragments as operands, so no use of them is scheduled before it.
+  auto process = [&](int kt, uint32_t tbase, uint32_t sbase) {
     i32x4 fk[NK];
 #pragma unroll
-    for (int t = 0; t < NK; ++t) {  // in MFMA order
-      fk[t] = *reinterpret_cast<const i32x4*>(kp + 32 * t);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    const float2 kq = ksc[st][n32];  // the lane's key: {s_j, ek_j} (0 past Nk)
+    for (int t = 0; t < NK; ++t)
+      asm volatile("ds_read_b128 %0, %1" : "=v"(fk[t]) : "v"(tbase + koff[t]) : "memory");
+    float2 kq;  // the lane's key: {s_j, ek_j} (0 past Nk)
+    asm volatile("ds_read_b64 %0, %1" : "=v"(kq) : "v"(sbase + 8u * (uint32_t)n32) : "memory");
+    if constexpr (NK == 4)
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fk[0]), "+v"(fk[1]), "+v"(fk[2]), "+v"(fk[3]), "+v"(kq) : : "memory");
+    else
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fk[0]), "+v"(fk[1]), "+v"(kq) : : "memory");
     __builtin_amdgcn_sched_barrier(0);
     i32x16 S[QPW];
 #pragma unroll
-    for (int s = 0; s < QPW; ++s) S[s] = i32x16{};
-#pragma unroll
     for (int s = 0; s < QPW; ++s) {
 #pragma unroll
-      for (int t = 0; t < NK; ++t) S[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A8[s][t], fk[t], S[s], 0, 0, 0);
+      for (int t = 0; t < NK; ++t)
+        S[s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A8[s][t], fk[t], t ? S[s] : i32x16{}, 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);  // keep the chains apart
     }
     const uint32_t bit = 1u << (kt & 31);
@@ -693,19 +807,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
     }
   };
 
-  fetch(0);
-  commit(0);
-  if (nit > 1) fetch(1);
-  __syncthreads();
-  for (int i = 0; i < nit; ++i) {
-    const int kt = k0 + i;
-    if (P.zero) zs.clear<NTHR>(P, i, tid);
-    process(kt, i & 1);
-    screen_flush<QPW, true>(P, BR, it, qt0, live, hb, cn, kt);
-    // the other stage was last read before the previous barrier
-    if (i + 1 < nit) commit(i + 1);
-    if (i + 2 < nit) fetch(i + 2);
-    __syncthreads();
+  // the last stage with a tile some query tile of the wave sees (later tiles of a stage are
+  // masked in the test)
+  const int jl = live[0] ? (ktl[QPW - 1] - k0) / TPI : -1;
+  for (int j = 0; j < nst; ++j) {
+    wait_stage(j);
+    __syncthreads();  // stage j is in LDS; every wave is past stage j - 1, whose slot is reloaded
+    if (j + I8_AHEAD < nst) issue(j + I8_AHEAD);
+    if (P.zero) zs.clear<NTHR>(P, TPI * j, tid, min(TPI, nit - TPI * j));
+    if (j <= jl) {
+      const int st = j % I8_STAGES;
+      const uint32_t kb = lds_addr(&kst[st][0]), sb = lds_addr(&ksc[st][0]);
+#pragma unroll
+      for (int u = 0; u < TPI; ++u) process(k0 + TPI * j + u, kb + (uint32_t)(u * TB), sb + (uint32_t)(u * 256));
+    }
+    // the stage's last tile of the item (stages never straddle a bitmask word)
+    screen_flush<QPW, true>(P, BR, it, qt0, live, hb, cn, min(k0 + TPI * j + TPI - 1, k1 - 1));
   }
   screen_counts<QPW>(P, BR, it, qt0, live, cn);
   screen_count<QPW>(P, it, live, ktl);

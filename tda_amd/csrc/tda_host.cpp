@@ -313,8 +313,12 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
       for (int qb = 0; qb < nqb; ++qb) t += (blk_tiles(qb) + kc - 1) / kc;
       return t;
     };
+    // at most 2^18 key tiles per item: an item's int8 key rows (32 x 128 bytes per tile) then
+    // span under 2^30 bytes, within the screen's 32-bit buffer offsets
+    constexpr int kMaxKc = 1 << 18;
     const int64_t streams = (int64_t)a->branches * a->batch * a->heads;
     int kc = (blk_tiles(nqb - 1) + 31) / 32 * 32;
+    if (kc > kMaxKc) kc = kMaxKc;
     while (kc > 32 && streams * items(kc) < kMinItems) kc -= 32;
     p.screen_kc = kc;
     p.screen_items = (int)items(kc);
