@@ -29,17 +29,20 @@ if ROOT not in sys.path:
 METRIC = "fwd/fwd+bwd TFLOP/s + % bf16 MFMA peak, diff-TDA B4 H16 N4096 d128"
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk/CU)
 PEAK_F32_TFLOPS = 157.3     # MI355X dense fp32 MFMA
+PEAK_I8_TOPS = 5033.2       # MI355X dense int8 MFMA (twice the bf16 rate; published as 5.0 POP/s)
 PEAK_HBM_GBS = 8000.0
 SHAPE = (4, 16, 4096, 128)
 BETA, LAM, POWER = 1.0, 0.5, 2.0
 FWD_UNITS, FWDBWD_UNITS = 3.0, 11.0          # counted causal-dense units (U = B*H*N^2*d)
 REF_FWD_UNITS, REF_FWDBWD_UNITS = 4.0, 14.0  # the reference's two independent TRA calls
 SCREEN_UNITS = 2.0                           # fwd_screen: Q1 K1^T and Q2 K2^T over the causal half
-# HBM bytes per launch of the dominant kernel (fwd_screen) at SHAPE, from rocprofv3 --pmc FETCH_SIZE
-# and --pmc WRITE_SIZE runs of this script, each scaled by what the same counter reads for
-# --copy-probe (a 2^30-byte device copy): FETCH_SIZE x 2.000, WRITE_SIZE x 1.000.  The command lines
-# and the per-kernel figures are in profiles/tda_c2_bf16_counters.md; re-measure after kernel changes.
-SCREEN_HBM_BYTES = None
+# (with normalize, fwd_screen runs v_mfma_i32_32x32x32_i8: 2U int8 operations, priced at the int8 peak)
+# HBM bytes per forward-only launch of the dominant kernel (fwd_screen) at SHAPE, from rocprofv3
+# --pmc FETCH_SIZE and --pmc WRITE_SIZE runs of this script, each scaled by what the same counter
+# reads for --copy-probe (a 2^30-byte device copy): FETCH_SIZE x 2.000, WRITE_SIZE x 1.000 (352.5 MB
+# read + 54.1 MB written).  The command lines and the per-kernel figures are in
+# profiles/tda_c2_bf16_counters.md; re-measure after kernel changes.
+SCREEN_HBM_BYTES = 4.066e8
 SCREEN_KERNEL = "fwd_screen"
 
 
@@ -217,8 +220,8 @@ def side_configs(steps: int, warmup: int):
                          "ms": ms, "tflops": units(shape1, 2.0) / (ms * 1e-3) / 1e12,
                          "pct_peak": 100.0 * units(shape1, 2.0) / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
                          "counted_units": 2.0, "launch_us": lu,
-                         "screen_frac_of_peak": (units(shape1, 1.0) / (lu.get(SCREEN_KERNEL, 1e9) * 1e-6) / 1e12
-                                                 / PEAK_BF16_TFLOPS),
+                         "screen_frac_of_i8_peak": (units(shape1, 1.0) / (lu.get(SCREEN_KERNEL, 1e9) * 1e-6) / 1e12
+                                                    / PEAK_I8_TOPS),
                          "screen_executed_gflop": screen_ex / 1e9, **st1}
     del q, k, v
     shape4 = (1, 32, 16384, 128)
@@ -404,7 +407,9 @@ def main(argv=None) -> int:
     # (the candidate pass issues fewer: one of each per branch and query tile)
     screen_exec = st["tiles_visited"] * tile_flops(d)
     exact_exec_max = st["tiles_screen_kept"] * 2 * tile_flops(d)
-    fwd_exec_tf = (screen_exec + exact_exec_max) / (fwd_ms * 1e-3) / 1e12
+    # fraction of the forward's time the matrix cores would need at their peaks for that work
+    # (screen: int8 operations; exact pass: bf16 FLOPs)
+    fwd_exec_frac = (screen_exec / (PEAK_I8_TOPS * 1e12) + exact_exec_max / (PEAK_BF16_TFLOPS * 1e12)) / (fwd_ms * 1e-3)
     res = {
         "metric": METRIC,
         "value": fb_tf,
@@ -429,10 +434,11 @@ def main(argv=None) -> int:
                 "kind": "dense-equivalent (3U)", "counted_units": FWD_UNITS,
                 "launch_us": {k: round(t, 2) for k, t in fwd_launch_us.items()},
                 "launch_sum_us": round(fwd_launch_total, 2),
-                "executed_mfma_tflops_max": fwd_exec_tf,
-                "executed_frac_of_peak_max": fwd_exec_tf / PEAK_BF16_TFLOPS,
-                "executed_note": "score tiles of every visited tile (screen) + at most one score and one A.V "
-                                 "tile per screen-kept tile (exact pass), from the kernels' tile counters",
+                "executed_screen_gop": screen_exec / 1e9, "executed_exact_gflop_max": exact_exec_max / 1e9,
+                "executed_frac_of_peak_max": fwd_exec_frac,
+                "executed_note": "int8 score tiles of every visited tile (screen, at the int8 peak) + at most "
+                                 "one bf16 score and one A.V tile per screen-kept tile (exact pass, at the bf16 "
+                                 "peak), over the forward's time; from the kernels' tile counters",
                 **st},
         "fwd_bwd": {"ms": fb_ms, "event_ms": step_ms, "wall_ms": wall_ms, "tflops": fb_tf,
                     "pct_peak": 100.0 * fb_tf / PEAK_BF16_TFLOPS, "kind": "dense-equivalent (11U)",
@@ -447,17 +453,20 @@ def main(argv=None) -> int:
             "note": "FLOPs of two independent TRA calls (4U fwd, 14U fwd+bwd), as the reference executes",
             "fwd_tflops": units(SHAPE, REF_FWD_UNITS) / (fwd_ms * 1e-3) / 1e12,
             "fwd_bwd_tflops": units(SHAPE, REF_FWDBWD_UNITS) / (fb_ms * 1e-3) / 1e12},
-        "roofline": {"kernel": SCREEN_KERNEL, "bound": "mfma",
-                     "achieved": screen_tf, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": screen_tf / PEAK_BF16_TFLOPS, "traffic": SCREEN_HBM_BYTES,
+        "roofline": {"kernel": SCREEN_KERNEL, "bound": "mfma", "mfma": "v_mfma_i32_32x32x32_i8",
+                     "achieved": screen_tf, "peak": PEAK_I8_TOPS, "unit": "TOP/s",
+                     "frac": screen_tf / PEAK_I8_TOPS, "traffic": SCREEN_HBM_BYTES,
                      "launch_us": screen_us,
-                     "algorithmic": f"2U = {screen_alg:.4e} FLOP per launch (Q1K1^T and Q2K2^T, causal half)",
-                     "executed_tflops": screen_exec / (screen_us * 1e-6) / 1e12,
-                     "executed_gflop": screen_exec / 1e9,
+                     "algorithmic": f"2U = {screen_alg:.4e} int8 operations per launch (Q1K1^T and Q2K2^T, "
+                                    "causal half)",
+                     "bf16_equivalent_frac": screen_tf / PEAK_BF16_TFLOPS,
+                     "executed_tops": screen_exec / (screen_us * 1e-6) / 1e12,
+                     "executed_gop": screen_exec / 1e9,
                      "timing": "HIP events recorded by the library on the launch stream before and after "
                                "this kernel, averaged over the timed forward calls",
                      "traffic_note": "HBM bytes per fwd_screen launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, "
-                                     "copy-calibrated); compulsory: Q1, K1, Q2, K2 once = 2.684e8"},
+                                     "copy-calibrated); compulsory: Q1, Q2 (bf16) and the int8 K1, K2 with "
+                                     "their scales once = 2.055e8"},
     }
     if SCREEN_HBM_BYTES:
         res["roofline"]["hbm_gbs_at_traffic"] = SCREEN_HBM_BYTES / (screen_us * 1e-6) / 1e9

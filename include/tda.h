@@ -190,7 +190,7 @@ int32_t tda_validate_bwd(const tda_bwd_args* args);
    arguments).  The _kv forms take the key rows Nk; the others are the Nk = Nq case.  The forward
    workspace functions without a tda_fwd_args return the largest any call of that shape needs
    (bf16 with normalize, head_dim 128); tda_fwd_workspace_bytes_for gives the exact need of one
-   call (its dtype, normalize and head_dim; the workspace fields are not read). */
+   call (from its shape fields, dtype, normalize and head_dim; the pointers are not read). */
 size_t tda_occupancy_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 size_t tda_norms_floats(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 size_t tda_fwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
@@ -215,9 +215,12 @@ int32_t tda_bwd(const tda_bwd_args* args, void* stream);
  * as tda_fwd, except that args->workspace and args->workspace_bytes are ignored: the workspace
  * is a device array of the library, TDA_NOALLOC_SCRATCH_BYTES (16 MiB) per GPU, held from the
  * first call on that GPU until the process ends.  A call whose workspace
- * (tda_fwd_workspace_bytes_kv) exceeds it returns TDA_ERR_SCRATCH before touching the GPU
- * (e.g. B*H = 64 at seq_len 4096 needs 2.4 MiB; one query against B*H = 64 heads of 16384 keys
- * 0.5 MiB).  Every call on one GPU shares that GPU's array, which keeps the last call's
+ * (tda_fwd_workspace_bytes_for) exceeds it returns TDA_ERR_SCRATCH before touching the GPU.
+ * The normalised bf16 forward's workspace holds int8 copies of the key rows (head_dim + 8
+ * bytes per key row and branch): TRA at B*H = 64, seq_len 2048, head_dim 64 needs 9.6 MiB and
+ * fits; differential TDA at B*H = 64, seq_len 4096, head_dim 128 needs 70.3 MiB and does not;
+ * without normalize the same call needs 2.3 MiB, and one query against B*H = 64 heads of 16384
+ * keys 0.5 MiB.  Every call on one GPU shares that GPU's array, which keeps the last call's
  * contents: calls that overlap on one GPU (other streams, unordered host threads) race and
  * must be serialised by the caller.  The outputs (out, norms, occupancy, pairs, stats) are
  * the caller's as for tda_fwd. */

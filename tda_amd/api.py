@@ -20,13 +20,37 @@ Superset behaviour (all results identical where the reference is defined):
     and the row sees keys j <= q_offset + i (KV-cache decode, chunked prefill).  The default
     q_offset is max(Nk - Nq, 0): the queries are the last Nq positions of the keys, and 0
     when Nq = Nk, which is the reference's case.
-Only the causal form exists, as in the reference.  Supported head_dim: 64, 128.
+Only the causal form exists, as in the reference.  Supported head_dim: 16, 32, 64, 128 (the
+reference takes any power of two >= 16, TTA:348, :366-368).  The kernels run d = 64 and 128;
+d = 16 and 32 are computed at d = 64 with the rows zero-padded (dot products and norms
+unchanged) and beta scaled by sqrt(64 / d), so that tau = beta sqrt(2 ln(P+1) / d) is the same
+threshold; the padding's gradients are dropped and beta's gradient flows through the scaling.
+d = 256 raises ValueError (the kernels' register budgets are sized for d <= 128).
 """
 from __future__ import annotations
 
+import math
+
 import torch
+import torch.nn.functional as F
 
 from . import ops
+
+_KERNEL_DIMS = (64, 128)
+_PADDED_DIMS = (16, 32)  # computed at d = 64
+
+
+def _head_dim(d: int) -> int:
+    """The kernel head_dim for a caller head_dim d (ValueError when unsupported)."""
+    if d in _KERNEL_DIMS:
+        return d
+    if d in _PADDED_DIMS:
+        return 64
+    raise ValueError(f"head_dim must be 16, 32, 64 or 128, got {d}")
+
+
+def _pad(t: torch.Tensor, dk: int) -> torch.Tensor:
+    return t if t.shape[-1] == dk else F.pad(t, (0, dk - t.shape[-1]))
 
 _COMPUTE = {torch.float32: torch.float32, torch.bfloat16: torch.bfloat16,
             torch.float16: torch.float32, torch.float64: torch.float32}
@@ -62,8 +86,8 @@ def _run(tensors, names, beta, lam, relu_power, normalize, branches, q_offset=No
     ops._check_inputs(tensors, names, kv_from=kv_from)
     ref = tensors[0]
     off = _offset(q_offset, ref.shape[2], tensors[kv_from].shape[2])
-    if ref.shape[-1] not in (64, 128):
-        raise ValueError(f"head_dim must be 64 or 128, got {ref.shape[-1]}")
+    d = ref.shape[-1]
+    dk = _head_dim(d)
     p = _power(relu_power)
     dev = ref.device
     cdt = _COMPUTE.get(ref.dtype)
@@ -76,12 +100,16 @@ def _run(tensors, names, beta, lam, relu_power, normalize, branches, q_offset=No
         if lam_t is not None:
             zero = zero + lam_t * 0.0
         return torch.zeros_like(ref) + zero
-    xs = [t if t.dtype == cdt else t.to(cdt) for t in tensors]
+    xs = [_pad(t if t.dtype == cdt else t.to(cdt), dk) for t in tensors]
+    if dk != d:  # same tau at the padded width
+        beta_t = beta_t * math.sqrt(dk / d)
     if branches == 2:
         q1, q2, k1, k2, v = xs
     else:
         (q1, k1, v), q2, k2 = xs, None, None
     out = ops.TDAFunction.apply(q1, k1, q2, k2, v, beta_t, lam_t, p, bool(normalize), branches, off)
+    if dk != d:
+        out = out[..., :d]
     return out if out.dtype == ref.dtype else out.to(ref.dtype)
 
 
@@ -118,16 +146,19 @@ class ThresholdRelaFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, beta, relu_power):
         ops._check_inputs((q, k, v), ("q", "k", "v"), kv_from=1)
-        if q.shape[-1] not in (64, 128):
-            raise ValueError(f"head_dim must be 64 or 128, got {q.shape[-1]}")
+        d = q.shape[-1]
+        dk = _head_dim(d)
         p = _power(relu_power)
         cdt = _COMPUTE.get(q.dtype)
         if cdt is None:
             raise ValueError(f"unsupported dtype {q.dtype}")
         off = _offset(None, q.shape[2], k.shape[2])
         beta_t = _scalar(beta, q.device, "beta").detach()
-        qc, kc, vc = (t if t.dtype == cdt else t.to(cdt) for t in (q, k, v))
+        if dk != d:  # same tau at the padded width
+            beta_t = beta_t * math.sqrt(dk / d)
+        qc, kc, vc = (_pad(t if t.dtype == cdt else t.to(cdt), dk) for t in (q, k, v))
         ctx.dtype = q.dtype
+        ctx.d = d
         ctx.cfg = (p, off)
         if any(t.numel() == 0 for t in (q, k, v)):  # no query rows or no keys: the output is 0
             ctx.empty = True
@@ -145,6 +176,7 @@ class ThresholdRelaFunction(torch.autograd.Function):
                           pairs=pairs, zero=gbuf)
         ctx.save_for_backward(qc, kc, vc, beta_t, occ, pairs, *grads)
         ctx.zeroed = gbuf is not None
+        out = out[..., :d] if dk != d else out
         return out if out.dtype == q.dtype else out.to(q.dtype)
 
     @staticmethod
@@ -153,9 +185,12 @@ class ThresholdRelaFunction(torch.autograd.Function):
             return None, None, None, None, None
         qc, kc, vc, beta_t, occ, pairs, *grads = ctx.saved_tensors
         p, off = ctx.cfg
-        dq, dk, _, _, dv, _, _ = ops.backward(qc, kc, None, None, vc, dout.to(qc.dtype), beta_t, None, p, False, 1,
+        d = ctx.d
+        dout = _pad(dout.to(qc.dtype), qc.shape[-1])
+        dq, dk, _, _, dv, _, _ = ops.backward(qc, kc, None, None, vc, dout, beta_t, None, p, False, 1,
                                               None, occ, q_offset=off, pairs=pairs,
                                               grads=grads if ctx.zeroed else None)
+        dq, dk, dv = (g[..., :d] if g.shape[-1] != d else g for g in (dq, dk, dv))
         dq, dk, dv = (g if g.dtype == ctx.dtype else g.to(ctx.dtype) for g in (dq, dk, dv))
         ng = ctx.needs_input_grad
         return dq if ng[0] else None, dk if ng[1] else None, dv if ng[2] else None, None, None

@@ -181,8 +181,11 @@ size_t tda_fwd_workspace_bytes_kv(int64_t batch, int64_t heads, int64_t seq_len,
 }
 
 size_t tda_fwd_workspace_bytes_for(const tda_fwd_args* a) {
-  if (!a || check_common(common_of(*a)) != TDA_OK) return 0;
-  const Common c = common_of(*a);
+  if (!a) return 0;
+  // the shape fields decide the size; the device pointers (beta, lambda) are not needed yet
+  Common c = common_of(*a);
+  c.beta = c.lambda_param = reinterpret_cast<const float*>(a);
+  if (check_common(c) != TDA_OK) return 0;
   return (size_t)fwd_ws_bytes(a->batch * a->heads, a->seq_len, c.seq_len_kv, a->branches, k8_row_bytes(*a));
 }
 
