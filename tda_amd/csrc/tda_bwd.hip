@@ -18,6 +18,7 @@
 // forward's tile-occupancy bitmask is given, both passes visit only tiles with a non-zero
 // score: A = 0 on a tile implies G = 0 there, so nothing else contributes.
 #include "tda_common.hpp"
+#include "tda_fin.hpp"
 #include "tda_params.hpp"
 #include "tda_pos.hpp"
 
@@ -421,50 +422,18 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
 }
 
 // Deterministic second stage: fixed-order fp64 sum of the per-wave partials.
-constexpr int kFinThreads = 1024;
+constexpr int kFinThreads = kFinSlices;  // one thread per slice
+// The partials in the fixed order of tda_fin.hpp (bwd_tiles computes the same bits).
 __global__ void __launch_bounds__(kFinThreads) bwd_finish(const float* ws, int64_t items, const float* lam,
                                                           float* dbeta, float* dlam, int branches) {
-  // Each thread issues all its 16-byte loads (two (dbeta, dlambda) pairs each) before summing;
-  // the reduction order is fixed, so the result is bitwise reproducible.
-  __shared__ double sb[kFinThreads], sl[kFinThreads];
-  constexpr int U = 8;  // loads in flight per thread
-  const int64_t nq = items / 2;
-  const f32x4* w4 = reinterpret_cast<const f32x4*>(ws);
-  double a = 0.0, c = 0.0;
-  for (int64_t k0 = 0; k0 < nq; k0 += (int64_t)U * kFinThreads) {
-    f32x4 v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t k = k0 + (int64_t)u * kFinThreads + threadIdx.x;
-      v[u] = k < nq ? w4[k] : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      a += (double)v[u][0] + (double)v[u][2];
-      c += (double)v[u][1] + (double)v[u][3];
-    }
-  }
-  if ((items & 1) && threadIdx.x == 0) {
-    a += (double)ws[2 * items - 2];
-    c += (double)ws[2 * items - 1];
-  }
-  sb[threadIdx.x] = a;
-  sl[threadIdx.x] = c;
+  __shared__ double sl[2 * kFinSlices];
+  const double2 v = fin_slice_sum(ws, items, (int)threadIdx.x);
+  sl[2 * threadIdx.x] = v.x;
+  sl[2 * threadIdx.x + 1] = v.y;
   __syncthreads();
-  for (int o = kFinThreads / 2; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) {
-      sb[threadIdx.x] += sb[threadIdx.x + o];
-      sl[threadIdx.x] += sl[threadIdx.x + o];
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    if (dbeta) dbeta[0] = (float)sb[0];
-    if (dlam && branches == 2) {
-      const float lv = lam[0];
-      const bool gate = lv >= 0.f && lv <= 1.f;  // torch.clamp passes the gradient on [0, 1]
-      dlam[0] = gate ? (float)sl[0] : 0.f;
-    }
+  if (threadIdx.x < 64) {
+    const double2 t = fin_total(sl);
+    if (threadIdx.x == 0) fin_store(t, lam, dbeta, dlam, branches);
   }
 }
 

@@ -26,6 +26,7 @@
 // the LDS transpose read, as transposed fragments.  dbeta / dlambda partials: one pair per
 // (branch, query tile), summed in a fixed order by bwd_finish.
 #include "tda_common.hpp"
+#include "tda_fin.hpp"
 #include "tda_params.hpp"
 #include "tda_pos.hpp"
 
@@ -1165,11 +1166,52 @@ __global__ void __launch_bounds__(64) bwd_dkv_fast(BwdParams P, int per_wave) {
   for (; run; run &= run - 1u) bwd_dkv_tile<D, BR, PK, NORM>(P, W, first + __builtin_ctz(run));
 }
 
+// ------------------------------------------------------------------ both tile passes, one launch
+// With pair lists and the key-tile queue: single-wave workgroups that first run the
+// query-major tile pass for the lists that did not fit (64 list counts tested per round, the
+// lists in order) and then take the key tiles the key-major pair pass queued.  The query-major
+// items do not depend on the key-major pass, so they run after it here, which saves the launch
+// of a separate query-major tile pass.  (Adding the dbeta / dlambda sum here, by the last
+// workgroup to finish, cost more than the launch it saved: every workgroup's release fence
+// wrote back its XCD's L2.)
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(64) bwd_tiles(BwdParams P) {
+  __shared__ __attribute__((aligned(16))) BwdWaveLds<D> W;
+  const int l = lane_id();
+  const int BH = P.B * P.H;
+  const int64_t lists = (int64_t)BR * BH * P.nqt, lists_h = (int64_t)BH * P.nqt;
+  const uint32_t* counts = P.pairs + pair_lists(BR, BH, P.nqt) * 4 * kPairCap;
+  for (int64_t f = (int64_t)blockIdx.x * 64; f < lists; f += (int64_t)gridDim.x * 64) {
+    const bool need = f + l < lists && counts[f + l] > (uint32_t)kPairCap;
+    for (uint64_t m = wave_ballot(need); m; m &= m - 1ull) {
+      const int64_t lx = f + __builtin_ctzll(m);  // list (branch, head, query tile) -> tile-pass item
+      const int br = (int)(lx / lists_h);
+      const int64_t rem = lx % lists_h;
+      const int bh = (int)(rem / P.nqt), qt = (int)(rem % P.nqt);
+      const int64_t rest = (int64_t)(P.nqt - 1 - qt) * BH + bh;
+      bwd_dq_tile<D, BR, PK, NORM>(P, W, BR == 2 ? 2 * rest + br : rest);
+    }
+  }
+  const uint32_t queued = P.dkvq[0];
+  for (uint32_t k = blockIdx.x; k < queued; k += gridDim.x) bwd_dkv_tile<D, BR, PK, NORM>(P, W, P.dkvq[1 + k]);
+}
+
 // ------------------------------------------------------------------ dispatch
 template <int D, int BR, int PK, bool NORM>
 static int launch_t(const BwdParams& p, void* stream) {
   const int64_t qitems = (int64_t)BR * p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
+  if (p.pairs && p.dkvq) {  // the pair passes, both tile passes in one launch, the sum
+    hipLaunchKernelGGL((bwd_dq_pairs<D, BR, PK, NORM>), dim3((unsigned)qitems), dim3(64), 0, s, p);
+    launched(s, "bwd_dq_pairs");
+    hipLaunchKernelGGL((bwd_dkv_pairs<D, BR, PK, NORM>), dim3((unsigned)kitems), dim3(64), 0, s, p);
+    launched(s, "bwd_dkv_pairs");
+    // one wave per SIMD (the key-major tile body's registers)
+    hipLaunchKernelGGL((bwd_tiles<D, BR, PK, NORM>), dim3(1024u), dim3(64), 0, s, p);
+    launched(s, "bwd_tiles");
+    const int e = (int)hipGetLastError();
+    return e ? e : launch_bwd_finish(p, BR, qitems, stream);
+  }
   if (p.pairs) {
     hipLaunchKernelGGL((bwd_dq_pairs<D, BR, PK, NORM>), dim3((unsigned)qitems), dim3(64), 0, s, p);
     launched(s, "bwd_dq_pairs");

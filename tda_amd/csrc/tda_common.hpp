@@ -140,6 +140,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ unsigned long long wave_ballot(bool b) { return __ballot(b); }
 
+
 // Sum / maximum over aligned groups of W lanes (W = 2, 4, 8 or 16) by DPP moves within a 16-lane
 // row (no LDS round trip): quad_perm [1,0,3,2] and [2,3,0,1] pair lanes within quads, then
 // row_half_mirror (lane i <- 7 - i) and row_mirror (i <- 15 - i) pair quads and half-rows.  Each

@@ -38,6 +38,8 @@ constexpr uint32_t kPairOverflow = 0xffffffffu;  // count of a list the forward 
 // atomic adds).  A count above kCandCap marks a list that did not fit: the exact pass then walks
 // the bitmask tiles of that query tile.
 constexpr int kCandCap = 32;
+// Slices of the fixed-order dbeta / dlambda sum (tda_fin.hpp, bwd_finish).
+constexpr int kFinSlices = 1024;
 constexpr int64_t cand_words(int64_t lists) { return lists * (1 + kCandCap); }
 
 // Positions: query row i of a head sits at absolute position qoff + i and sees the keys

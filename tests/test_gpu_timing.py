@@ -53,7 +53,9 @@ def test_backward_and_fp32_launches():
         timer.arm()
         got = ops.backward(q1, k1, q2, k2, v, do, beta, lam, 2.0, True, 2, norms, occ, pairs=pairs)
         names = timer.collect()
-    assert names == ["bwd_dq_pairs", "bwd_dq_fast", "bwd_dkv_pairs", "bwd_dkv_fast", "bwd_finish"]
+    # with pair lists (and a key-tile queue that holds every key tile): the two pair passes, both
+    # tile passes in one launch, then the dbeta / dlambda sum
+    assert names == ["bwd_dq_pairs", "bwd_dkv_pairs", "bwd_tiles", "bwd_finish"]
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
     x = [t.float() for t in (q1, k1, v)]
