@@ -1260,25 +1260,32 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
     if (P.pairs && l == 0) P.pairs[pair_lists(P.nbr, BH, nqt) * 4 * kPairCap + lidx] = npairs;
   }
 
-  // Output rows through LDS (the swizzled V tile): lane (n, g) holds elements 32c + crow(r, g) of
-  // row n, i.e. half g of chunk 4c + u for values 4u .. 4u + 3; stores then cover whole rows
-  // (streaming stores, as in fwd_pv: nothing here reads the output again).
+  // Output rows through LDS (the V tile's space): lane (n, g) holds elements 32c + crow(r, g) of
+  // row n, i.e. half g of chunk k = 4c + u for values 4u .. 4u + 3.  Its 8 bytes go to half-chunk
+  // 2 (k ^ osig(n)) + (g ^ otau(n)) of the row: the two halves of chunk k share a 16-byte slot
+  // (swapped when otau(n) = 1) and the 32 rows of a half-wave's store fall on distinct banks (with
+  // the tile's 16-byte swizzle they met in pairs, two extra cycles per store); the row reads then
+  // take 16-byte slots, and the stores cover whole rows (streaming stores, as in fwd_pv: nothing
+  // here reads the output again).
+  auto osig = [](int r) { return (r >> 1) & (CPR - 1); };
+  auto otau = [](int r) { return D == 128 ? (r & 1) : ((r >> 4) & 1); };
   wave_lds_sync();
 #pragma unroll
   for (int c = 0; c < ND; ++c)
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      store4(vt + n32 * D + 8 * ((4 * c + u) ^ bswz<D>(n32)) + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2],
-             O[c][4 * u + 3]);
+      store4(vt + n32 * D + 4 * (2 * ((4 * c + u) ^ osig(n32)) + (g ^ otau(n32))), O[c][4 * u], O[c][4 * u + 1],
+             O[c][4 * u + 2], O[c][4 * u + 3]);
   wave_lds_sync();
   {
     bf16* ohead = (bf16*)P.out + (int64_t)b * P.s[F_OUT][0] + (int64_t)h * P.s[F_OUT][1];
 #pragma unroll
     for (int i = 0; i < VL; ++i) {
       const int r = vrow + RPI * i, row = 32 * qt + r;
+      u32x4 w = *reinterpret_cast<const u32x4*>(vt + r * D + 8 * (vch ^ osig(r)));
+      if (otau(r)) w = u32x4{w[2], w[3], w[0], w[1]};
       if (row < Nq)
-        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(vt + r * D + 8 * (vch ^ bswz<D>(r))),
-                                    reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch));
+        __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch));
     }
   }
   if (P.stats) {
