@@ -764,8 +764,7 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
 #pragma unroll
     for (int br = 0; br < BR; ++br) {
       uint32_t ub = match && c.br == br ? 1u << (c.key & 31) : 0u;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) ub |= (uint32_t)__shfl_xor((int)ub, o);
+      ub = wave_or(ub);
       used[br] |= ub;
     }
     np += (uint32_t)__builtin_popcountll(mm);

@@ -131,13 +131,6 @@ __device__ __forceinline__ float row_sumsq(const typename Pol::frag (&f)[NT]) {
   return a + __shfl_xor(a, 32);
 }
 
-// Deterministic wave-wide sum (fixed butterfly order).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
 __device__ __forceinline__ unsigned long long wave_ballot(bool b) { return __ballot(b); }
 
 
@@ -157,6 +150,22 @@ __device__ __forceinline__ float group_sum(float x) {
   if constexpr (W >= 8) x += dpp_mov<0x141>(x);
   if constexpr (W >= 16) x += dpp_mov<0x140>(x);
   return x;
+}
+// Wave-wide sum, deterministic: DPP within each 16-lane row, then two lane swaps (every lane
+// ends with the same bits).  Call with every lane active.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = group_sum<16>(v);
+  v += __shfl_xor(v, 16);
+  return v + __shfl_xor(v, 32);
+}
+// Wave-wide OR, the same way.
+__device__ __forceinline__ uint32_t wave_or(uint32_t v) {
+  v |= (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+  v |= (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+  v |= (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);
+  v |= (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);
+  v |= (uint32_t)__shfl_xor((int)v, 16);
+  return v | (uint32_t)__shfl_xor((int)v, 32);
 }
 template <int W>
 __device__ __forceinline__ float group_max(float x) {
