@@ -130,12 +130,13 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
   {
     const T* r1 = qvalid ? q1.row(b, h, i) : nullptr;
     const T* ro = qvalid ? dO.row(b, h, i) : nullptr;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) { Q1[t] = Pol::load_row(r1, t, g); DO[t] = Pol::load_row(ro, t, g); }
+    {
+      Pol::template load_rows<NT>(r1, g, Q1);
+      Pol::template load_rows<NT>(ro, g, DO);
+    }
     if constexpr (BR == 2) {
       const T* r2 = qvalid ? q2.row(b, h, i) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) Q2[t] = Pol::load_row(r2, t, g);
+      Pol::template load_rows<NT>(r2, g, Q2);
     }
   }
   float rq1 = 1.f, rq2 = 1.f;
@@ -177,18 +178,15 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
     f32x16 S1 = f32x16{}, S2 = f32x16{}, Dp = f32x16{};
     {
       const T* r = (j < Nk) ? k1.row(b, h, j) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) S1 = Pol::mma(Pol::load_row(r, t, g), Q1[t], S1);
+      S1 = Pol::template mma_row<NT>(r, g, Q1, S1);
     }
     if constexpr (BR == 2) {
       const T* r = (j < Nk) ? k2.row(b, h, j) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) S2 = Pol::mma(Pol::load_row(r, t, g), Q2[t], S2);
+      S2 = Pol::template mma_row<NT>(r, g, Q2, S2);
     }
     {
       const T* r = (j < Nk) ? vv.row(b, h, j) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) Dp = Pol::mma(Pol::load_row(r, t, g), DO[t], Dp);
+      Dp = Pol::template mma_row<NT>(r, g, DO, Dp);
     }
     f32x16 E1, E2;
     bool any = false;
@@ -294,12 +292,13 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
   {
     const T* r1 = kvalid ? k1.row(b, h, j) : nullptr;
     const T* rv = kvalid ? vv.row(b, h, j) : nullptr;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) { K1[t] = Pol::load_row(r1, t, g); V[t] = Pol::load_row(rv, t, g); }
+    {
+      Pol::template load_rows<NT>(r1, g, K1);
+      Pol::template load_rows<NT>(rv, g, V);
+    }
     if constexpr (BR == 2) {
       const T* r2 = kvalid ? k2.row(b, h, j) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) K2[t] = Pol::load_row(r2, t, g);
+      Pol::template load_rows<NT>(r2, g, K2);
     }
   }
   float rk1 = 1.f, rk2 = 1.f;
@@ -339,18 +338,15 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
     f32x16 S1 = f32x16{}, S2 = f32x16{}, Dp = f32x16{};
     {
       const T* r = (ia < Nq) ? q1.row(b, h, ia) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) S1 = Pol::mma(Pol::load_row(r, t, g), K1[t], S1);
+      S1 = Pol::template mma_row<NT>(r, g, K1, S1);
     }
     if constexpr (BR == 2) {
       const T* r = (ia < Nq) ? q2.row(b, h, ia) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) S2 = Pol::mma(Pol::load_row(r, t, g), K2[t], S2);
+      S2 = Pol::template mma_row<NT>(r, g, K2, S2);
     }
     {
       const T* r = (ia < Nq) ? dO.row(b, h, ia) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) Dp = Pol::mma(Pol::load_row(r, t, g), V[t], Dp);
+      Dp = Pol::template mma_row<NT>(r, g, V, Dp);
     }
     f32x16 EV, E1, E2;
     bool any = false;

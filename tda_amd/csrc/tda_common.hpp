@@ -6,7 +6,8 @@
 //   A (M x K): lane l holds row m = l % 32 and E consecutive K indices starting at E*g.
 //   B (K x N): lane l holds column n = l % 32 and E consecutive K indices starting at E*g.
 // bf16 uses v_mfma_f32_32x32x16_bf16 (K = 16 per instruction, E = 8 elements per lane);
-// fp32 uses v_mfma_f32_32x32x2f32 (K = 2, E = 1).
+// fp32 uses v_mfma_f32_32x32x2f32 (K = 2, E = 1; over d its row fragments take the elements in
+// another order, see PolF32::load_rows).
 //
 // Two operand shapes appear in every kernel:
 //   * "row fragments": a 32-row tile of a (N, d) tensor contracted over d.  Lane (m, g) holds
@@ -53,6 +54,19 @@ struct PolBF16 {
     if (!row) return zero();
     return *reinterpret_cast<const frag*>(row + KS * t + E * g);
   }
+  // All NT = D / KS steps of a row.
+  template <int NT>
+  __device__ __forceinline__ static void load_rows(const T* row, int g, frag (&out)[NT]) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) out[t] = load_row(row, t, g);
+  }
+  // acc += (row fragments, streamed from `row`) x (resident fragments b), over the NT steps.
+  template <int NT>
+  __device__ __forceinline__ static f32x16 mma_row(const T* row, int g, const frag (&b)[NT], f32x16 acc) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc = mma(load_row(row, t, g), b[t], acc);
+    return acc;
+  }
   // Pack values [s*E, s*E+E) of a C tile into a B operand (round to nearest even).
   __device__ __forceinline__ static frag pack_c(const f32x16& c, int s) {
     frag f;
@@ -77,9 +91,36 @@ struct PolF32 {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
   }
   __device__ __forceinline__ static frag zero() { return 0.f; }
-  __device__ __forceinline__ static frag load_row(const T* row, int t, int g) {
-    if (!row) return 0.f;
-    return row[KS * t + g];
+  // All NT = D / 2 steps of a row: lane half g takes elements g NT .. g NT + NT - 1, one per
+  // step (a contraction over d may assign the elements to steps in any order, the same for both
+  // operands; every fp32 contraction over d takes both from load_rows).  16-byte loads.
+  template <int NT>
+  __device__ __forceinline__ static void load_rows(const T* row, int g, frag (&out)[NT]) {
+    static_assert(NT % 4 == 0, "whole 16-byte vectors");
+    if (!row) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) out[t] = 0.f;
+      return;
+    }
+    const f32x4* p = reinterpret_cast<const f32x4*>(row + g * NT);
+#pragma unroll
+    for (int m = 0; m < NT / 4; ++m) {
+      const f32x4 v = p[m];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[4 * m + e] = v[e];
+    }
+  }
+  // acc += (row fragments, streamed from `row` four steps per 16-byte load) x b, over NT steps.
+  template <int NT>
+  __device__ __forceinline__ static f32x16 mma_row(const T* row, int g, const frag (&b)[NT], f32x16 acc) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(row ? row + g * NT : row);
+#pragma unroll
+    for (int m = 0; m < NT / 4; ++m) {
+      const f32x4 v = row ? p[m] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = mma(v[e], b[4 * m + e], acc);
+    }
+    return acc;
   }
   __device__ __forceinline__ static frag pack_c(const f32x16& c, int s) { return c[s]; }
   __device__ __forceinline__ static float sumsq(frag f) { return f * f; }

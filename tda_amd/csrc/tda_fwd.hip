@@ -57,12 +57,10 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
   frag Q1[NT], Q2[NT];
   {
     const T* r1 = qvalid ? q1.row(b, h, i) : nullptr;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) Q1[t] = Pol::load_row(r1, t, g);
+    Pol::template load_rows<NT>(r1, g, Q1);
     if constexpr (BR == 2) {
       const T* r2 = qvalid ? q2.row(b, h, i) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) Q2[t] = Pol::load_row(r2, t, g);
+      Pol::template load_rows<NT>(r2, g, Q2);
     }
   }
   float rq1 = 1.f, rq2 = 1.f;
@@ -102,8 +100,7 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
     {
       frag K1[NT];
       const T* r1 = (j < Nk) ? k1.row(b, h, j) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) K1[t] = Pol::load_row(r1, t, g);
+      Pol::template load_rows<NT>(r1, g, K1);
 #pragma unroll
       for (int t = 0; t < NT; ++t) S1 = Pol::mma(K1[t], Q1[t], S1);
       if constexpr (NORM) {
@@ -116,8 +113,7 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
     if constexpr (BR == 2) {
       frag K2[NT];
       const T* r2 = (j < Nk) ? k2.row(b, h, j) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) K2[t] = Pol::load_row(r2, t, g);
+      Pol::template load_rows<NT>(r2, g, K2);
 #pragma unroll
       for (int t = 0; t < NT; ++t) S2 = Pol::mma(K2[t], Q2[t], S2);
       if constexpr (NORM) {
@@ -202,14 +198,12 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
         const int j = 32 * kt + n32;
         frag K[NT];
         const T* r1 = (j < Nk) ? k1.row(b, h, j) : nullptr;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) K[t] = Pol::load_row(r1, t, g);
+        Pol::template load_rows<NT>(r1, g, K);
         const float rka = inv_norm(row_sumsq<Pol, NT>(K));
         if (g == 0 && j < Nk) P.norms[norm_base(P, N_K1, bh) + j] = rka;
         if constexpr (BR == 2) {
           const T* r2 = (j < Nk) ? k2.row(b, h, j) : nullptr;
-#pragma unroll
-          for (int t = 0; t < NT; ++t) K[t] = Pol::load_row(r2, t, g);
+          Pol::template load_rows<NT>(r2, g, K);
           const float rkb = inv_norm(row_sumsq<Pol, NT>(K));
           if (g == 0 && j < Nk) P.norms[norm_base(P, N_K2, bh) + j] = rkb;
         }
