@@ -18,11 +18,12 @@
 //               are all zero, never drop a non-zero one.  No V and no output accumulators, so
 //               several waves share a SIMD.  With normalisation it also lists each query
 //               tile's candidate keys (the keys of its passing lanes).
-//   fwd_pv_cand (normalize) one wave per query tile whose candidate lists fit: the score tile
-//               of its rows against the candidate keys (the same MFMA sequence and operand
-//               values as fwd_pv, so the same scores), the exact weights and out += coef A V
-//               over the candidates' V rows; the bitmask row is rewritten exactly.  Query
-//               tiles whose lists overflow go to a queue for fwd_pv.
+//   fwd_pv_cand (normalize) one wave per branch of a query tile whose candidate lists fit:
+//               the score tile of its rows against the candidate keys (the same MFMA sequence
+//               and operand values as fwd_pv, so the same scores), the exact weights and
+//               coef A V over the candidates' V rows, the branches' sums added through LDS;
+//               the bitmask row is rewritten exactly.  Query tiles whose lists overflow go to
+//               a queue for fwd_pv.
 //   fwd_pv      the tile pass, one wave per query tile (every tile without normalisation, the
 //               queued ones with it): walks the set bits of both branches, recomputes the
 //               score tile, forms the exact weights ReLU(x)^p with the causal mask, and
@@ -1068,21 +1069,28 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
 // candidate c, rows past the count zero) is computed with the MFMA sequence of fwd_pv, its
 // operands loaded straight from the rows (the same values in the same operands: bitwise the same
 // scores); the candidates' V rows go to a swizzled LDS tile by direct loads, and the exact
-// weights with the causal mask accumulate out += coef A V as in fwd_pv.  One gather round
-// per branch replaces one per kept key tile.  The bitmask row is rewritten from the key tiles
+// weights with the causal mask accumulate coef A V as in fwd_pv.  One gather round per branch
+// replaces one per kept key tile.  With two branches each runs on its own wave of the workgroup
+// (half the dependent loads per wave; LDS per wave as with one) and the second wave's sum is
+// added to the first's through LDS before the first stores the rows.  The bitmask row is rewritten from the key tiles
 // holding a non-zero weight; the pair list takes the non-zero weights in the order (value r,
 // lane).
 template <int D, int BR, int PK>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fwd_pv_cand(FwdParams P) {
+__global__ void __launch_bounds__(64 * BR) __attribute__((amdgpu_waves_per_eu(3))) fwd_pv_cand(FwdParams P) {
   constexpr int NT = D / 16, ND = D / 32;
   constexpr int CPR = D / 8;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;  // rows per load instruction
   constexpr int VL = 32 / RPI;   // load instructions per tile
-  __shared__ __attribute__((aligned(16))) bf16 vt[32 * D];  // V rows, chunk-swizzled (bswz)
-  __shared__ __attribute__((aligned(16))) int ckey[32];     // candidate keys (padding: -1)
-  __shared__ __attribute__((aligned(16))) float crk[32];   // their inverse norms
+  // one wave per branch, each with its own tiles
+  __shared__ __attribute__((aligned(16))) bf16 vts[BR][32 * D];  // V rows, chunk-swizzled (bswz)
+  __shared__ __attribute__((aligned(16))) int ckeys[BR][32];     // candidate keys (padding: -1)
+  __shared__ __attribute__((aligned(16))) float crks[BR][32];   // their inverse norms
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = BR == 2 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;  // = its branch
+  bf16* vt = vts[wv];
+  int* ckey = ckeys[wv];
+  float* crk = crks[wv];
   const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
   int bh, qt;
   {
@@ -1109,8 +1117,8 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
   bool fit = true;
 #pragma unroll
   for (int br = 0; br < BR; ++br) fit = fit && nc[br] <= (uint32_t)kCandCap;
-  if (!fit) {  // fwd_pv walks the bitmask tiles
-    if (l == 0) P.pvq[1 + atomicAdd(P.pvq, 1u)] = (uint32_t)(bh * nqt + qt);
+  if (!fit) {  // fwd_pv walks the bitmask tiles (both waves leave: the test is the same)
+    if (l == 0 && wv == 0) P.pvq[1 + atomicAdd(P.pvq, 1u)] = (uint32_t)(bh * nqt + qt);
     return;
   }
   if (P.screen_items > (Nq + 255) / 256) {
@@ -1146,8 +1154,8 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
   for (int c = 0; c < ND; ++c) O[c] = f32x16{};
   unsigned computed = 0, checked = 0;
 
-#pragma unroll
-  for (int br = 0; br < BR; ++br) {
+  {
+    const int br = wv;
     const uint32_t n = nc[br];
     const int64_t lidx = ((int64_t)br * BH + bh) * nqt + qt;
     uint32_t* orow = P.occ + lidx * P.occ_w;
@@ -1177,7 +1185,7 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
         Q[t] = *reinterpret_cast<const bf16x8*>(qrow + 16 * t + 8 * g);
         K[t] = *reinterpret_cast<const bf16x8*>(krow + 16 * t + 8 * g);
       }
-      wave_lds_sync();  // the previous branch's reads of the tile are done
+      wave_lds_sync();
 #pragma unroll
       for (int u = 0; u < VL; ++u) {
         const int r = u * RPI + l / CPR;
@@ -1255,9 +1263,35 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
         }
         computed += (unsigned)__builtin_popcount(word);
       }
-      wave_lds_sync();  // the tiles are reused by the next branch and the output
+      wave_lds_sync();  // the tile is reused by the output
     }
     if (P.pairs && l == 0) P.pairs[pair_lists(P.nbr, BH, nqt) * 4 * kPairCap + lidx] = npairs;
+  }
+  if (P.stats) {
+    const float cs = wave_sum((float)computed), ks = wave_sum((float)checked);
+    if (l == 0 && ks > 0.f) {
+      atomicAdd(P.stats + 1, (unsigned long long)cs);
+      atomicAdd(P.stats + 2, (unsigned long long)ks);
+    }
+  }
+  if constexpr (BR == 2) {
+    // out = O (branch 1's wave, -lambda A2 V) + O (branch 0's wave, A1 V): the second through
+    // the (now unused) V tiles of both waves, then the first wave stores the rows
+    static_assert(BR * 32 * D * 2 >= 64 * 16 * ND * 4, "accumulators fit the tiles");
+    float* xch = reinterpret_cast<float*>(&vts[0][0]);
+    __syncthreads();  // both waves are done with their tiles
+    if (wv == 1) {
+#pragma unroll
+      for (int c = 0; c < ND; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xch[(16 * c + r) * 64 + l] = O[c][r];
+    }
+    __syncthreads();
+    if (wv == 1) return;
+#pragma unroll
+    for (int c = 0; c < ND; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) O[c][r] += xch[(16 * c + r) * 64 + l];
   }
 
   // Output rows through LDS (the V tile's space): lane (n, g) holds elements 32c + crow(r, g) of
@@ -1288,13 +1322,6 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) fw
         __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch));
     }
   }
-  if (P.stats) {
-    const float cs = wave_sum((float)computed), ks = wave_sum((float)checked);
-    if (l == 0 && ks > 0.f) {
-      atomicAdd(P.stats + 1, (unsigned long long)cs);
-      atomicAdd(P.stats + 2, (unsigned long long)ks);
-    }
-  }
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -1316,7 +1343,7 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   }
   launched(s, "fwd_screen");
   if (NORM && p.cand) {
-    hipLaunchKernelGGL((fwd_pv_cand<D, BR, PK>), dim3((unsigned)(BH * p.nqt)), dim3(64), 0, s, p);
+    hipLaunchKernelGGL((fwd_pv_cand<D, BR, PK>), dim3((unsigned)(BH * p.nqt)), dim3(64 * BR), 0, s, p);
     launched(s, "fwd_pv_cand");
   }
   if (NORM && p.cand) {  // the query tiles the candidate pass could not take, from its queue
