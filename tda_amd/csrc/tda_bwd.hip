@@ -419,7 +419,7 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
 
 // Deterministic second stage: fixed-order fp64 sum of the per-wave partials.
 constexpr int kFinThreads = kFinSlices;  // one thread per slice
-// The partials in the fixed order of tda_fin.hpp (bwd_tiles computes the same bits).
+// The partials in the fixed order of tda_fin.hpp: kFinSlices slice sums, then one wave's total.
 __global__ void __launch_bounds__(kFinThreads) bwd_finish(const float* ws, int64_t items, const float* lam,
                                                           float* dbeta, float* dlam, int branches) {
   __shared__ double sl[2 * kFinSlices];

@@ -26,7 +26,6 @@
 // the LDS transpose read, as transposed fragments.  dbeta / dlambda partials: one pair per
 // (branch, query tile), summed in a fixed order by bwd_finish.
 #include "tda_common.hpp"
-#include "tda_fin.hpp"
 #include "tda_params.hpp"
 #include "tda_pos.hpp"
 
