@@ -306,12 +306,15 @@ __device__ __forceinline__ int max16i(const i32x16& v) {
 // reduction and its stores after the last.  It also zeroes the screen's candidate counts and the
 // tile-pass queue count.  (Eight elements per lane, half-size stores, measured 56 us against 46 at
 // B4 H16 N4096 d128, two branches.)
-#ifndef TDA_KN_GROUPS
-#define TDA_KN_GROUPS 4
-#endif
-constexpr int KN_GROUPS = TDA_KN_GROUPS;  // row groups per wave
+// Row groups per wave: 4 at d = 128 (64 rows), 2 at d = 64 (32 rows; measured 11.2 us against
+// 12.1 with 4 at B4 H16 N2048 d64, one branch, where the grid is small).
+template <int D>
+constexpr int kn_groups() {
+  return D == 64 ? 2 : 4;
+}
 template <int D>
 __global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
+  constexpr int KN_GROUPS = kn_groups<D>();
   constexpr int LPR = D / 16, RPG = 64 / LPR, ROWS = RPG * KN_GROUPS;
   const int l = lane_id(), sub = l % LPR;
   const int BH = P.B * P.H, N = P.Nk;
@@ -1329,7 +1332,7 @@ template <int D, int BR, int PK, bool NORM>
 int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   const int BH = p.B * p.H;
   if constexpr (NORM) {
-    constexpr int rows = (64 / (D / 16)) * KN_GROUPS;  // rows per wave
+    constexpr int rows = (64 / (D / 16)) * kn_groups<D>();  // rows per wave
     const int64_t waves = (int64_t)BR * BH * ((p.Nk + rows - 1) / rows);
     hipLaunchKernelGGL(key_prep<D>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, BR);
     launched(s, "key_prep");
