@@ -78,6 +78,7 @@ __device__ __forceinline__ void dma_tile_b(const bf16* rows, int64_t st, int r0,
 struct PairLanes {
   int key, row;
   float x;
+  uint32_t slot;  // the pair's column-bucket slot (kNoSlot: none)
 };
 __device__ __forceinline__ PairLanes load_pairs(const uint32_t* ent, uint32_t n) {
   const int l = lane_id();
@@ -86,7 +87,7 @@ __device__ __forceinline__ PairLanes load_pairs(const uint32_t* ent, uint32_t n)
   // x through a bit cast of the whole vector: hipcc compiled __builtin_bit_cast(float, e[2])
   // to element 0 (the key index)
   const f32x4 ef = __builtin_bit_cast(f32x4, e);
-  return PairLanes{(int)e[0], (int)e[1], ef[2]};
+  return PairLanes{(int)e[0], (int)e[1], ef[2], e[3]};
 }
 
 __device__ __forceinline__ void dma_row_vals_b(const float* vals, int r0, int n, float* dst) {
@@ -351,8 +352,8 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) bw
 // order, dq_i = sum over its pairs, in list order, of dS k_j (times the key's inverse norm with
 // normalisation), dS = coef p x^(p-1) (do_i . v_j) with x the forward's exact value; then the
 // normalize backward of the row.  Each pair's dk weight, dS (times rq_i with normalisation),
-// goes to the workspace slot of its list entry for bwd_dkv_pairs.  No LDS, no matrix cores: per
-// pair two row loads and one wave-wide dot product.
+// goes to the workspace slot of its list entry and to its column-bucket entry for
+// bwd_dkv_pairs.  No LDS, no matrix cores: per pair two row loads and one wave-wide dot product.
 template <int D>
 struct RowVec {
   static constexpr int E = D / 64;  // elements per lane
@@ -571,7 +572,11 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   finish();
   // back to list order: lane s sends its weight to the lane of its list entry
   const float wkl = __builtin_bit_cast(float, __builtin_amdgcn_ds_permute(4 * SP.e, __builtin_bit_cast(int, wks)));
-  if ((uint32_t)l < npairs) P.pws[lidx * kPairCap + l] = wkl;
+  if ((uint32_t)l < npairs) {
+    P.pws[lidx * kPairCap + l] = wkl;
+    if (P.colbuf && PL.slot < (uint32_t)kColCap)  // the dk weight of the pair's column-bucket entry
+      P.colbuf[(((int64_t)bh * P.nkt + (PL.key >> 5)) * kColCap + PL.slot) * 4 + 3] = __builtin_bit_cast(uint32_t, wkl);
+  }
   if (l == 0) {
     P.ws[2 * lidx + 0] = pb;  // slot of (branch, head, query tile), whichever pass takes it
     P.ws[2 * lidx + 1] = pl;
@@ -609,6 +614,7 @@ __device__ __forceinline__ bool column_overflows(const BwdParams& P, int bh, int
 
 // LDS slots of the key-major pair pass: pairs of one column gathered at once.
 constexpr int kColPairs = 64;
+static_assert(kColCap == kColPairs && kColCap == 64, "a column bucket: one entry per lane, as many as the slots");
 // List-load rounds of one walk step of the key-major pair pass (two lists per round).
 constexpr int kWalkRounds = 4;
 
@@ -622,15 +628,17 @@ struct ColEntry {
   float wk;    // dk weight from the query-major pair pass
 };
 
-// One wave per key tile whose column has only lists that fit.  It walks the column's lists
-// (both branches, query-tile chunks of 64, two lists per step: lanes 0-31 and 32-63) and keeps
-// the pairs with a key in this tile.  For each key row j that some pair names, in increasing
+// One wave per key tile whose column has only lists that fit.  Its pairs come from the column's
+// bucket when the forward filled one with all of them (every entry with its dk weight: one round
+// of loads), else it walks the column's lists (both branches, query-tile chunks of 64, two lists
+// per step: lanes 0-31 and 32-63) and keeps the pairs with a key in this tile.  For each key row j that some pair names, in increasing
 // order, whole-row vector work over its pairs:
 //   dv_j  += coef A_ij do_i          A_ij = x^p (x the forward's exact value)
 //   dk_j  += w_ij q_i                w_ij = coef p x^(p-1) (do_i . v_j) (times rq_i with
 //                                    normalisation), stored by the query-major pair pass
 // then the normalize backward of dk_j; the tile's other gradient rows are stored as zeros.
-// Pairs of a row meet its accumulators in walk order (chunk, branch, query tile, list entry).
+// Pairs of a row meet its accumulators in walk order (chunk, branch, query tile, list entry),
+// or, from a bucket, in the order (branch, query row).
 // Up to kColPairs pairs are gathered into LDS slots in one walk; a column with more walks its
 // lists once per named row.  No matrix cores and no V: per pair two row loads.
 template <int D, int BR, int PK, bool NORM>
@@ -743,13 +751,42 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
     return true;
   };
 
-  // ---- first walk: rows named, pairs into the slots while they fit
   uint32_t np = 0;
   unsigned visited = 0;
   uint32_t used[BR];  // key rows named by a pair, per branch
 #pragma unroll
   for (int br = 0; br < BR; ++br) used[br] = 0u;
-  const bool fits = walk([&](const ColEntry& c) {
+  // lane s < np: pair s {query row | branch << 31, key row in the tile, x, dk weight}, and the
+  // second key of the order the pairs are taken in (after the key row)
+  int pi_l = 0, pjl_l = 0;
+  float px_l = 0.f, pw_l = 0.f;
+  uint32_t k2_l = (uint32_t)l;
+
+  // ---- the column's bucket, when the forward filled it with every pair of the column (one
+  // round of loads; the pairs are then taken in the order (key row, branch, query row))
+  bool from_bucket = false;
+  if (P.colcnt && !P.stats) {
+    const int64_t col = (int64_t)bh * P.nkt + kt;
+    const uint32_t cc = (uint32_t)__builtin_amdgcn_readfirstlane((int)P.colcnt[col]);
+    const u32x4 be = *reinterpret_cast<const u32x4*>(P.colbuf + (col * kColCap + l) * 4);
+    if (!(cc & kColTaint) && cc <= (uint32_t)kColCap) {
+      from_bucket = true;
+      np = cc;
+      const bool in = (uint32_t)l < np;
+      const f32x4 bf = __builtin_bit_cast(f32x4, be);  // x, w: a bit cast of the whole vector (see load_pairs)
+      pi_l = in ? (int)be[0] : 0;
+      pjl_l = in ? (int)be[1] : 0;
+      px_l = in ? bf[2] : 0.f;
+      pw_l = in ? bf[3] : 0.f;
+      k2_l = (uint32_t)pi_l;
+#pragma unroll
+      for (int br = 0; br < BR; ++br)
+        used[br] = wave_or(in && (int)(((uint32_t)pi_l >> 31) & 1u) == br ? 1u << pjl_l : 0u);
+    }
+  }
+
+  // ---- else the first walk: rows named, pairs into the slots while they fit
+  const bool fits = from_bucket || walk([&](const ColEntry& c) {
     const bool match = c.valid && (c.key >> 5) == kt;
     const uint64_t mm = wave_ballot(match);
     visited += ((mm & 0xffffffffull) ? 1u : 0u) + ((mm >> 32) ? 1u : 0u);
@@ -836,18 +873,24 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
   };
 
   if (slotted) {
-    // The slots sorted by key row, then slot order: lane s gets the pair of rank s (lanes past
-    // np keep their own slot).  Then the pairs in that order, the loads of kRowBatch at a time
-    // in flight together; a key row is finished when the next pair names another.
-    const int sl = (uint32_t)l < np ? l : 0;
-    const int pi_l = ps_i[sl], pjl_l = ps_jl[sl];
-    const float px_l = ps_x[sl], pw_l = ps_w[sl];
+    // The pairs sorted by key row, then the second key (walk: slot order; bucket: branch and
+    // query row): lane s gets the pair of rank s (lanes past np keep their own slot).  Then the
+    // pairs in that order, the loads of kRowBatch at a time in flight together; a key row is
+    // finished when the next pair names another.
+    if (!from_bucket) {
+      const int sl = (uint32_t)l < np ? l : 0;
+      pi_l = ps_i[sl];
+      pjl_l = ps_jl[sl];
+      px_l = ps_x[sl];
+      pw_l = ps_w[sl];
+    }
     int rank = l;
     if ((uint32_t)l < np) {
       rank = 0;
       for (uint32_t f = 0; f < np; ++f) {
         const int jf = __builtin_amdgcn_readlane(pjl_l, (int)f);
-        rank += jf < pjl_l || (jf == pjl_l && (int)f < l) ? 1 : 0;
+        const uint32_t kf = (uint32_t)__builtin_amdgcn_readlane((int)k2_l, (int)f);
+        rank += jf < pjl_l || (jf == pjl_l && kf < k2_l) ? 1 : 0;
       }
     }
     const int s_i = __builtin_amdgcn_ds_permute(4 * rank, pi_l);

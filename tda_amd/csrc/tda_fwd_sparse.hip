@@ -303,9 +303,9 @@ __device__ __forceinline__ int max16i(const i32x16& v) {
 // has none.  A group of D/16 lanes reads one row (two 16-byte loads and one 16-byte int8 store per
 // lane), the row sums and maxima are DPP reductions within the group; each wave covers
 // KN_GROUPS row groups of one (branch, head) with all its loads issued before the first
-// reduction and its stores after the last.  It also zeroes the screen's candidate counts and the
-// tile-pass queue count.  (Eight elements per lane, half-size stores, measured 56 us against 46 at
-// B4 H16 N4096 d128, two branches.)
+// reduction and its stores after the last.  It also zeroes the screen's candidate counts, the
+// tile-pass queue count and the column buckets' counts.  (Eight elements per lane, half-size
+// stores, measured 56 us against 46 at B4 H16 N4096 d128, two branches.)
 // Row groups per wave: 4 at d = 128 (64 rows), 2 at d = 64 (32 rows; measured 11.2 us against
 // 12.1 with 4 at B4 H16 N2048 d64, one branch, where the grid is small).
 template <int D>
@@ -325,6 +325,8 @@ __global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
     uint32_t* counts = P.cand + lists * kCandCap;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < lists; i += nthr) counts[i] = 0u;
     if (blockIdx.x == 0 && threadIdx.x == 0) P.pvq[0] = 0u;
+    if (P.colcnt)  // the column buckets' counts (the candidate pass appends)
+      for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < (int64_t)BH * P.nkt; i += nthr) P.colcnt[i] = 0u;
   }
   if ((int64_t)wid >= (int64_t)BR * BH * wpr) return;
   const int sidx = (int)(wid / wpr), br = sidx / BH, bh = sidx % BH;
@@ -961,7 +963,7 @@ __device__ __forceinline__ void fwd_pv_tile(const FwdParams& P, bf16* vt_, bf16*
               const uint32_t slot = npairs + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
                                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
               if (hit && slot < (uint32_t)kPairCap)
-                *reinterpret_cast<u32x4*>(pent + 4 * slot) = u32x4{(uint32_t)key, (uint32_t)n32, __builtin_bit_cast(uint32_t, x), 0u};
+                *reinterpret_cast<u32x4*>(pent + 4 * slot) = u32x4{(uint32_t)key, (uint32_t)n32, __builtin_bit_cast(uint32_t, x), kNoSlot};
               npairs += (uint32_t)__builtin_popcountll(bal);
             }
           }
@@ -969,6 +971,8 @@ __device__ __forceinline__ void fwd_pv_tile(const FwdParams& P, bf16* vt_, bf16*
           keep &= ~(1u << (kt & 31));
           continue;
         }
+        // pairs of the tile pass are in no column bucket: the key-major backward walks the lists
+        if (P.colcnt && l == 0) atomicOr(P.colcnt + (int64_t)bh * P.nkt + kt, kColTaint);
         ++computed;
         const bf16x8 PF0 = PolBF16::pack_c(C, 0), PF1 = PolBF16::pack_c(C, 1);
         wave_lds_sync();
@@ -1088,12 +1092,14 @@ __global__ void __launch_bounds__(64 * BR) __attribute__((amdgpu_waves_per_eu(3)
   __shared__ __attribute__((aligned(16))) bf16 vts[BR][32 * D];  // V rows, chunk-swizzled (bswz)
   __shared__ __attribute__((aligned(16))) int ckeys[BR][32];     // candidate keys (padding: -1)
   __shared__ __attribute__((aligned(16))) float crks[BR][32];   // their inverse norms
+  __shared__ __attribute__((aligned(16))) u32x4 plists[BR][kPairCap];  // the branch's pair list
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int wv = BR == 2 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;  // = its branch
   bf16* vt = vts[wv];
   int* ckey = ckeys[wv];
   float* crk = crks[wv];
+  u32x4* plist = plists[wv];
   const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
   int bh, qt;
   {
@@ -1240,10 +1246,25 @@ __global__ void __launch_bounds__(64 * BR) __attribute__((amdgpu_waves_per_eu(3)
             const uint32_t slot = npairs + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
                                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
             if (hit && slot < (uint32_t)kPairCap)
-              *reinterpret_cast<u32x4*>(pent + 4 * slot) = u32x4{(uint32_t)key, (uint32_t)n32, __builtin_bit_cast(uint32_t, x), 0u};
+              plist[slot] = u32x4{(uint32_t)key, (uint32_t)n32, __builtin_bit_cast(uint32_t, x), kNoSlot};
             npairs += (uint32_t)__builtin_popcountll(bal);
           }
         }
+      // The list's entries, lane e for entry e: with column buckets each takes a slot in the
+      // bucket of its key tile (the adds are in flight during the products below) and the entry
+      // records it; a list past the cap taints the columns of every candidate with a non-zero
+      // weight instead (its pairs past the cap are in no list).
+      const uint32_t ne = min(npairs, (uint32_t)kPairCap);
+      u32x4 pe = u32x4{0u, 0u, 0u, kNoSlot};
+      uint32_t* ccol = P.colcnt ? P.colcnt + (int64_t)bh * P.nkt : nullptr;
+      if (pent) {
+        wave_lds_sync();
+        if ((uint32_t)l < ne) {
+          pe = plist[l];
+          if (ccol) pe[3] = atomicAdd(ccol + ((int)pe[0] >> 5), 1u) & ~kColTaint;  // the slot
+        }
+        if (ccol && npairs > (uint32_t)kPairCap && l < 32 && ((cnz >> l) & 1u)) atomicOr(ccol + (ckey[l] >> 5), kColTaint);
+      }
       if (cnz) {
         const bf16x8 PF0 = PolBF16::pack_c(C, 0), PF1 = PolBF16::pack_c(C, 1);
 #pragma unroll
@@ -1251,6 +1272,12 @@ __global__ void __launch_bounds__(64 * BR) __attribute__((amdgpu_waves_per_eu(3)
           O[c] = PolBF16::mma(tile_tr_frag<D>(vt, 0, c), PF0, O[c]);
           O[c] = PolBF16::mma(tile_tr_frag<D>(vt, 1, c), PF1, O[c]);
         }
+      }
+      if (pent && (uint32_t)l < ne) {
+        *reinterpret_cast<u32x4*>(pent + 4 * l) = pe;
+        if (ccol && pe[3] < (uint32_t)kColCap)
+          *reinterpret_cast<u32x4*>(P.colbuf + (((int64_t)bh * P.nkt + ((int)pe[0] >> 5)) * kColCap + pe[3]) * 4) =
+              u32x4{((uint32_t)(32 * qt) + pe[1]) | (br ? 0x80000000u : 0u), pe[0] & 31u, pe[2], 0u};
       }
       // the bitmask row: lane w rewrites word w from the key tiles of the candidates with a
       // non-zero weight (the screen's words cover the key tiles of all candidates, nothing else)

@@ -23,10 +23,30 @@ enum NormSlot { N_Q1 = 0, N_K1 = 1, N_Q2 = 2, N_K2 = 3 };
 // for that query tile.
 constexpr int kPairCap = 32;
 constexpr int64_t pair_lists(int64_t branches, int64_t bh, int64_t nqt) { return branches * bh * nqt; }
-constexpr int64_t pair_words(int64_t branches, int64_t bh, int64_t nqt) {
-  return pair_lists(branches, bh, nqt) * (1 + 4 * kPairCap);
-}
 constexpr uint32_t kPairOverflow = 0xffffffffu;  // count of a list the forward did not write
+
+// Column buckets (after the lists, same buffer): for each (head, key tile) the pairs of every
+// branch whose key lies in the tile, so that the backward's key-major pass reads its pairs in one
+// round instead of walking every query tile's list.  Layout (u32 words from the buffer start,
+// each part 16-byte aligned): the counts, one per column (col = bh * nkt + kt), zeroed by
+// key_prep and raised by the exact pass's atomic adds, kColTaint set when the bucket does not
+// hold every pair of the column with its dk weight (a pair list past kPairCap, pairs from the
+// tile pass); then kColCap entries per column, each 4 u32 {query row i | branch << 31, key row
+// within the tile, bits of x_ij, bits of the dk weight (written by the backward's query-major
+// pass)}, in no fixed order (appended by atomics: the reader sorts them).  The pair entry's
+// fourth word holds its bucket slot.  Sized for nkt <= nqt; used only then (bf16, normalised,
+// more than one query tile).
+constexpr int kColCap = 64;
+constexpr uint32_t kColTaint = 0x80000000u;
+constexpr uint32_t kNoSlot = 0xffffffffu;
+constexpr int64_t round4(int64_t w) { return (w + 3) / 4 * 4; }
+constexpr int64_t pair_list_words(int64_t branches, int64_t bh, int64_t nqt) {
+  return round4(pair_lists(branches, bh, nqt) * (1 + 4 * kPairCap));
+}
+constexpr int64_t col_count_words(int64_t bh, int64_t nkt) { return round4(bh * nkt); }
+constexpr int64_t pair_words(int64_t branches, int64_t bh, int64_t nqt) {
+  return pair_list_words(branches, bh, nqt) + col_count_words(bh, nqt) + bh * nqt * kColCap * 4;
+}
 
 // Candidate keys (bf16 with normalisation, forward workspace): for each (branch, head, query
 // tile) the keys j whose screen lane passed (max over its query rows of the screen score above
@@ -62,6 +82,8 @@ struct FwdParams {
   unsigned long long* stats; // may be null
   float* part;               // bf16 with one query tile: per-chunk partial outputs (workspace)
   uint32_t* pairs;           // may be null: pair lists (bf16)
+  uint32_t* colcnt;          // may be null: column bucket counts and entries (in pairs)
+  uint32_t* colbuf;
   int nbr;                   // branches
   uint32_t* cand;            // candidate keys (workspace; null for a single query tile)
   uint32_t* pvq;             // with cand: query tiles for the tile pass ([0] count, then bh nqt + qt),
@@ -95,6 +117,8 @@ struct BwdParams {
   const uint32_t* pairs;     // may be null: the forward's pair lists (used with occ)
   float* pws;                // [pair lists][kPairCap] dk weight of each pair (workspace), written by
                              // the query-major pair pass, read by the key-major one
+  const uint32_t* colcnt;    // may be null: the forward's column buckets (counts, entries; the
+  uint32_t* colbuf;          // query-major pair pass writes each entry's dk weight)
   uint32_t* dkvq;            // may be null: key tiles for the key-major tile pass ([0] count, then
                              // items), zeroed by the query-major pair pass, filled by the key-major
                              // pair pass (workspace)

@@ -216,7 +216,9 @@ int main() {
   CHECK(tda_norms_floats_kv(2, 3, 10, 20, 2) == (size_t)2 * 6 * 30);
   CHECK(tda_fwd_workspace_bytes_kv(1, 1, 1, 5000, 1) == (size_t)256 + 5 * 1 * 128 * 4);
   CHECK(tda_fwd_workspace_bytes(1, 1, 33, 3) == 0);
-  CHECK(tda_pair_words(4, 16, 4096, 2) == (size_t)2 * 64 * 128 * (1 + 4 * 32));
+  // the lists (entries and counts), the column counts, kColCap = 64 entries of 4 words per column
+  CHECK(tda_pair_words(4, 16, 4096, 2) == (size_t)2 * 64 * 128 * (1 + 4 * 32) + 64 * 128 + (size_t)64 * 128 * 64 * 4);
+  CHECK(tda_pair_words(1, 1, 33, 1) == (size_t)(2 * (1 + 4 * 32) + 2) + 4 + (size_t)2 * 64 * 4);
   CHECK(tda_bwd_workspace_bytes(0, 1, 1, 128) == 0);
   for (int32_t code : {0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11, -12, -13, -100}) {
     const char* s = tda_error_string(code);

@@ -189,3 +189,85 @@ def test_long_key_range_backward(beta):
         assert torch.isfinite(x.float()).all(), name
         assert rel_err(x.float().cpu(), ref[name]) <= 2e-2, name
         assert rel_err(x.float().cpu(), y.float().cpu()) <= 1e-2, name
+
+
+def _column_layout(B, H, N, branches):
+    """Word offsets of the column buckets in the pair buffer (tda_params.hpp: the lists, then the
+    column counts, then kColCap entries per column, each part a multiple of 4 words)."""
+    nqt = (N + 31) // 32
+    lists = branches * B * H * nqt
+    r4 = lambda w: (w + 3) // 4 * 4  # noqa: E731
+    lw = r4(lists * (1 + 4 * CAP))
+    return lists, nqt, lw, lw + r4(B * H * nqt)
+
+
+COLCAP = 64  # kColCap in tda_params.hpp
+
+
+@pytest.mark.parametrize("shape,branches,beta", [
+    ((2, 2, 97, 128), 1, 0.2),   # lists past the cap: their columns tainted
+    ((1, 3, 700, 64), 2, 1.0),
+    ((1, 2, 2500, 128), 2, 1.0),
+    ((1, 2, 513, 64), 1, 0.0),   # dense: candidate lists overflow, the tile pass taints
+])
+def test_column_buckets_hold_the_listed_pairs(shape, branches, beta):
+    """The forward's column buckets: each listed pair with a bucket slot sits in the bucket of its
+    key tile at that slot ({row | branch << 31, key row in the tile, x}); a column's count is the
+    number of such pairs; the columns of a list past the cap and of pairs without a slot (tile
+    pass) are tainted.  After a backward with the lists every entry of an untainted column holds
+    a finite dk weight, and the backward is linear in dout bit for bit (2 dout: every gradient
+    doubles exactly), so repeated backwards rewrite the weights."""
+    from collections import defaultdict
+    from tda_amd import ops
+    f = _forward(shape, branches, beta, 2.0, True, seed=31)
+    B, H, N, d = shape
+    lists, nqt, cw0, bw0 = _column_layout(B, H, N, branches)
+    nkt = nqt
+    P = f["pairs"].cpu().to(torch.int64) & 0xffffffff
+    counts, ent = P[lists * 4 * CAP:lists * 4 * CAP + lists], P[:lists * 4 * CAP].view(lists, CAP, 4)
+    cc = P[cw0:cw0 + B * H * nkt]
+    cb = P[bw0:bw0 + B * H * nkt * COLCAP * 4].view(B * H * nkt, COLCAP, 4)
+    expect, tainted = defaultdict(set), set()
+    for br in range(branches):
+        for bh in range(B * H):
+            for qt in range(nqt):
+                li = (br * B * H + bh) * nqt + qt
+                c = int(counts[li])
+                for e in range(min(c, CAP)):
+                    j, row, xb, slot = (int(v) for v in ent[li, e])
+                    col = bh * nkt + j // 32
+                    if c > CAP or slot == 0xffffffff:
+                        tainted.add(col)
+                    if slot == 0xffffffff:
+                        continue
+                    expect[col].add((((32 * qt + row) | (br << 31)), j % 32, xb))
+                    if slot < COLCAP:
+                        assert tuple(int(v) for v in cb[col, slot, :3]) == ((32 * qt + row) | (br << 31), j % 32, xb)
+    clean = 0
+    for col in range(B * H * nkt):
+        n, t = int(cc[col]) & 0x7fffffff, int(cc[col]) >> 31
+        assert n == len(expect[col]), col
+        if col in tainted:
+            assert t == 1, col
+        if n <= COLCAP:
+            assert {tuple(int(v) for v in cb[col, s, :3]) for s in range(n)} == expect[col], col
+        clean += int(t == 0 and 0 < n <= COLCAP)
+    if shape[2] > 97 and beta > 0:  # sparse: most columns untainted
+        assert clean > 0
+    if shape[2] == 97 or beta == 0.0:
+        assert tainted
+    args = (f["q1"], f["k1"], f["q2"], f["k2"], f["v"])
+    tail = (f["bt"], f["lt"], 2.0, True, branches)
+    g1 = ops.backward(*args, f["do"], *tail, norms=f["norms"], occupancy=f["occ"], pairs=f["pairs"])
+    P = f["pairs"].cpu().to(torch.int64) & 0xffffffff
+    cc = P[cw0:cw0 + B * H * nkt]
+    cb = P[bw0:bw0 + B * H * nkt * COLCAP * 4].view(B * H * nkt, COLCAP, 4)
+    for col in range(B * H * nkt):
+        n, t = int(cc[col]) & 0x7fffffff, int(cc[col]) >> 31
+        if t == 0 and n <= COLCAP:
+            w = cb[col, :n, 3].to(torch.int32).view(torch.float32)
+            assert torch.isfinite(w).all(), col
+    g2 = ops.backward(*args, 2 * f["do"], *tail, norms=f["norms"], occupancy=f["occ"], pairs=f["pairs"])
+    for a, b2 in zip(g1, g2):
+        if a is not None:
+            assert torch.equal(2 * a, b2)

@@ -1,7 +1,8 @@
 """tda_fwd_noalloc (workspace in the library's own device array) against tda_fwd (caller
 workspace) through the C ABI: identical outputs and side outputs, bit for bit (the same kernels
-on the same inputs), on two calls in a row whose second is smaller, so that what the first
-call left in the array must not reach the second's results.  Every call on one GPU shares the
+on the same inputs; the pair buffer's column buckets up to the order of their atomic appends), on
+two calls in a row whose second is smaller, so that what the first call left in the array must
+not reach the second's results.  Every call on one GPU shares the
 array; these calls run in order on one stream."""
 import pytest
 import torch
@@ -33,10 +34,34 @@ def _run(shape, nk, branches, dtype, normalize, p, seed, no_alloc, q_offset=0):
     return dict(out=out, norms=norms, occ=occ, pairs=pairs, stats=stats)
 
 
-def _same(a, b):
+def _pair_parts(pairs, shape, branches):
+    """The pair buffer in parts that do not depend on the order of the column buckets' atomic
+    appends (tda_params.hpp): list entries without their bucket slot word, list counts, column
+    counts, and each column's bucket entries (row, key row, x) sorted (columns of at most 64)."""
+    B, H, N, _ = shape
+    nqt = (N + 31) // 32
+    lists = branches * B * H * nqt
+    r4 = lambda w: (w + 3) // 4 * 4  # noqa: E731
+    lw = r4(lists * (1 + 4 * 32))
+    P = pairs.cpu().to(torch.int64) & 0xffffffff
+    ent = P[:lists * 4 * 32].view(lists, 32, 4)[:, :, :3]
+    counts = P[lists * 4 * 32:lists * 4 * 32 + lists]
+    cc = P[lw:lw + B * H * nqt]
+    cb = P[lw + r4(B * H * nqt):].view(B * H * nqt, 64, 4)[:, :, :3]
+    n = [int(c) & 0x7fffffff for c in cc]  # past 64 pairs which ones got a slot varies: counts only
+    cols = [sorted(tuple(int(v) for v in cb[c, s]) for s in range(n[c])) if n[c] <= 64 else []
+            for c in range(B * H * nqt)]
+    return ent, counts, cc, cols
+
+
+def _same(a, b, shape, branches):
     for key in a:
         if a[key] is None:
             assert b[key] is None
+            continue
+        if key == "pairs":
+            for x, y in zip(_pair_parts(a[key], shape, branches), _pair_parts(b[key], shape, branches)):
+                assert (torch.equal(x, y) if isinstance(x, torch.Tensor) else x == y), key
             continue
         assert torch.equal(a[key].view(torch.int8) if a[key].dtype.is_floating_point else a[key],
                            b[key].view(torch.int8) if b[key].dtype.is_floating_point else b[key]), key
@@ -65,5 +90,5 @@ def test_noalloc_matches_tda_fwd_on_two_calls(first, second):
         want = _run(shape, nk, branches, dtype, normalize, p, 50 + n, False, qoff)
         got = _run(shape, nk, branches, dtype, normalize, p, 50 + n, True, qoff)
         assert want["out"].abs().max() > 0
-        _same(want, got)
+        _same(want, got, shape, branches)
 
