@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define TDA_ABI_VERSION 6
+#define TDA_ABI_VERSION 7
 
 /* element types of q, k, v, out and gradients */
 #define TDA_DTYPE_F32  0
@@ -133,8 +133,9 @@ typedef struct tda_fwd_args {
   uint32_t* pairs;          /* optional output (may be NULL), tda_pair_words() words, 16-byte
                                aligned: for each (branch, head, query tile) the list of its
                                non-zero weights (key index, row, exact threshold margin), which
-                               lets the backward read only the rows they name; bf16 only (the
-                               f32 forward leaves it alone) */
+                               lets the backward read only the rows they name, and (normalised,
+                               more than 32 query rows, Nk <= Nq rounded up to 32) the same pairs
+                               bucketed by key tile; bf16 only (the f32 forward leaves it alone) */
   void*    zero;            /* optional (may be NULL with zero_bytes == 0): a device range the
                                call sets to zero, 16-byte aligned, zero_bytes a multiple of 16.
                                For training: the buffer of the backward's gradients, zeroed while
@@ -169,8 +170,10 @@ typedef struct tda_bwd_args {
   unsigned long long* stats;/* optional: [0] += tiles visited, [1] += tiles computed */
   int64_t seq_len_kv;       /* as in tda_fwd_args (dq, dout: Nq rows; dk, dv: Nk rows) */
   int64_t q_offset;
-  const uint32_t* pairs;    /* the forward's pair lists, or NULL; used only with occupancy
-                               (bf16): lists that did not fit fall back to the bitmask tiles */
+  uint32_t* pairs;          /* the forward's pair buffer, or NULL; used only with occupancy
+                               (bf16): lists that did not fit fall back to the bitmask tiles.
+                               The call writes each bucketed pair's dk weight into it, so two
+                               backward calls on one pair buffer must not overlap. */
   int32_t grads_zeroed;     /* 1: dq1, dk1, (dq2, dk2,) dv hold zeros already (e.g. the forward's
                                zero range); the call then stores only the gradient rows that a
                                non-zero weight reaches.  0: every row is stored.  No counterpart
@@ -202,7 +205,9 @@ size_t tda_fwd_workspace_bytes_kv(int64_t batch, int64_t heads, int64_t seq_len,
                                   int32_t branches);
 size_t tda_fwd_workspace_bytes_for(const tda_fwd_args* args);
 size_t tda_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim);
-/* Words of the pair-list output (queries seq_len; no dependence on the key rows). */
+/* Words of the pair buffer: the lists and the column buckets (queries seq_len; no dependence
+   on the key rows: the buckets are used only when the key tiles are no more than the query
+   tiles). */
 size_t tda_pair_words(int64_t batch, int64_t heads, int64_t seq_len, int32_t branches);
 
 /* Enqueue the forward / backward pass on `stream` (a hipStream_t). */

@@ -13,7 +13,7 @@ import threading
 HERE = os.path.dirname(os.path.abspath(__file__))
 DEFAULT_LIB = os.path.join(HERE, "libtda_hip.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 

@@ -143,12 +143,15 @@ int main() {
     tda_bwd_args a = bwd_args();
     a.grads_zeroed = 1;
     a.occupancy = static_cast<const uint32_t*>(FAKE);
-    a.pairs = static_cast<const uint32_t*>(FAKE);
+    a.pairs = static_cast<uint32_t*>(FAKE);
     CHECK(tda_bwd(&a, nullptr) == TDA_OK);
     CHECK(stub::last_bwd.grads_zeroed == 1 && stub::last_bwd.pairs != nullptr && stub::last_bwd.dkvq != nullptr);
+    // column buckets after the 2 * 6 * 4 lists (129 words each), counts of 6 * 4 columns
+    CHECK(stub::last_bwd.colcnt == static_cast<const uint32_t*>(FAKE) + 48 * 129 &&
+          stub::last_bwd.colbuf == static_cast<uint32_t*>(FAKE) + 48 * 129 + 24);
     a.occupancy = nullptr;  // without the bitmask the pair lists are not used
     CHECK(tda_bwd(&a, nullptr) == TDA_OK);
-    CHECK(stub::last_bwd.pairs == nullptr);
+    CHECK(stub::last_bwd.pairs == nullptr && stub::last_bwd.colcnt == nullptr);
   }
   {  // a failed launch maps to TDA_ERR_HIP and is kept for tda_last_hip_error
     tda_fwd_args a = fwd_args();
