@@ -9,13 +9,15 @@
 // branches are read once (their inverse norms computed on the fly, no separate pass) and V only
 // for the key tiles holding a non-zero weight.  The key range is split for parallelism:
 //   fwd_decode      one workgroup per (head, chunk of 32 key tiles); wave w takes the chunk's
-//                   key tiles w, w + 4, ...  Per key tile: the key fragments of both branches,
-//                   their inverse norms (written to the norms table), the transposed score tiles
-//                   S^T = K Q^T on the matrix cores, the exact weights, and, when a wave ballot
-//                   finds a non-zero one, O^T += V^T A^T with V staged through the wave's LDS.
-//                   The four waves' partial outputs are summed through LDS into one fp32 partial
-//                   per chunk; the chunk's 32 tile bits form bitmask word `chunk` of the query
-//                   tile's row, written whole.
+//                   key tiles w, w + 4, ...  Pass 1, per (key tile, branch), with the next two
+//                   items' key rows in flight: the key fragments, their inverse norms (written
+//                   to the norms table), the transposed score tile S^T = K Q^T on the matrix
+//                   cores and the exact test, a wave ballot into the tile's bitmask bit.  Pass 2,
+//                   per tile with a non-zero weight: the same scores and weights again and
+//                   O^T += V^T A^T with V staged through the wave's LDS.  The four waves'
+//                   partial outputs are summed through LDS into one fp32 partial per chunk; the
+//                   chunk's 32 tile bits form bitmask word `chunk` of the query tile's row,
+//                   written whole.
 //   fwd_decode_sum  out = sum of the chunk partials, chunk by chunk in order (deterministic).
 #include "tda_common.hpp"
 #include "tda_params.hpp"
@@ -33,6 +35,7 @@ __global__ void __launch_bounds__(64 * kDecWaves, 2) fwd_decode(FwdParams P, flo
   __shared__ __attribute__((aligned(16))) bf16 vlds[kDecWaves][TTileBF16<D>::ELEMS];
   __shared__ __attribute__((aligned(16))) float red[D][33];  // partial O^T (d, query), padded
   __shared__ uint32_t wbits[BR][kDecWaves];
+  __shared__ __attribute__((aligned(16))) float rkl[kDecWaves][32];  // a tile's key norms, per wave
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -70,63 +73,113 @@ __global__ void __launch_bounds__(64 * kDecWaves, 2) fwd_decode(FwdParams P, flo
   float lam = 0.f;
   if constexpr (BR == 2) lam = clamp01(*P.lam);
 
+  // Pass 1, every key tile of the wave (kt = 32 chunk + wv + 4 m) and branch: the key rows
+  // (those of the next two (tile, branch) items in flight while one is tested), their inverse
+  // norms into the norms table, the score tile and the exact test, which sets the tile's bitmask
+  // bit.  No V and no output accumulators: the registers hold three items' key rows instead.
+  // Pass 2 recomputes the few tiles with a non-zero weight (the same operations on the same
+  // values: the same scores and weights) and accumulates O^T += V^T A^T.
+  // A lane past Nk loads row Nk - 1, and an item past the last key tile loads that tile (no
+  // branch around the loads): such scores are masked by key < Nk, such norms are not stored.
+  auto load_rows_br = [&](int kt, int br, bf16x8 (&K)[NT]) {
+    const int j = min(32 * kt + n32, Nk - 1);
+    const bf16* row = kr[br].row(b, h, j);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) K[t] = *reinterpret_cast<const bf16x8*>(row + 16 * t + 8 * g);
+  };
+  auto load_k = [&](int kt, bf16x8 (&K)[BR][NT]) {
+#pragma unroll
+    for (int br = 0; br < BR; ++br) load_rows_br(kt, br, K[br]);
+  };
+  float* rkw = rkl[wv];
+  // the inverse norms of a tile's keys in branch br (written to the norms table when `store`)
+  // and the values r of this lane (keys crow(r, g)) from the wave's LDS slots
+  auto key_norms = [&](int kt, int br, const bf16x8 (&K)[NT], f32x4 (&rk4)[4], bool store) {
+    const int j = 32 * kt + n32;
+    float rk = 1.f;
+    if constexpr (NORM) {
+      rk = inv_norm(row_sumsq<Pol, NT>(K));
+      if (store && g == 0 && j < Nk) P.norms[norm_base(P, br ? N_K2 : N_K1, bh) + j] = rk;
+    }
+    if (g == 0) rkw[n32] = rk;
+    wave_lds_sync();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rk4[u] = *reinterpret_cast<const f32x4*>(rkw + 8 * u + 4 * g);
+    wave_lds_sync();  // the slots are rewritten by the next item
+  };
+  // the score tile of branch br: this lane's 16 values (query n32, keys crow(r, g))
+  auto scores = [&](const bf16x8 (&K)[NT], int br) {
+    f32x16 S = {};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) S = Pol::mma(K[t], Q[br][t], S);
+    return S;
+  };
+  auto weight_pos = [&](int key, float s, float rkr, float rqb, float& x) {
+    x = __builtin_fmaf(s * rkr, rqb, -tau);
+    return qvalid && key <= pq && key < Nk && x > 0.f;
+  };
+
+  uint32_t word[BR];
+#pragma unroll
+  for (int br = 0; br < BR; ++br) word[br] = 0u;
+  unsigned visited = 0, computed = 0;
+  {
+    constexpr int NI = (32 / kDecWaves) * BR;  // (tile, branch) items of the wave
+    constexpr int NB = 3;                      // key-row buffers: two items in flight
+    auto item_kt = [&](int it) { return 32 * chunk + wv + kDecWaves * (it / BR); };
+    bf16x8 Kr[NB][NT];
+#pragma unroll
+    for (int it = 0; it < NB - 1; ++it) load_rows_br(min(item_kt(it), P.nkt - 1), it % BR, Kr[it]);
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      if (it + NB - 1 < NI)
+        load_rows_br(min(item_kt(it + NB - 1), P.nkt - 1), (it + NB - 1) % BR, Kr[(it + NB - 1) % NB]);
+      const int kt = item_kt(it), br = it % BR;
+      if (kt >= P.nkt) continue;
+      f32x4 rk4[4];
+      key_norms(kt, br, Kr[it % NB], rk4, true);
+      if (kt > klast) continue;  // keys after the last query position: norms only
+      if (br == 0) visited += BR;
+      const f32x16 S = scores(Kr[it % NB], br);
+      const int k0 = 32 * kt;
+      bool pos_any = false;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x;
+        pos_any |= weight_pos(k0 + crow(r, g), S[r], rk4[r >> 2][r & 3], rq[br], x);
+      }
+      const bool any = wave_ballot(pos_any) != 0ull;
+      word[br] |= (uint32_t)any << (kt & 31);
+      computed += any ? 1u : 0u;
+    }
+  }
+
+  // Pass 2: the tiles of this wave with a non-zero weight in either branch.
   TTileBF16<D> vt;
   vt.lds = vlds[wv];
   f32x16 O[ND];
 #pragma unroll
   for (int c = 0; c < ND; ++c) O[c] = f32x16{};
-  uint32_t word[BR];
-#pragma unroll
-  for (int br = 0; br < BR; ++br) word[br] = 0u;
-  unsigned visited = 0, computed = 0;
-
-  for (int u = wv; u < 32; u += kDecWaves) {
-    const int kt = 32 * chunk + u;
-    if (kt >= P.nkt) break;
-    const int k0 = 32 * kt, j = k0 + n32;  // key row this lane loads (A operand row)
+  uint32_t hits = word[0];
+  if constexpr (BR == 2) hits |= word[1];
+  for (; hits; hits &= hits - 1u) {
+    const int kt = 32 * chunk + __builtin_ctz(hits), k0 = 32 * kt;
     bf16x8 K[BR][NT];
-#pragma unroll
-    for (int br = 0; br < BR; ++br) {
-      const bf16* row = j < Nk ? kr[br].row(b, h, j) : nullptr;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) K[br][t] = Pol::load_row(row, t, g);
-    }
-    float rk[BR];
-#pragma unroll
-    for (int br = 0; br < BR; ++br) {
-      rk[br] = 1.f;
-      if constexpr (NORM) {
-        rk[br] = inv_norm(row_sumsq<Pol, NT>(K[br]));
-        if (g == 0 && j < Nk) P.norms[norm_base(P, br ? N_K2 : N_K1, bh) + j] = rk[br];
-      }
-    }
-    if (kt > klast) continue;  // keys after the last query position: norms only
-    visited += BR;
+    load_k(kt, K);
     f32x16 C = {};
-    bool any[BR];
 #pragma unroll
     for (int br = 0; br < BR; ++br) {
-      f32x16 S = {};
-#pragma unroll
-      for (int t = 0; t < NT; ++t) S = Pol::mma(K[br][t], Q[br][t], S);
-      bool pos_any = false;
+      f32x4 rk4[4];
+      key_norms(kt, br, K[br], rk4, false);
+      const f32x16 S = scores(K[br], br);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = k0 + crow(r, g);
-        const float rkr = NORM ? __shfl(rk[br], crow(r, g)) : 1.f;
-        const float x = __builtin_fmaf(S[r] * rkr, rq[br], -tau);
-        const bool pos = qvalid && key <= pq && key < Nk && x > 0.f;
+        float x;
+        const bool pos = weight_pos(k0 + crow(r, g), S[r], rk4[r >> 2][r & 3], rq[br], x);
         const float a = pos ? pow_p<PK>(x, pw) : 0.f;
         C[r] = br == 0 ? a : __builtin_fmaf(-lam, a, C[r]);
-        pos_any |= pos;
       }
-      any[br] = wave_ballot(pos_any) != 0ull;
-      word[br] |= (uint32_t)any[br] << (kt & 31);
-      computed += any[br] ? 1u : 0u;
     }
-    bool need = any[0];
-    if constexpr (BR == 2) need = need || any[1];
-    if (!need) continue;
     vt.stage(vv, b, h, k0, Nk);
     wave_lds_sync();
 #pragma unroll
@@ -187,8 +240,18 @@ __global__ void __launch_bounds__(256) fwd_decode_sum(FwdParams P, const float* 
   const int bh = (int)(e / (Nq * D)), r = (int)(e % (Nq * D));
   const int n = r / D, d = r % D;
   const float* src = part + (int64_t)bh * nch * Nq * D + r;
+  const int64_t cs = (int64_t)Nq * D;  // distance between two chunks' partials
+  // eight chunks' loads in flight at a time, added in chunk order
   float acc = 0.f;
-  for (int c = 0; c < nch; ++c) acc += src[(int64_t)c * Nq * D];
+  int c = 0;
+  for (; c + 8 <= nch; c += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[(int64_t)(c + u) * cs];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += v[u];
+  }
+  for (; c < nch; ++c) acc += src[(int64_t)c * cs];
   const int b = bh / P.H, h = bh % P.H;
   bf16* o = (bf16*)P.out + (int64_t)b * P.s[F_OUT][0] + (int64_t)h * P.s[F_OUT][1] + (int64_t)n * P.s[F_OUT][2];
   o[d] = (bf16)acc;

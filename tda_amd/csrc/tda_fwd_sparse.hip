@@ -581,10 +581,11 @@ __device__ __forceinline__ void wait_vm() {  // vmcnt(N) with the other counters
   static_assert(N >= 0 && N < 64, "vmcnt field");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
-// rint(x) for |x| < 2^22 by the float adder: x + 1.5 * 2^23 rounds to an integer (ties to even)
-// whose low bits are that integer's two's complement; returns the sum.
+// rint(x y) of the exact product, |x y| < 2^22, by one fma: x y + 1.5 * 2^23 rounds to an integer
+// (ties to even) whose low bits are that integer's two's complement; returns the sum.  The
+// integer as a float is the sum minus the constant (exact).
 constexpr float kRintMagic = 12582912.0f;
-__device__ __forceinline__ float rint_sum(float x) { return x + kRintMagic; }
+__device__ __forceinline__ float rint_fma(float x, float y) { return __builtin_fmaf(x, y, kRintMagic); }
 
 template <int D>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) fwd_screen_i8(FwdParams P, int BR) {
@@ -745,7 +746,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
           const int j = 4 * u + e;
           float x = (float)qv[t][j >> 3][j & 7] * sc;
           if (any_nonfinite) x = __builtin_isfinite(x) ? x : 0.f;
-          const float rs = rint_sum(x * inv);  // rint(x inv), |x inv| <= 127 (1 + 2^-22)
+          const float rs = rint_fma(x, inv);  // rint(x inv) of the exact product, |x inv| <= 127 (1 + 2^-22)
           a[e] = __builtin_bit_cast(int, rs);  // low byte: the int8 value
           const float r = __builtin_fmaf(-sq[s], rs - kRintMagic, x);
           r2 = __builtin_fmaf(r, r, r2);

@@ -5,9 +5,11 @@ The screen (tda_amd/csrc/tda_fwd_sparse.hip: key_prep and fwd_screen_i8) keeps k
 query tile when, for some row i of the tile,
     fl(fl(float(A_ij) * fl(sq * s_j))) > thr_j,
 with
-    kh_j = fl(k_j rk_j),  s_j = max|kh_j| / 127,  b_j = rint(kh_j * 127 / max|kh_j|)   (key_prep)
+    kh_j = fl(k_j rk_j),  s_j = max|kh_j| / 127,  b_j = rint(fl(kh_j * fl(127 / max|kh_j|)))   (key_prep)
     qh_i = fl(q_i rq_i),  sq = m / 127 with m = max_i rq_i max|q_i| over the tile's rows,
-    a_i = rint(qh_i * 127 / m),  A_ij = a_i . b_j (exact int32)
+    a_i = rint(qh_i * fl(127 / m)) of the exact product (one fma against 1.5 * 2^23),
+    A_ij = a_i . b_j (exact int32)
+(rint ties to even)
     ek_j, eq >= the norms of the residuals kh_j - s_j b_j and qh_i - sq a_i (eq: the tile's
     largest), times 1 + 2^-12,
     thr_j = tmin - |tmin| 2^-19 - 2^-14 - eq (1 + 2^-10) - ek_j (1 + 2^-10 + 4 eq),
@@ -41,6 +43,12 @@ def _fma32(a, b, c):
     return (np.asarray(a, np.float64) * np.asarray(b, np.float64) + np.asarray(c, np.float64)).astype(np.float32)
 
 
+def rint_prod(x: np.ndarray, inv) -> np.ndarray:
+    """rint(x * inv) of the exact product of fp32 values (exact in fp64), ties to even: the
+    kernels' fma(x, inv, 1.5 * 2^23)."""
+    return np.rint(np.asarray(x, np.float64) * np.float64(inv))
+
+
 def res_bound(r: np.ndarray) -> float:
     """The kernels' bound on a residual's norm: fp32 sum of squares (fma chain), square root,
     times 1 + 2^-12."""
@@ -57,7 +65,8 @@ def quant_key(k: np.ndarray):
     m = F32(np.max(np.abs(kh)))
     s = F32(m * F32(1.0 / 127.0))
     inv = F32(127.0) / m if m > 0 else F32(0.0)
-    b = np.clip(np.rint((kh * inv).astype(np.float32)), -127, 127)
+    b = np.rint((kh * inv).astype(np.float32))
+    assert np.all(np.abs(b) <= 127)
     r = _fma32(-s, b.astype(np.float32), kh)
     return b.astype(np.int64), float(s), res_bound(r), rk, kh
 
@@ -70,7 +79,8 @@ def quant_tile(qs: np.ndarray):
     sq = F32(m * F32(1.0 / 127.0))
     inv = F32(127.0) / m if m > 0 else F32(0.0)
     qh = (qs.astype(np.float32) * rq[:, None]).astype(np.float32)
-    a = np.clip(np.rint((qh * inv).astype(np.float32)), -127, 127)
+    a = rint_prod(qh, inv)
+    assert np.all(np.abs(a) <= 127)
     r = _fma32(-sq, a.astype(np.float32), qh)
     eq = max(res_bound(x) for x in r)
     return a.astype(np.int64), float(sq), eq, qh
