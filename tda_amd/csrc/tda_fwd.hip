@@ -25,8 +25,14 @@ template <int D> struct TTileSel<PolF32, D> { using type = TTileF32<D>; };
 // rows as the resident B operand.  In the C layout each lane then owns one query and 16 keys,
 // so the per-query threshold, inverse norm and the causal test are per-lane scalars, and the
 // thresholded tile packs directly into the B operand of O^T += V^T A^T.
-template <class Pol, int D, int BR, int PK, bool NORM>
+//
+// SCR (fp32, normalised, after key_prep and fwd_screen_i8 ran on the same inputs): the screen's
+// bitmask names every key tile holding a non-zero weight (a superset), so the wave visits only
+// those tiles; the inverse norms come from the table the screen and key_prep wrote (the values
+// the screen's bound is stated for), and the bitmask words are rewritten exactly.
+template <class Pol, int D, int BR, int PK, bool NORM, bool SCR = false>
 __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
+  static_assert(!SCR || NORM, "the screened pass is the normalised one");
   using T = typename Pol::T;
   using frag = typename Pol::frag;
   constexpr int NT = D / Pol::KS;  // MFMA steps over d
@@ -64,7 +70,12 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
     }
   }
   float rq1 = 1.f, rq2 = 1.f;
-  if constexpr (NORM) {
+  if constexpr (SCR) {
+    if (qvalid) {
+      rq1 = P.norms[norm_base(P, N_Q1, bh) + i];
+      if constexpr (BR == 2) rq2 = P.norms[norm_base(P, N_Q2, bh) + i];
+    }
+  } else if constexpr (NORM) {
     rq1 = inv_norm(row_sumsq<Pol, NT>(Q1));
     if constexpr (BR == 2) rq2 = inv_norm(row_sumsq<Pol, NT>(Q2));
     if (P.norms && qvalid && g == 0) {
@@ -89,9 +100,29 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
   uint32_t* occrow = P.occ ? P.occ + ((int64_t)bh * P.nqt + qt) * P.occ_w : nullptr;
   const int64_t occ_br = (int64_t)BH * P.nqt * P.occ_w;  // distance between the branch planes
   uint32_t word = 0, word2 = 0;
-  unsigned visited = 0, computed = 0;
+  unsigned visited = 0, computed = 0, checked = 0;
 
   for (int kt = 0; kt <= ktl; ++kt) {
+    if constexpr (SCR) {
+      // the screen's bits of this word (per branch), read before this wave rewrites the word
+      const uint32_t s1 = occrow[kt >> 5], s2 = BR == 2 ? occrow[occ_br + (kt >> 5)] : 0u;
+      const uint32_t keep = (s1 | s2) & (~0u << (kt & 31));  // kept tiles kt .. of the word
+      const int next = keep ? (kt & ~31) + __builtin_ctz(keep) : (kt | 31) + 1;
+      if (next > kt) {  // skipped tiles hold no weight: close the word if it ends among them
+        const int wend = kt | 31;
+        if (next > wend || next > ktl) {
+          if (l == 0) {
+            occrow[kt >> 5] = word;
+            if constexpr (BR == 2) occrow[occ_br + (kt >> 5)] = word2;
+          }
+          word = word2 = 0;
+          kt = wend;
+          continue;
+        }
+        kt = next;
+      }
+      checked += ((s1 >> (kt & 31)) & 1u) + ((s2 >> (kt & 31)) & 1u);
+    }
     const int k0 = kt * 32;
     const int j = k0 + n32;  // key row this lane loads for the A operand
     const bool kfirst = qt == qt_first(kt, qoff);  // the first query tile to see kt writes its norms
@@ -104,8 +135,10 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) S1 = Pol::mma(K1[t], Q1[t], S1);
       if constexpr (NORM) {
-        const float rk = inv_norm(row_sumsq<Pol, NT>(K1));
-        if (P.norms && kfirst && g == 0 && j < Nk) P.norms[norm_base(P, N_K1, bh) + j] = rk;
+        float rk;
+        if constexpr (SCR) rk = j < Nk ? P.norms[norm_base(P, N_K1, bh) + j] : 0.f;
+        else rk = inv_norm(row_sumsq<Pol, NT>(K1));
+        if (!SCR && P.norms && kfirst && g == 0 && j < Nk) P.norms[norm_base(P, N_K1, bh) + j] = rk;
 #pragma unroll
         for (int r = 0; r < 16; ++r) rk1r[r] = __shfl(rk, crow(r, g));
       }
@@ -117,8 +150,10 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) S2 = Pol::mma(K2[t], Q2[t], S2);
       if constexpr (NORM) {
-        const float rk = inv_norm(row_sumsq<Pol, NT>(K2));
-        if (P.norms && kfirst && g == 0 && j < Nk) P.norms[norm_base(P, N_K2, bh) + j] = rk;
+        float rk;
+        if constexpr (SCR) rk = j < Nk ? P.norms[norm_base(P, N_K2, bh) + j] : 0.f;
+        else rk = inv_norm(row_sumsq<Pol, NT>(K2));
+        if (!SCR && P.norms && kfirst && g == 0 && j < Nk) P.norms[norm_base(P, N_K2, bh) + j] = rk;
 #pragma unroll
         for (int r = 0; r < 16; ++r) rk2r[r] = __shfl(rk, crow(r, g));
       }
@@ -191,8 +226,8 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
 
   // Key tiles no query tile sees (keys past the last query position): their inverse norms
   // still go to the table (the backward's normalize epilogue reads every key row's), written
-  // by the last query tile's wave.
-  if constexpr (NORM) {
+  // by the last query tile's wave (with SCR key_prep wrote every key row's).
+  if constexpr (NORM && !SCR) {
     if (P.norms && qt == P.nqt - 1) {
       for (int kt = ktl + 1; kt < P.nkt; ++kt) {
         const int j = 32 * kt + n32;
@@ -219,25 +254,34 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
       for (int u = 0; u < 4; ++u)
         store4(orow + 32 * c + 8 * u + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2], O[c][4 * u + 3]);
   }
-  if (P.stats && l == 0) {
-    atomicAdd(P.stats + 0, (unsigned long long)visited);
+  if (P.stats && l == 0) {  // with SCR the screen counted the causal tiles; `checked`: its kept ones
+    atomicAdd(P.stats + (SCR ? 2 : 0), (unsigned long long)(SCR ? checked : visited));
     atomicAdd(P.stats + 1, (unsigned long long)computed);
   }
 }
 
 // ------------------------------------------------------------------ dispatch
+// Normalised fp32 calls with more than one query tile and the int8 keys' workspace run the int8
+// screen first (key_prep and fwd_screen_i8 on the fp32 rows, tda_fwd_sparse.hip), then the
+// screened fwd_wave.
 template <class Pol, int D, int BR, int PK, bool NORM>
-static int launch_fwd_t(const FwdParams& p, void* stream) {
+static int launch_fwd_t(const FwdParams& p, const KernelKey& k, void* stream) {
   const int64_t items = (int64_t)p.B * p.H * p.nqt;
   const unsigned grid = (unsigned)((items + 3) / 4);
-  hipLaunchKernelGGL((fwd_wave<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, (hipStream_t)stream, p);
+  if (NORM && p.k8 && p.nqt > 1) {
+    const int e = launch_fwd_screen_f32(p, k, stream);
+    if (e) return e;
+    hipLaunchKernelGGL((fwd_wave<Pol, D, BR, PK, NORM, NORM>), dim3(grid), dim3(256), 0, (hipStream_t)stream, p);
+  } else {
+    hipLaunchKernelGGL((fwd_wave<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, (hipStream_t)stream, p);
+  }
   launched(stream, "fwd_wave");
   return (int)hipGetLastError();
 }
 
 template <class Pol, int D, int BR, int PK>
 static int sel_norm(const FwdParams& p, const KernelKey& k, void* s) {
-  return k.normalize ? launch_fwd_t<Pol, D, BR, PK, true>(p, s) : launch_fwd_t<Pol, D, BR, PK, false>(p, s);
+  return k.normalize ? launch_fwd_t<Pol, D, BR, PK, true>(p, k, s) : launch_fwd_t<Pol, D, BR, PK, false>(p, k, s);
 }
 template <class Pol, int D, int BR>
 static int sel_pk(const FwdParams& p, const KernelKey& k, void* s) {
@@ -272,14 +316,16 @@ int launch_zero(const FwdParams& p, void* stream) {
 }
 
 // bf16 runs the screen + sparse A.V kernels (tda_fwd_sparse.hip), or with a single query tile
-// the split-key decode kernels (tda_fwd_decode.hip); fp32 runs fwd_wave.  The screen clears the
-// call's zero range; the other paths launch zero_range.
+// the split-key decode kernels (tda_fwd_decode.hip); fp32 runs fwd_wave, after the int8 screen
+// when normalised with more than one query tile.  The screen clears the call's zero range; the
+// other paths launch zero_range.
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream) {
   int e;
   if (k.dtype == 1 && !(p.nqt == 1 && p.part)) return launch_fwd_sparse(p, k, stream);
   if (k.dtype == 1) e = launch_fwd_decode(p, k, p.part, stream);
   else e = sel_d<PolF32>(p, k, stream);
-  return e ? e : launch_zero(p, stream);
+  const bool screened = k.dtype == 0 && k.normalize && p.k8 && p.nqt > 1;  // the screen cleared it
+  return e ? e : screened ? 0 : launch_zero(p, stream);
 }
 
 }  // namespace tda

@@ -312,7 +312,31 @@ template <int D>
 constexpr int kn_groups() {
   return D == 64 ? 2 : 4;
 }
-template <int D>
+// Row elements of a key_prep or screen lane: 16 consecutive bf16 (two 16-byte vectors) or fp32
+// (four) values; element j as a float.
+template <class T>
+struct Row16 {
+  static constexpr int E = 16 / sizeof(T);  // elements per 16-byte vector
+  using V = std::conditional_t<sizeof(T) == 2, bf16x8, f32x4>;
+  V v[16 / E];
+  __device__ __forceinline__ void load(const T* r) {
+#pragma unroll
+    for (int u = 0; u < 16 / E; ++u) v[u] = *reinterpret_cast<const V*>(r + E * u);
+  }
+  __device__ __forceinline__ float operator[](int j) const { return (float)v[j / E][j % E]; }
+  // the sum of squares: two fma chains over elements 0-7 and 8-15, added
+  __device__ __forceinline__ float sumsq() const {
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a = __builtin_fmaf((*this)[j], (*this)[j], a);
+      b = __builtin_fmaf((*this)[8 + j], (*this)[8 + j], b);
+    }
+    return a + b;
+  }
+};
+
+template <int D, class T>
 __global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
   constexpr int KN_GROUPS = kn_groups<D>();
   constexpr int LPR = D / 16, RPG = 64 / LPR, ROWS = RPG * KN_GROUPS;
@@ -331,22 +355,20 @@ __global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
   if ((int64_t)wid >= (int64_t)BR * BH * wpr) return;
   const int sidx = (int)(wid / wpr), br = sidx / BH, bh = sidx % BH;
   const int t0 = (int)(wid % wpr) * ROWS + l / LPR;
-  const bf16* kin = (const bf16*)(br ? P.in[F_K2] : P.in[F_K1]);
+  const T* kin = (const T*)(br ? P.in[F_K2] : P.in[F_K1]);
   const int64_t sb = br ? P.s[F_K2][0] : P.s[F_K1][0], sh = br ? P.s[F_K2][1] : P.s[F_K1][1];
   const int64_t st = br ? P.s[F_K2][2] : P.s[F_K1][2];
-  const bf16* head = kin + (int64_t)(bh / P.H) * sb + (int64_t)(bh % P.H) * sh;
-  bf16x8 x[KN_GROUPS][2];
+  const T* head = kin + (int64_t)(bh / P.H) * sb + (int64_t)(bh % P.H) * sh;
+  Row16<T> x[KN_GROUPS];
 #pragma unroll
   for (int u = 0; u < KN_GROUPS; ++u) {
     const int t = min(t0 + RPG * u, N - 1);
-    const bf16* r = head + (int64_t)t * st + 16 * sub;
-    x[u][0] = *reinterpret_cast<const bf16x8*>(r);
-    x[u][1] = *reinterpret_cast<const bf16x8*>(r + 8);
+    x[u].load(head + (int64_t)t * st + 16 * sub);
   }
   float ss[KN_GROUPS], rk[KN_GROUPS];
 #pragma unroll
   for (int u = 0; u < KN_GROUPS; ++u) {
-    ss[u] = group_sum<LPR>(PolBF16::sumsq(x[u][0]) + PolBF16::sumsq(x[u][1]));
+    ss[u] = group_sum<LPR>(x[u].sumsq());
     rk[u] = inv_norm(ss[u]);
   }
   float* out = P.norms + norm_base(P, br ? N_K2 : N_K1, bh);
@@ -364,7 +386,7 @@ __global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
   for (int u = 0; u < KN_GROUPS; ++u) {
     float kh[16], m = 0.f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) kh[j] = (float)x[u][j >> 3][j & 7] * rk[u];
+    for (int j = 0; j < 16; ++j) kh[j] = x[u][j] * rk[u];
     if (!__builtin_isfinite(ss[u])) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) kh[j] = __builtin_isfinite(kh[j]) ? kh[j] : 0.f;
@@ -587,7 +609,7 @@ __device__ __forceinline__ void wait_vm() {  // vmcnt(N) with the other counters
 constexpr float kRintMagic = 12582912.0f;
 __device__ __forceinline__ float rint_fma(float x, float y) { return __builtin_fmaf(x, y, kRintMagic); }
 
-template <int D>
+template <int D, class T>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) fwd_screen_i8(FwdParams P, int BR) {
   constexpr int QPW = 2, NTHR = 256, TPI = I8_TPI;
   constexpr int NK = D / 32;                     // int8 MFMA steps over d
@@ -662,11 +684,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
 
   // ---- resident int8 query fragments and the per-tile constants of the test
   const int qslot = br ? F_Q2 : F_Q1;
-  const bf16* qin = (const bf16*)(br ? P.in[F_Q2] : P.in[F_Q1]);
+  const T* qin = (const T*)(br ? P.in[F_Q2] : P.in[F_Q1]);
   const int64_t qsb = br ? P.s[F_Q2][0] : P.s[F_Q1][0], qsh = br ? P.s[F_Q2][1] : P.s[F_Q1][1];
   const int64_t qst = br ? P.s[F_Q2][2] : P.s[F_Q1][2];
   (void)qslot;
-  const bf16* qhead = qin + (int64_t)b * qsb + (int64_t)h * qsh;
+  const T* qhead = qin + (int64_t)b * qsb + (int64_t)h * qsh;
   const float beta = *P.beta;
   i32x4 A8[QPW][NK];
   float sq[QPW], tq[QPW], cq[QPW];  // scale, thr part of the tile, coefficient of ek_j
@@ -674,53 +696,58 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
   for (int s = 0; s < QPW; ++s) {
     const int iq = q0w + 32 * s + n32;
     const bool valid = iq < Nq;
-    const bf16* row = qhead + (int64_t)min(iq, Nq - 1) * qst;  // rows >= Nq: never vote
-    bf16x8 qv[NK][2];  // lane (m, g): elements 32 t + 16 g .. + 16 of row m
+    const T* row = qhead + (int64_t)min(iq, Nq - 1) * qst;  // rows >= Nq: never vote
+    Row16<T> qv[NK];  // lane (m, g): elements 32 t + 16 g .. + 16 of row m
 #pragma unroll
-    for (int t = 0; t < NK; ++t) {
-      qv[t][0] = *reinterpret_cast<const bf16x8*>(row + 32 * t + 16 * g);
-      qv[t][1] = *reinterpret_cast<const bf16x8*>(row + 32 * t + 16 * g + 8);
-    }
+    for (int t = 0; t < NK; ++t) qv[t].load(row + 32 * t + 16 * g);
     // the row's sum of squares and largest |q|; a row with a finite sum of squares has only
     // finite elements, and every element of it then scales to |x| <= m below
     float ss = 0.f, mq = 0.f;
 #pragma unroll
     for (int t = 0; t < NK; ++t)
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float x = (float)qv[t][c][j];
-          ss = __builtin_fmaf(x, x, ss);
-          mq = fmaxf(mq, fabsf(x));
-        }
+      for (int j = 0; j < 16; ++j) {
+        const float x = qv[t][j];
+        ss = __builtin_fmaf(x, x, ss);
+        mq = fmaxf(mq, fabsf(x));
+      }
     ss += __shfl_xor(ss, 32);
     const bool finite_row = __builtin_isfinite(ss);
     if (!finite_row) {  // the largest finite |q| (non-finite elements quantise as 0)
-      uint32_t mb = 0u;
+      if constexpr (sizeof(T) == 2) {
+        uint32_t mb = 0u;
+#pragma unroll
+        for (int t = 0; t < NK; ++t)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const u32x4 w = __builtin_bit_cast(u32x4, qv[t].v[c]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const uint32_t lo = w[k] & 0x7fffu, hi = (w[k] >> 16) & 0x7fffu;
+              mb = max(mb, (lo & 0x7f80u) != 0x7f80u ? lo : 0u);
+              mb = max(mb, (hi & 0x7f80u) != 0x7f80u ? hi : 0u);
+            }
+          }
+        mq = __builtin_bit_cast(float, mb << 16);
+      } else {
+        mq = 0.f;
+#pragma unroll
+        for (int t = 0; t < NK; ++t)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) mq = fmaxf(mq, __builtin_isfinite(qv[t][j]) ? fabsf(qv[t][j]) : 0.f);
+      }
+    }
+    if constexpr (sizeof(T) == 2) {
+      // the row values are converted again below, not kept as fp32 (register pressure)
 #pragma unroll
       for (int t = 0; t < NK; ++t)
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const u32x4 w = __builtin_bit_cast(u32x4, qv[t][c]);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const uint32_t lo = w[k] & 0x7fffu, hi = (w[k] >> 16) & 0x7fffu;
-            mb = max(mb, (lo & 0x7f80u) != 0x7f80u ? lo : 0u);
-            mb = max(mb, (hi & 0x7f80u) != 0x7f80u ? hi : 0u);
-          }
+          u32x4 w = __builtin_bit_cast(u32x4, qv[t].v[c]);
+          asm volatile("" : "+v"(w));
+          qv[t].v[c] = __builtin_bit_cast(bf16x8, w);
         }
-      mq = __builtin_bit_cast(float, mb << 16);
     }
-    // the row values are converted again below, not kept as fp32 (register pressure)
-#pragma unroll
-    for (int t = 0; t < NK; ++t)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        u32x4 w = __builtin_bit_cast(u32x4, qv[t][c]);
-        asm volatile("" : "+v"(w));
-        qv[t][c] = __builtin_bit_cast(bf16x8, w);
-      }
     const float rq = inv_norm(ss);
     if (g == 0 && valid && it.chunk == 0) P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + iq] = rq;
     const float sc = valid ? rq : 0.f;
@@ -744,7 +771,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int j = 4 * u + e;
-          float x = (float)qv[t][j >> 3][j & 7] * sc;
+          float x = qv[t][j] * sc;
           if (any_nonfinite) x = __builtin_isfinite(x) ? x : 0.f;
           const float rs = rint_fma(x, inv);  // rint(x inv) of the exact product, |x inv| <= 127 (1 + 2^-22)
           a[e] = __builtin_bit_cast(int, rs);  // low byte: the int8 value
@@ -1362,12 +1389,12 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   if constexpr (NORM) {
     constexpr int rows = (64 / (D / 16)) * kn_groups<D>();  // rows per wave
     const int64_t waves = (int64_t)BR * BH * ((p.Nk + rows - 1) / rows);
-    hipLaunchKernelGGL(key_prep<D>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, BR);
+    hipLaunchKernelGGL((key_prep<D, bf16>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, BR);
     launched(s, "key_prep");
   }
   const dim3 grid((unsigned)(BR * BH) * (unsigned)p.screen_items);
   if constexpr (NORM) {
-    hipLaunchKernelGGL(fwd_screen_i8<D>, grid, dim3(256), 0, s, p, BR);
+    hipLaunchKernelGGL((fwd_screen_i8<D, bf16>), grid, dim3(256), 0, s, p, BR);
   } else {
     constexpr int QPW = 2, TPB = 1;
     hipLaunchKernelGGL((fwd_screen<D, QPW, TPB>), grid, dim3(512 / QPW), 0, s, p, BR);
@@ -1409,6 +1436,30 @@ int sel_br(const FwdParams& p, const KernelKey& k, hipStream_t s) {
 int launch_fwd_sparse(const FwdParams& p, const KernelKey& k, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   return k.d == 128 ? sel_br<128>(p, k, s) : sel_br<64>(p, k, s);
+}
+
+// The int8 screen over fp32 rows, for the normalised fp32 pass (fwd_wave in its screened form,
+// tda_fwd.hip): key_prep and fwd_screen_i8 read the fp32 inputs and write the norms table and a
+// bitmask that keeps every tile holding a non-zero weight.  No candidate lists: the fp32 pass
+// walks the bitmask.
+int launch_fwd_screen_f32(const FwdParams& p0, const KernelKey& k, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  FwdParams p = p0;
+  p.cand = nullptr;
+  const int BR = k.branches, BH = p.B * p.H;
+  const dim3 grid((unsigned)(BR * BH) * (unsigned)p.screen_items);
+  auto run = [&](auto dc) {
+    constexpr int D = decltype(dc)::value;
+    constexpr int rows = (64 / (D / 16)) * kn_groups<D>();  // rows per wave
+    const int64_t waves = (int64_t)BR * BH * ((p.Nk + rows - 1) / rows);
+    hipLaunchKernelGGL((key_prep<D, float>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, BR);
+    launched(s, "key_prep");
+    hipLaunchKernelGGL((fwd_screen_i8<D, float>), grid, dim3(256), 0, s, p, BR);
+    launched(s, "fwd_screen");
+  };
+  if (k.d == 128) run(std::integral_constant<int, 128>{});
+  else run(std::integral_constant<int, 64>{});
+  return (int)hipGetLastError();
 }
 
 }  // namespace tda

@@ -101,9 +101,10 @@ int64_t fwd_ws_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t br
   return fwd_occ_bytes(bh, seq_len, seq_len_kv, branches) + fwd_part_bytes(bh, seq_len, seq_len_kv) +
          fwd_cand_bytes(bh, seq_len, branches) + fwd_k8_bytes(bh, seq_len, seq_len_kv, branches, kd);
 }
-// Row bytes of the int8 keys a call needs (0: it uses none).
+// Row bytes of the int8 keys a call needs (0: it uses none): the normalised calls, whose int8
+// screen runs on bf16 and on fp32 rows.
 int64_t k8_row_bytes(const tda_fwd_args& a) {
-  return a.dtype == TDA_DTYPE_BF16 && a.normalize ? a.head_dim : 0;
+  return a.normalize ? a.head_dim : 0;
 }
 constexpr int64_t kMaxHeadDim = 128;  // the size functions without head_dim assume the largest
 bool size_args_ok(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv, int32_t branches) {

@@ -136,6 +136,7 @@ struct KernelKey {
 
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_fwd_sparse(const FwdParams& p, const KernelKey& k, void* stream);
+int launch_fwd_screen_f32(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_fwd_decode(const FwdParams& p, const KernelKey& k, float* part, void* stream);
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream);

@@ -137,7 +137,13 @@ int main() {
     a.dtype = TDA_DTYPE_F32;
     a.workspace_bytes = tda_fwd_workspace_bytes_for(&a);
     CHECK(tda_fwd(&a, nullptr) == TDA_OK);
-    CHECK(stub::last_fwd.k8 == nullptr && stub::last_fwd.screen_items >= 1 && stub::last_fwd.screen_kc % 32 == 0);
+    // normalised fp32 with more than one query tile: the int8 screen runs on the fp32 rows
+    CHECK(stub::last_fwd.k8 != nullptr && stub::last_fwd.ksc != nullptr);
+    CHECK(stub::last_fwd.screen_items >= 1 && stub::last_fwd.screen_kc % 32 == 0);
+    a.normalize = 0;
+    a.workspace_bytes = tda_fwd_workspace_bytes_for(&a);
+    CHECK(tda_fwd(&a, nullptr) == TDA_OK);
+    CHECK(stub::last_fwd.k8 == nullptr);
   }
   {
     tda_bwd_args a = bwd_args();

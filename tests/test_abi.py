@@ -162,8 +162,8 @@ def test_fwd_validator_rejects(mutate, code):
 
 
 def test_workspace_for_one_call():
-    """tda_fwd_workspace_bytes_for: the int8 keys only for bf16 with normalize and more than one
-    query tile, at the call's head_dim; never above the shape-only bound."""
+    """tda_fwd_workspace_bytes_for: the int8 keys only with normalize (bf16 or fp32) and more
+    than one query tile, at the call's head_dim; never above the shape-only bound."""
     lib = _lib()
     r256 = lambda b: 256 * ((b + 255) // 256)  # noqa: E731
     a = _fwd_args()  # bf16, normalize, (2, 3, 100, 128), two branches
@@ -171,9 +171,9 @@ def test_workspace_for_one_call():
     assert full == lib.tda_fwd_workspace_bytes(2, 3, 100, 2)
     a.normalize = 0
     assert full - lib.tda_fwd_workspace_bytes_for(ctypes.byref(a)) == r256(2 * 6 * 100 * 128) + r256(2 * 6 * 100 * 8)
-    a.normalize, a.dtype = 1, _abi.DTYPE_F32
+    a.normalize, a.dtype = 1, _abi.DTYPE_F32  # the int8 screen also runs on fp32 rows
     assert lib.tda_fwd_workspace_bytes_for(ctypes.byref(a)) == lib.tda_fwd_workspace_bytes_for(
-        ctypes.byref(_fwd_args(dtype=_abi.DTYPE_F32))) < full
+        ctypes.byref(_fwd_args(dtype=_abi.DTYPE_F32))) == full
     b = _fwd_args(shape=(2, 3, 100, 64))
     assert full - lib.tda_fwd_workspace_bytes_for(ctypes.byref(b)) == r256(2 * 6 * 100 * 128) - r256(2 * 6 * 100 * 64)
     b.seq_len, b.seq_len_kv, b.q_offset = 20, 300, 280  # one query tile: decode partials, no int8 keys

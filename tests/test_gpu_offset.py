@@ -41,6 +41,12 @@ def test_rows_of_full_pass_equal_offset_block(dt, o, m):
         # one query tile in bf16 takes the split-key decode kernels, which add per-wave partial
         # outputs: the same terms in another fp32 order
         assert rel_err(blk, full[:, :, o:o + m]) <= 1e-2
+    elif m <= 32:
+        # one query tile in fp32 takes the unscreened pass, which sums the rows' squares for their
+        # norms in its own order (the screened pass of the full call uses the screen's): norms a
+        # few ulps apart, which weights just above tau amplify (x^p of a small x); both within the
+        # fp32 parity tolerance
+        assert rel_err(blk, full[:, :, o:o + m]) <= 1e-4
     else:
         assert torch.equal(blk, full[:, :, o:o + m])
     # keys after the block's last position are never read

@@ -64,10 +64,8 @@ def test_tile_sparsity_tda(dtype):
     assert not (strong & ~st.occupancy.cpu()).any()
     assert 0.0 < st.skipped_fraction < 1.0
     assert st.density.shape == (2,)
-    if dtype == torch.bfloat16:
-        assert st.tiles_screened >= st.tiles_nonzero
-    else:
-        assert st.tiles_screened is None
+    # normalised with more than one query tile: both dtypes run the int8 screen first
+    assert st.tiles_screened >= st.tiles_nonzero
 
 
 @pytest.mark.gpu
