@@ -103,9 +103,11 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
   unsigned visited = 0, computed = 0, checked = 0;
 
   for (int kt = 0; kt <= ktl; ++kt) {
+    bool use1 = true, use2 = true;  // SCR: the branches the screen kept this tile in
     if constexpr (SCR) {
       // the screen's bits of this word (per branch), read before this wave rewrites the word
-      const uint32_t s1 = occrow[kt >> 5], s2 = BR == 2 ? occrow[occ_br + (kt >> 5)] : 0u;
+      const uint32_t s1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)occrow[kt >> 5]);
+      const uint32_t s2 = BR == 2 ? (uint32_t)__builtin_amdgcn_readfirstlane((int)occrow[occ_br + (kt >> 5)]) : 0u;
       const uint32_t keep = (s1 | s2) & (~0u << (kt & 31));  // kept tiles kt .. of the word
       const int next = keep ? (kt & ~31) + __builtin_ctz(keep) : (kt | 31) + 1;
       if (next > kt) {  // skipped tiles hold no weight: close the word if it ends among them
@@ -121,14 +123,17 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
         }
         kt = next;
       }
-      checked += ((s1 >> (kt & 31)) & 1u) + ((s2 >> (kt & 31)) & 1u);
+      use1 = (s1 >> (kt & 31)) & 1u;
+      use2 = (s2 >> (kt & 31)) & 1u;
+      checked += (use1 ? 1u : 0u) + (use2 ? 1u : 0u);
     }
     const int k0 = kt * 32;
     const int j = k0 + n32;  // key row this lane loads for the A operand
     const bool kfirst = qt == qt_first(kt, qoff);  // the first query tile to see kt writes its norms
     f32x16 S1 = f32x16{}, S2 = f32x16{};
-    float rk1r[16], rk2r[16];
-    {
+    float rk1r[16] = {}, rk2r[16] = {};
+    // a branch the screen did not keep here holds no weight in the tile: no scores for it
+    if (use1) {
       frag K1[NT];
       const T* r1 = (j < Nk) ? k1.row(b, h, j) : nullptr;
       Pol::template load_rows<NT>(r1, g, K1);
@@ -143,7 +148,7 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
         for (int r = 0; r < 16; ++r) rk1r[r] = __shfl(rk, crow(r, g));
       }
     }
-    if constexpr (BR == 2) {
+    if (BR == 2 && use2) {
       frag K2[NT];
       const T* r2 = (j < Nk) ? k2.row(b, h, j) : nullptr;
       Pol::template load_rows<NT>(r2, g, K2);
@@ -173,9 +178,9 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
         m2 = fmaxf(m2, valid ? S2[r] : -INFINITY);
       }
     }
-    const bool any1 = wave_ballot(__builtin_fmaf(m1, rq1, -tau) > 0.f) != 0ull;
+    const bool any1 = use1 && wave_ballot(__builtin_fmaf(m1, rq1, -tau) > 0.f) != 0ull;
     bool any2 = false;
-    if constexpr (BR == 2) any2 = wave_ballot(__builtin_fmaf(m2, rq2, -tau) > 0.f) != 0ull;
+    if constexpr (BR == 2) any2 = use2 && wave_ballot(__builtin_fmaf(m2, rq2, -tau) > 0.f) != 0ull;
     visited += BR;
     computed += (any1 ? 1 : 0) + (any2 ? 1 : 0);
     if (any1) word |= 1u << (kt & 31);
@@ -187,10 +192,10 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
         const int key = k0 + crow(r, g);
         const bool valid = qvalid && key <= pq && key < Nk;
         const float x1 = __builtin_fmaf(S1[r], rq1, -tau);
-        float a = (valid && x1 > 0.f) ? pow_p<PK>(x1, pw) : 0.f;
+        float a = (valid && any1 && x1 > 0.f) ? pow_p<PK>(x1, pw) : 0.f;
         if constexpr (BR == 2) {
           const float x2 = __builtin_fmaf(S2[r], rq2, -tau);
-          const float a2 = (valid && x2 > 0.f) ? pow_p<PK>(x2, pw) : 0.f;
+          const float a2 = (valid && any2 && x2 > 0.f) ? pow_p<PK>(x2, pw) : 0.f;
           a = __builtin_fmaf(-lam, a2, a);
         }
         C[r] = a;
