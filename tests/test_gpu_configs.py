@@ -202,3 +202,24 @@ def test_backward_with_and_without_bitmask_identical():
     c = ops.backward(q1, k1, q2, k2, v, do, beta, lam, 2.0, True, 2, norms=norms, occupancy=occ)
     for x, y in zip(a, c):
         assert torch.equal(x, y)
+
+
+def test_c2_tda_forward_fp32():
+    """The configs[2] shape and inputs in float32 (the reference's compute precision): the
+    normalised fp32 forward runs the int8 screen on the fp32 rows and the screened fp32 pass;
+    every head against the oracle at the fp32 tolerance 1e-4, bitwise determinism, and the
+    tile counters (screen-kept tiles a superset of the non-zero ones)."""
+    from tda_amd import ops
+    xs = make_inputs((4, 16, 4096, 128), 2, 5, torch.float32)
+    q1, q2, k1, k2, v = xs
+    beta = torch.full((), 1.0, device="cuda")
+    lam = torch.full((), 0.5, device="cuda")
+    stats = torch.zeros(3, dtype=torch.int64, device="cuda")
+    out = ops.forward(q1, k1, q2, k2, v, beta, lam, 2.0, True, 2, stats=stats)
+    ref = oracle_out(*xs, 1.0, 0.5, 2.0, True, 2, dtype=torch.float64)
+    _every_head(out, ref, tol=1e-4)
+    assert torch.equal(out, ops.forward(q1, k1, q2, k2, v, beta, lam, 2.0, True, 2))
+    visited, computed, checked = (int(x) for x in stats.tolist())
+    nt = 4096 // 32
+    assert visited == 2 * 64 * nt * (nt + 1) // 2
+    assert 0 < computed <= checked < visited // 10
