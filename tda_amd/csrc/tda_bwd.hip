@@ -167,20 +167,23 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
   const float* nk2 = NORM ? P.norms + norm_base(P, N_K2, bh) : nullptr;
 
   for (int kt = 0; kt <= ktl; ++kt) {
-    if (occrow) {  // tile holds a non-zero score of either branch?
-      uint32_t w = occrow[kt >> 5];
-      if constexpr (BR == 2) w |= occrow[occ_br + (kt >> 5)];
-      if (!((w >> (kt & 31)) & 1u)) continue;
+    // with the bitmask: the branches holding a non-zero weight in the tile (a branch without
+    // one adds nothing to any sum below, so its scores and products are skipped)
+    bool use1 = true, use2 = BR == 2;
+    if (occrow) {
+      use1 = (__builtin_amdgcn_readfirstlane((int)occrow[kt >> 5]) >> (kt & 31)) & 1;
+      if constexpr (BR == 2) use2 = (__builtin_amdgcn_readfirstlane((int)occrow[occ_br + (kt >> 5)]) >> (kt & 31)) & 1;
+      if (!use1 && !use2) continue;
     }
     ++visited;
     const int k0 = kt * 32;
     const int j = k0 + n32;
     f32x16 S1 = f32x16{}, S2 = f32x16{}, Dp = f32x16{};
-    {
+    if (use1) {
       const T* r = (j < Nk) ? k1.row(b, h, j) : nullptr;
       S1 = Pol::template mma_row<NT>(r, g, Q1, S1);
     }
-    if constexpr (BR == 2) {
+    if (BR == 2 && use2) {
       const T* r = (j < Nk) ? k2.row(b, h, j) : nullptr;
       S2 = Pol::template mma_row<NT>(r, g, Q2, S2);
     }
@@ -200,13 +203,13 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
         if constexpr (BR == 2) rk2 = valid ? nk2[key] : 0.f;
       }
       const float x1 = __builtin_fmaf(NORM ? S1[r] * rk1 : S1[r], rq1, -tau);
-      const bool p1 = valid && x1 > 0.f;
+      const bool p1 = use1 && valid && x1 > 0.f;
       const float ds1 = p1 ? dpow_p<PK>(x1, pw) * Dp[r] : 0.f;
       float ds2 = 0.f;
       bool p2 = false;
       if constexpr (BR == 2) {
         const float x2 = __builtin_fmaf(NORM ? S2[r] * rk2 : S2[r], rq2, -tau);
-        p2 = valid && x2 > 0.f;
+        p2 = use2 && valid && x2 > 0.f;
         ds2 = p2 ? -lam * dpow_p<PK>(x2, pw) * Dp[r] : 0.f;
         lsum = __builtin_fmaf(p2 ? pow_p<PK>(x2, pw) : 0.f, Dp[r], lsum);
       }
@@ -217,15 +220,17 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
     }
     if (!occrow && wave_ballot(any) == 0ull) continue;
     ++computed;
-    prepare_tile<Pol, D>(kt_tile, k1, b, h, k0, Nk);
+    if (use1) {
+      prepare_tile<Pol, D>(kt_tile, k1, b, h, k0, Nk);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const frag bp = Pol::pack_c(E1, s);
+      for (int s = 0; s < NS; ++s) {
+        const frag bp = Pol::pack_c(E1, s);
 #pragma unroll
-      for (int c = 0; c < ND; ++c) A1[c] = Pol::mma(kt_tile.frag(s, c), bp, A1[c]);
+        for (int c = 0; c < ND; ++c) A1[c] = Pol::mma(kt_tile.frag(s, c), bp, A1[c]);
+      }
+      release_tile<Pol>(kt_tile);
     }
-    release_tile<Pol>(kt_tile);
-    if constexpr (BR == 2) {
+    if (BR == 2 && use2) {
       prepare_tile<Pol, D>(kt_tile, k2, b, h, k0, Nk);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -327,20 +332,23 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
   const int64_t occ_br = (int64_t)BH * P.nqt * P.occ_w;  // branch-plane distance of the bitmask
 
   for (int qt = qt_first(kt, qoff); qt < P.nqt; ++qt) {
-    if (occcol) {  // tile holds a non-zero score of either branch?
-      uint32_t w = occcol[(int64_t)qt * P.occ_w];
-      if constexpr (BR == 2) w |= occcol[occ_br + (int64_t)qt * P.occ_w];
-      if (!((w >> (kt & 31)) & 1u)) continue;
+    // with the bitmask: the branches holding a non-zero weight in the tile (see bwd_dq)
+    bool use1 = true, use2 = BR == 2;
+    if (occcol) {
+      use1 = (__builtin_amdgcn_readfirstlane((int)occcol[(int64_t)qt * P.occ_w]) >> (kt & 31)) & 1;
+      if constexpr (BR == 2)
+        use2 = (__builtin_amdgcn_readfirstlane((int)occcol[occ_br + (int64_t)qt * P.occ_w]) >> (kt & 31)) & 1;
+      if (!use1 && !use2) continue;
     }
     ++visited;
     const int q0 = qt * 32;
     const int ia = q0 + n32;  // query row this lane loads for the A operand
     f32x16 S1 = f32x16{}, S2 = f32x16{}, Dp = f32x16{};
-    {
+    if (use1) {
       const T* r = (ia < Nq) ? q1.row(b, h, ia) : nullptr;
       S1 = Pol::template mma_row<NT>(r, g, K1, S1);
     }
-    if constexpr (BR == 2) {
+    if (BR == 2 && use2) {
       const T* r = (ia < Nq) ? q2.row(b, h, ia) : nullptr;
       S2 = Pol::template mma_row<NT>(r, g, K2, S2);
     }
@@ -361,14 +369,14 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
       }
       const float tau = beta * tau_coeff(qoff + qi, P.inv_d);
       const float x1 = __builtin_fmaf(NORM ? S1[r] * rk1 : S1[r], rq1, -tau);
-      const bool p1 = valid && x1 > 0.f;
+      const bool p1 = use1 && valid && x1 > 0.f;
       float a = p1 ? pow_p<PK>(x1, pw) : 0.f;
       const float ds1 = p1 ? dpow_p<PK>(x1, pw) * Dp[r] : 0.f;
       float ds2 = 0.f;
       bool p2 = false;
       if constexpr (BR == 2) {
         const float x2 = __builtin_fmaf(NORM ? S2[r] * rk2 : S2[r], rq2, -tau);
-        p2 = valid && x2 > 0.f;
+        p2 = use2 && valid && x2 > 0.f;
         a = __builtin_fmaf(-lam, p2 ? pow_p<PK>(x2, pw) : 0.f, a);
         ds2 = p2 ? -lam * dpow_p<PK>(x2, pw) * Dp[r] : 0.f;
       }
@@ -387,15 +395,17 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
       for (int c = 0; c < ND; ++c) AV[c] = Pol::mma(tile.frag(s, c), bp, AV[c]);
     }
     release_tile<Pol>(tile);
-    prepare_tile<Pol, D>(tile, q1, b, h, q0, Nq);
+    if (use1) {
+      prepare_tile<Pol, D>(tile, q1, b, h, q0, Nq);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const frag bp = Pol::pack_c(E1, s);
+      for (int s = 0; s < NS; ++s) {
+        const frag bp = Pol::pack_c(E1, s);
 #pragma unroll
-      for (int c = 0; c < ND; ++c) AK1[c] = Pol::mma(tile.frag(s, c), bp, AK1[c]);
+        for (int c = 0; c < ND; ++c) AK1[c] = Pol::mma(tile.frag(s, c), bp, AK1[c]);
+      }
+      release_tile<Pol>(tile);
     }
-    release_tile<Pol>(tile);
-    if constexpr (BR == 2) {
+    if (BR == 2 && use2) {
       prepare_tile<Pol, D>(tile, q2, b, h, q0, Nq);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {

@@ -185,11 +185,14 @@ def test_occupancy_and_norms_match_oracle(shape, heads):
     assert computed <= checked <= 2.5 * computed
 
 
-def test_backward_with_and_without_bitmask_identical():
+@pytest.mark.parametrize("dtype", [BF, torch.float32])
+def test_backward_with_and_without_bitmask_identical(dtype):
+    """With the forward's bitmask the backward skips the tiles, and (fp32) the branches of a
+    tile, that hold no non-zero weight; without it every tile is scored.  Bitwise the same."""
     from tda_amd import ops
     shape = (1, 4, 1000, 128)
-    xs = make_inputs(shape, 5, 5, BF)
-    (do,) = make_inputs(shape, 6, 1, BF)
+    xs = make_inputs(shape, 5, 5, dtype)
+    (do,) = make_inputs(shape, 6, 1, dtype)
     q1, q2, k1, k2, v = xs
     beta = torch.full((), 1.0, device="cuda")
     lam = torch.full((), 0.5, device="cuda")
