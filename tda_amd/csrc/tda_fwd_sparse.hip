@@ -281,12 +281,17 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
-// Signed byte j of an int8 lane value packed 4 per int (two's complement).
-__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
-  return (a & 255) | ((b & 255) << 8) | ((c & 255) << 16) | ((d & 255) << 24);
-}
-__device__ __forceinline__ int quant(float x, float inv) {
-  return min(127, max(-127, (int)__builtin_rintf(x * inv)));
+// rint(x y) of the exact product, |x y| < 2^22, by one fma: x y + 1.5 * 2^23 rounds to an integer
+// (ties to even) whose low bits are that integer's two's complement; returns the sum.  The
+// integer as a float is the sum minus the constant (exact).
+constexpr float kRintMagic = 12582912.0f;
+__device__ __forceinline__ float rint_fma(float x, float y) { return __builtin_fmaf(x, y, kRintMagic); }
+// The low bytes of four rint_fma sums (int8 values in [-127, 127]) packed into one int, byte e
+// from argument e, by three byte permutes.
+__device__ __forceinline__ int pack4_rint(float a, float b, float c, float d) {
+  const uint32_t ab = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, a), 0x0c0c0400u);
+  const uint32_t cd = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, d), __builtin_bit_cast(uint32_t, c), 0x0c0c0400u);
+  return (int)__builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
 __device__ __forceinline__ int max16i(const i32x16& v) {
@@ -394,17 +399,17 @@ __global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(kh[j]));
     m = group_max<LPR>(m);
+    // every |kh| <= m, so b = rint(kh 127 / m) of the exact product lies in [-127, 127]
     const float sc = m * (1.f / 127.f), inv = m > 0.f ? 127.f / m : 0.f;
-    int b[16];
-    float e2 = 0.f;
+    float rs[16], e2 = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      b[j] = quant(kh[j], inv);
-      const float r = __builtin_fmaf(-sc, (float)b[j], kh[j]);
+      rs[j] = rint_fma(kh[j], inv);
+      const float r = __builtin_fmaf(-sc, rs[j] - kRintMagic, kh[j]);
       e2 = __builtin_fmaf(r, r, e2);
     }
-    packed[u] = i32x4{pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7]), pack4(b[8], b[9], b[10], b[11]),
-                      pack4(b[12], b[13], b[14], b[15])};
+    packed[u] = i32x4{pack4_rint(rs[0], rs[1], rs[2], rs[3]), pack4_rint(rs[4], rs[5], rs[6], rs[7]),
+                      pack4_rint(rs[8], rs[9], rs[10], rs[11]), pack4_rint(rs[12], rs[13], rs[14], rs[15])};
     se[u] = float2{sc, res_bound(group_sum<LPR>(e2))};
   }
 #pragma unroll
@@ -603,12 +608,6 @@ __device__ __forceinline__ void wait_vm() {  // vmcnt(N) with the other counters
   static_assert(N >= 0 && N < 64, "vmcnt field");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
-// rint(x y) of the exact product, |x y| < 2^22, by one fma: x y + 1.5 * 2^23 rounds to an integer
-// (ties to even) whose low bits are that integer's two's complement; returns the sum.  The
-// integer as a float is the sum minus the constant (exact).
-constexpr float kRintMagic = 12582912.0f;
-__device__ __forceinline__ float rint_fma(float x, float y) { return __builtin_fmaf(x, y, kRintMagic); }
-
 template <int D, class T>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) fwd_screen_i8(FwdParams P, int BR) {
   constexpr int QPW = 2, NTHR = 256, TPI = I8_TPI;
@@ -767,18 +766,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
       int w[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        int a[4];
+        float rs[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int j = 4 * u + e;
           float x = qv[t][j] * sc;
           if (any_nonfinite) x = __builtin_isfinite(x) ? x : 0.f;
-          const float rs = rint_fma(x, inv);  // rint(x inv) of the exact product, |x inv| <= 127 (1 + 2^-22)
-          a[e] = __builtin_bit_cast(int, rs);  // low byte: the int8 value
-          const float r = __builtin_fmaf(-sq[s], rs - kRintMagic, x);
+          rs[e] = rint_fma(x, inv);  // rint(x inv) of the exact product, |x inv| <= 127 (1 + 2^-22)
+          const float r = __builtin_fmaf(-sq[s], rs[e] - kRintMagic, x);
           r2 = __builtin_fmaf(r, r, r2);
         }
-        w[u] = pack4(a[0], a[1], a[2], a[3]);
+        w[u] = pack4_rint(rs[0], rs[1], rs[2], rs[3]);
       }
       A8[s][t] = i32x4{w[0], w[1], w[2], w[3]};
       __builtin_amdgcn_sched_barrier(0);  // one step's values live at a time

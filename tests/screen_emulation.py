@@ -5,9 +5,10 @@ The screen (tda_amd/csrc/tda_fwd_sparse.hip: key_prep and fwd_screen_i8) keeps k
 query tile when, for some row i of the tile,
     fl(fl(float(A_ij) * fl(sq * s_j))) > thr_j,
 with
-    kh_j = fl(k_j rk_j),  s_j = max|kh_j| / 127,  b_j = rint(fl(kh_j * fl(127 / max|kh_j|)))   (key_prep)
+    kh_j = fl(k_j rk_j),  s_j = max|kh_j| / 127,  b_j = rint(kh_j * fl(127 / max|kh_j|))   (key_prep)
     qh_i = fl(q_i rq_i),  sq = m / 127 with m = max_i rq_i max|q_i| over the tile's rows,
-    a_i = rint(qh_i * fl(127 / m)) of the exact product (one fma against 1.5 * 2^23),
+    a_i = rint(qh_i * fl(127 / m)),
+both rints of the exact product (one fma against 1.5 * 2^23),
     A_ij = a_i . b_j (exact int32)
 (rint ties to even)
     ek_j, eq >= the norms of the residuals kh_j - s_j b_j and qh_i - sq a_i (eq: the tile's
@@ -65,7 +66,7 @@ def quant_key(k: np.ndarray):
     m = F32(np.max(np.abs(kh)))
     s = F32(m * F32(1.0 / 127.0))
     inv = F32(127.0) / m if m > 0 else F32(0.0)
-    b = np.rint((kh * inv).astype(np.float32))
+    b = rint_prod(kh, inv)
     assert np.all(np.abs(b) <= 127)
     r = _fma32(-s, b.astype(np.float32), kh)
     return b.astype(np.int64), float(s), res_bound(r), rk, kh
