@@ -9,7 +9,9 @@ from .api import (  # noqa: F401
     threshold_rela_triton,
 )
 from .layer import ThresholdDifferentialAttention  # noqa: F401
+from .ops import grad_prealloc, grad_prealloc_enabled, set_grad_prealloc  # noqa: F401
 from .stats import TileStats, tile_sparsity  # noqa: F401
 
 __all__ = ["threshold_rela_triton", "differential_threshold_rela_triton", "ThresholdRelaFunction",
-           "ThresholdDifferentialAttention", "tile_sparsity", "TileStats"]
+           "ThresholdDifferentialAttention", "tile_sparsity", "TileStats", "set_grad_prealloc",
+           "grad_prealloc", "grad_prealloc_enabled"]

@@ -61,7 +61,8 @@ def _scalar(x, device, name):
     if isinstance(x, torch.Tensor):
         if x.numel() != 1:
             raise ValueError(f"{name} must be a scalar, got shape {tuple(x.shape)}")
-        return x.to(device=device, dtype=torch.float32).reshape(())
+        x = x.to(device=device, dtype=torch.float32)
+        return x if x.dim() == 0 else x.reshape(())
     return torch.full((), float(x), dtype=torch.float32, device=device)
 
 
@@ -171,7 +172,8 @@ class ThresholdRelaFunction(torch.autograd.Function):
             _, occ = ops.side_buffers(qc.shape, 1, False, qc.device, kc.shape[2])
             if cdt == torch.bfloat16:
                 pairs = ops.pair_buffer(qc.shape, 1, qc.device)
-                gbuf, grads = ops.grad_buffers(qc, kc, None, None, vc, 1)
+                if all(ctx.needs_input_grad[:3]) and ops.grad_prealloc_enabled():
+                    gbuf, grads = ops.grad_buffers(qc, kc, None, None, vc, 1)
         out = ops.forward(qc, kc, None, None, vc, beta_t, None, p, False, 1, None, occ, q_offset=off,
                           pairs=pairs, zero=gbuf)
         ctx.save_for_backward(qc, kc, vc, beta_t, occ, pairs, *grads)
@@ -187,9 +189,10 @@ class ThresholdRelaFunction(torch.autograd.Function):
         p, off = ctx.cfg
         d = ctx.d
         dout = _pad(dout.to(qc.dtype), qc.shape[-1])
+        zeroed, ctx.zeroed = ctx.zeroed, False  # the cleared buffers serve the first backward only
         dq, dk, _, _, dv, _, _ = ops.backward(qc, kc, None, None, vc, dout, beta_t, None, p, False, 1,
                                               None, occ, q_offset=off, pairs=pairs,
-                                              grads=grads if ctx.zeroed else None)
+                                              grads=grads if zeroed else None)
         dq, dk, dv = (g[..., :d] if g.shape[-1] != d else g for g in (dq, dk, dv))
         dq, dk, dv = (g if g.dtype == ctx.dtype else g.to(ctx.dtype) for g in (dq, dk, dv))
         ng = ctx.needs_input_grad
