@@ -66,7 +66,7 @@ extern "C" {
 #define TDA_OK                 0
 #define TDA_ERR_NULL_POINTER  -1   /* a required pointer is NULL */
 #define TDA_ERR_SHAPE         -2   /* batch/heads/seq_len out of range */
-#define TDA_ERR_HEAD_DIM      -3   /* head_dim not in {64, 128} */
+#define TDA_ERR_HEAD_DIM      -3   /* head_dim not in {64, 128, 256} */
 #define TDA_ERR_DTYPE         -4   /* dtype not TDA_DTYPE_F32 / TDA_DTYPE_BF16 */
 #define TDA_ERR_LAYOUT        -5   /* stride[3] != 1, 16-byte alignment broken, or a
                                       sequence stride above 2^25 elements */

@@ -20,12 +20,13 @@ Superset behaviour (all results identical where the reference is defined):
     and the row sees keys j <= q_offset + i (KV-cache decode, chunked prefill).  The default
     q_offset is max(Nk - Nq, 0): the queries are the last Nq positions of the keys, and 0
     when Nq = Nk, which is the reference's case.
-Only the causal form exists, as in the reference.  Supported head_dim: 16, 32, 64, 128 (the
-reference takes any power of two >= 16, TTA:348, :366-368).  The kernels run d = 64 and 128;
+Only the causal form exists, as in the reference.  Supported head_dim: 16, 32, 64, 128, 256
+(the reference takes any power of two >= 16, TTA:348, :366-368).  The kernels run d = 64, 128
+and 256 (256: column-split kernels, each wave owning half of the output columns);
 d = 16 and 32 are computed at d = 64 with the rows zero-padded (dot products and norms
 unchanged) and beta scaled by sqrt(64 / d), so that tau = beta sqrt(2 ln(P+1) / d) is the same
 threshold; the padding's gradients are dropped and beta's gradient flows through the scaling.
-d = 256 raises ValueError (the kernels' register budgets are sized for d <= 128).
+Other head_dims raise ValueError.
 """
 from __future__ import annotations
 
@@ -36,7 +37,7 @@ import torch.nn.functional as F
 
 from . import ops
 
-_KERNEL_DIMS = (64, 128)
+_KERNEL_DIMS = (64, 128, 256)
 _PADDED_DIMS = (16, 32)  # computed at d = 64
 
 
@@ -46,7 +47,7 @@ def _head_dim(d: int) -> int:
         return d
     if d in _PADDED_DIMS:
         return 64
-    raise ValueError(f"head_dim must be 16, 32, 64 or 128, got {d}")
+    raise ValueError(f"head_dim must be 16, 32, 64, 128 or 256, got {d}")
 
 
 def _pad(t: torch.Tensor, dk: int) -> torch.Tensor:

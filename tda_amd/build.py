@@ -29,7 +29,7 @@ HIP_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 
 HIP_SOURCES = ["tda_fwd.hip", "tda_fwd_sparse.hip", "tda_fwd_decode.hip", "tda_bwd.hip", "tda_bwd_fast.hip",
-               "tda_noalloc.hip"]
+               "tda_wide.hip", "tda_noalloc.hip"]
 HOST_SOURCES = ["tda_host.cpp"]
 # host-only code that calls the HIP runtime API (no device code): g++ against the ROCm headers
 HIP_HOST_SOURCES = ["tda_timing.cpp"]

@@ -484,8 +484,10 @@ int launch_bwd_finish(const BwdParams& p, int branches, int64_t items, void* str
   return (int)hipGetLastError();
 }
 
-// bf16 runs the bitmask-driven kernels of tda_bwd_fast.hip; fp32 runs bwd_dq / bwd_dkv.
+// head_dim 256 runs the column-split kernels of tda_wide.hip; otherwise bf16 runs the
+// bitmask-driven kernels of tda_bwd_fast.hip and fp32 runs bwd_dq / bwd_dkv.
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream) {
+  if (k.d == 256) return launch_bwd_wide(p, k, stream);
   return k.dtype == 1 ? launch_bwd_fast(p, k, stream) : bsel_d<PolF32>(p, k, stream);
 }
 

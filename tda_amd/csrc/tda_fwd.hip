@@ -320,12 +320,16 @@ int launch_zero(const FwdParams& p, void* stream) {
   return (int)hipGetLastError();
 }
 
-// bf16 runs the screen + sparse A.V kernels (tda_fwd_sparse.hip), or with a single query tile
+// head_dim 256 runs tda_wide.hip; otherwise bf16 runs the screen + sparse A.V kernels (tda_fwd_sparse.hip), or with a single query tile
 // the split-key decode kernels (tda_fwd_decode.hip); fp32 runs fwd_wave, after the int8 screen
 // when normalised with more than one query tile.  The screen clears the call's zero range; the
 // other paths launch zero_range.
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream) {
   int e;
+  if (k.d == 256) {  // both dtypes: the column-split kernels of tda_wide.hip (no screen)
+    e = launch_fwd_wide(p, k, stream);
+    return e ? e : launch_zero(p, stream);
+  }
   if (k.dtype == 1 && !(p.nqt == 1 && p.part)) return launch_fwd_sparse(p, k, stream);
   if (k.dtype == 1) e = launch_fwd_decode(p, k, p.part, stream);
   else e = sel_d<PolF32>(p, k, stream);

@@ -49,7 +49,7 @@ int32_t check_common(const Common& c) {
   if (c.dtype != TDA_DTYPE_F32 && c.dtype != TDA_DTYPE_BF16) return TDA_ERR_DTYPE;
   if (c.branches != 1 && c.branches != 2) return TDA_ERR_BRANCHES;
   if (c.causal != 1) return TDA_ERR_CAUSAL;
-  if (c.head_dim != 64 && c.head_dim != 128) return TDA_ERR_HEAD_DIM;
+  if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) return TDA_ERR_HEAD_DIM;
   if (c.batch < 1 || c.heads < 1 || c.seq_len < 1) return TDA_ERR_SHAPE;
   if (c.seq_len > (int64_t(1) << 30)) return TDA_ERR_SHAPE;
   if (c.batch * c.heads > (int64_t(1) << 24)) return TDA_ERR_SHAPE;
@@ -102,9 +102,9 @@ int64_t fwd_ws_bytes(int64_t bh, int64_t seq_len, int64_t seq_len_kv, int64_t br
          fwd_cand_bytes(bh, seq_len, branches) + fwd_k8_bytes(bh, seq_len, seq_len_kv, branches, kd);
 }
 // Row bytes of the int8 keys a call needs (0: it uses none): the normalised calls, whose int8
-// screen runs on bf16 and on fp32 rows.
+// screen runs on bf16 and on fp32 rows, up to head_dim 128 (head_dim 256 has no screen).
 int64_t k8_row_bytes(const tda_fwd_args& a) {
-  return a.normalize ? a.head_dim : 0;
+  return a.normalize && a.head_dim <= 128 ? a.head_dim : 0;
 }
 constexpr int64_t kMaxHeadDim = 128;  // the size functions without head_dim assume the largest
 bool size_args_ok(int64_t batch, int64_t heads, int64_t seq_len, int64_t seq_len_kv, int32_t branches) {
@@ -154,7 +154,7 @@ const char* tda_error_string(int32_t code) {
     case TDA_OK: return "ok";
     case TDA_ERR_NULL_POINTER: return "a required pointer is NULL";
     case TDA_ERR_SHAPE: return "batch, heads or seq_len out of range";
-    case TDA_ERR_HEAD_DIM: return "head_dim must be 64 or 128";
+    case TDA_ERR_HEAD_DIM: return "head_dim must be 64, 128 or 256";
     case TDA_ERR_DTYPE: return "dtype must be float32 or bfloat16";
     case TDA_ERR_LAYOUT:
       return "tensor layout unsupported: last-dim stride must be 1, strides/pointers 16-byte aligned, "

@@ -128,7 +128,7 @@ struct BwdParams {
 // Kernel-family launchers (return a hipError_t value).  Template selection happens inside.
 struct KernelKey {
   int dtype;      // 0 f32, 1 bf16
-  int d;          // 64 or 128
+  int d;          // 64, 128 or 256
   int branches;   // 1 or 2
   int pkind;      // 2: p == 2, 1: p == 1, 0: general
   int normalize;  // 0 or 1
@@ -140,6 +140,9 @@ int launch_fwd_screen_f32(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_fwd_decode(const FwdParams& p, const KernelKey& k, float* part, void* stream);
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream);
+// head_dim 256 (tda_wide.hip): the column-split forward and backward
+int launch_fwd_wide(const FwdParams& p, const KernelKey& k, void* stream);
+int launch_bwd_wide(const BwdParams& p, const KernelKey& k, void* stream);
 // Set the forward's zero range to zero (paths without the screen, which clears it otherwise).
 int launch_zero(const FwdParams& p, void* stream);
 // Sum the (dbeta, dlambda) partial pairs ws[2 * item], item < items, in a fixed order.

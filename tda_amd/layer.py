@@ -29,7 +29,7 @@ class ThresholdDifferentialAttention(nn.Module):
     Args:
         embed_dim: model width E of the input and output.
         num_heads: H.
-        head_dim: d, 16, 32, 64 or 128 (default E // H).
+        head_dim: d, 16, 32, 64, 128 or 256 (default E // H).
         relu_power: p of ReLU(.)^p.
         normalize: cosine scores (L2-normalised q and k rows).
         beta_init, lambda_init: initial threshold scale and branch weight.
@@ -44,8 +44,8 @@ class ThresholdDifferentialAttention(nn.Module):
                  differential: bool = True, bias: bool = False, device=None, dtype=None):
         super().__init__()
         head_dim = head_dim if head_dim is not None else embed_dim // num_heads
-        if head_dim not in (16, 32, 64, 128):
-            raise ValueError(f"head_dim must be 16, 32, 64 or 128, got {head_dim}")
+        if head_dim not in (16, 32, 64, 128, 256):
+            raise ValueError(f"head_dim must be 16, 32, 64, 128 or 256, got {head_dim}")
         self.embed_dim, self.num_heads, self.head_dim = embed_dim, num_heads, head_dim
         self.relu_power, self.normalize, self.differential = float(relu_power), bool(normalize), differential
         self.n_proj = 5 if differential else 3  # q1, q2, k1, k2, v  |  q, k, v

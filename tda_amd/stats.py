@@ -64,8 +64,8 @@ def tile_sparsity(q, k, v, beta, relu_power=2.0, normalize=False, *, q2=None, k2
                       kv_from=1 if branches == 1 else 2)
     if q.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError(f"tile_sparsity takes float32 or bfloat16 inputs, got {q.dtype}")
-    if q.shape[-1] not in (64, 128):
-        raise ValueError(f"head_dim must be 64 or 128, got {q.shape[-1]}")
+    if q.shape[-1] not in (64, 128, 256):
+        raise ValueError(f"head_dim must be 64, 128 or 256, got {q.shape[-1]}")
     b, h, n, _ = q.shape
     nk = k.shape[2]
     if n == 0 or nk == 0:
@@ -84,7 +84,8 @@ def tile_sparsity(q, k, v, beta, relu_power=2.0, normalize=False, *, q2=None, k2
     t, tk = (n + TILE - 1) // TILE, (nk + TILE - 1) // TILE
     occupancy = _unpack(occ, branches, b, h, t, tk)
     return out, TileStats(occupancy=occupancy, tiles_causal=causal, tiles_nonzero=nonzero,
-                          tiles_screened=screened if q.dtype == torch.bfloat16 or (normalize and n > TILE)
+                          tiles_screened=screened if q.shape[-1] <= 128 and (q.dtype == torch.bfloat16 or
+                                                                             (normalize and n > TILE))
                           else None)
 
 

@@ -123,7 +123,8 @@ def test_valid_args_pass():
     (lambda a: setattr(a, "branches", 3), _abi.ERR_BRANCHES),
     (lambda a: setattr(a, "causal", 0), _abi.ERR_CAUSAL),
     (lambda a: setattr(a, "head_dim", 96), _abi.ERR_HEAD_DIM),
-    (lambda a: setattr(a, "head_dim", 256), _abi.ERR_HEAD_DIM),
+    (lambda a: setattr(a, "head_dim", 512), _abi.ERR_HEAD_DIM),
+    (lambda a: setattr(a, "head_dim", 32), _abi.ERR_HEAD_DIM),
     (lambda a: setattr(a, "seq_len", 0), _abi.ERR_SHAPE),
     (lambda a: setattr(a, "batch", 0), _abi.ERR_SHAPE),
     (lambda a: setattr(a, "relu_power", -1.0), _abi.ERR_POWER),
@@ -181,6 +182,10 @@ def test_workspace_for_one_call():
     b.head_dim = 96
     assert lib.tda_fwd_workspace_bytes_for(ctypes.byref(b)) == 0
     assert lib.tda_fwd_workspace_bytes_for(None) == 0
+    w = _fwd_args(shape=(2, 3, 100, 256))  # head_dim 256 has no screen: no int8 keys
+    a.normalize, a.dtype = 0, _abi.DTYPE_BF16
+    assert lib.tda_fwd_workspace_bytes_for(ctypes.byref(w)) == lib.tda_fwd_workspace_bytes_for(ctypes.byref(a))
+    assert lib.tda_validate_fwd(ctypes.byref(w)) == _abi.OK
 
 
 def test_zero_range_args_pass():

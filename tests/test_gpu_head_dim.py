@@ -3,7 +3,8 @@ public functions compute them at d = 64 with zero-padded rows and beta scaled by
 (tda_amd/api.py).  Checked against the oracle at the caller's d (its tau uses that d, so the
 padding and the scaling are pinned independently): outputs, every gradient, dbeta and dlambda,
 fp32 <= 1e-4 and bf16 <= 2e-2, normalize on and off, and through ThresholdRelaFunction and the
-nn.Module.  d = 256 is refused with ValueError."""
+nn.Module.  Other head_dims than 16, 32, 64, 128 and 256 are refused with ValueError (256:
+tests/test_gpu_wide.py)."""
 import pytest
 import torch
 
@@ -81,7 +82,7 @@ def test_module_head_dim_32():
     assert torch.isfinite(x.grad).all()
 
 
-@pytest.mark.parametrize("d", [8, 48, 256])
+@pytest.mark.parametrize("d", [8, 48, 96, 512])
 def test_unsupported_head_dim_raises(d):
     from tda_amd import threshold_rela_triton
     q, k, v = make_inputs((1, 1, 16, d), 1, 3, torch.float32)
