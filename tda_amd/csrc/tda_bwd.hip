@@ -43,6 +43,30 @@ __device__ __forceinline__ void release_tile(TT&) {
   if constexpr (sizeof(typename Pol::T) == 2) wave_lds_sync();
 }
 
+// acc += A B^T over d with both operands' row fragments streamed from memory (A: lane (m, g)
+// supplies row ra of tile row m; B: lane (n, g) supplies row rb): the element order of
+// load_rows / mma_row, so the sums are bitwise those of a resident operand.  A null row reads
+// as zeros.  The fp32 passes keep no operand resident: three resident fragment sets of a 32-row
+// tile (192 VGPRs at d = 128) next to the accumulators spilled to scratch.
+template <class Pol, int NT>
+__device__ __forceinline__ f32x16 mma_rows2(const typename Pol::T* ra, const typename Pol::T* rb, int g, f32x16 acc) {
+  if constexpr (sizeof(typename Pol::T) == 4) {
+    const f32x4* pa = reinterpret_cast<const f32x4*>(ra ? ra + g * NT : ra);
+    const f32x4* pb = reinterpret_cast<const f32x4*>(rb ? rb + g * NT : rb);
+#pragma unroll
+    for (int m = 0; m < NT / 4; ++m) {
+      const f32x4 a = ra ? pa[m] : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 b = rb ? pb[m] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = Pol::mma(a[e], b[e], acc);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc = Pol::mma(Pol::load_row(ra, t, g), Pol::load_row(rb, t, g), acc);
+  }
+  return acc;
+}
+
 // Apply the F.normalize backward to a gradient tile held in the transposed C layout
 // (lane = one row, value r of column block c = element 32c + crow(r, g)) and store it.
 template <class Pol, int D, bool NORM>
@@ -126,19 +150,9 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
   const TRef<T> dq1{(T*)P.grad[0], P.s[B_DQ1][0], P.s[B_DQ1][1], P.s[B_DQ1][2]};
   const TRef<T> dq2{(T*)P.grad[2], P.s[B_DQ2][0], P.s[B_DQ2][1], P.s[B_DQ2][2]};
 
-  frag Q1[NT], Q2[NT], DO[NT];
-  {
-    const T* r1 = qvalid ? q1.row(b, h, i) : nullptr;
-    const T* ro = qvalid ? dO.row(b, h, i) : nullptr;
-    {
-      Pol::template load_rows<NT>(r1, g, Q1);
-      Pol::template load_rows<NT>(ro, g, DO);
-    }
-    if constexpr (BR == 2) {
-      const T* r2 = qvalid ? q2.row(b, h, i) : nullptr;
-      Pol::template load_rows<NT>(r2, g, Q2);
-    }
-  }
+  const T* qr1 = qvalid ? q1.row(b, h, i) : nullptr;  // this lane's rows (B operands, streamed)
+  const T* qr2 = (BR == 2 && qvalid) ? q2.row(b, h, i) : nullptr;
+  const T* dor = qvalid ? dO.row(b, h, i) : nullptr;
   float rq1 = 1.f, rq2 = 1.f;
   if constexpr (NORM) {
     if (qvalid) {
@@ -166,14 +180,31 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
   const float* nk1 = NORM ? P.norms + norm_base(P, N_K1, bh) : nullptr;
   const float* nk2 = NORM ? P.norms + norm_base(P, N_K2, bh) : nullptr;
 
-  for (int kt = 0; kt <= ktl; ++kt) {
+  // With the bitmask the wave visits only the tiles with a bit set in either branch, one load
+  // per bitmask word (not per key tile): the set bits of the current word, then the next word.
+  int cw = -1;
+  uint32_t w1 = 0u, w2 = 0u;  // the branches' bits of word cw
+  auto next_kt = [&](int kt) {
+    if (!occrow) return kt;
+    while (kt <= ktl) {
+      if ((kt >> 5) != cw) {
+        cw = kt >> 5;
+        w1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)occrow[cw]);
+        if constexpr (BR == 2) w2 = (uint32_t)__builtin_amdgcn_readfirstlane((int)occrow[occ_br + cw]);
+      }
+      const uint32_t m = (w1 | w2) >> (kt & 31);
+      if (m) return kt + __builtin_ctz(m);
+      kt = (kt | 31) + 1;
+    }
+    return kt;
+  };
+  for (int kt = next_kt(0); kt <= ktl; kt = next_kt(kt + 1)) {
     // with the bitmask: the branches holding a non-zero weight in the tile (a branch without
     // one adds nothing to any sum below, so its scores and products are skipped)
     bool use1 = true, use2 = BR == 2;
     if (occrow) {
-      use1 = (__builtin_amdgcn_readfirstlane((int)occrow[kt >> 5]) >> (kt & 31)) & 1;
-      if constexpr (BR == 2) use2 = (__builtin_amdgcn_readfirstlane((int)occrow[occ_br + (kt >> 5)]) >> (kt & 31)) & 1;
-      if (!use1 && !use2) continue;
+      use1 = (w1 >> (kt & 31)) & 1u;
+      if constexpr (BR == 2) use2 = (w2 >> (kt & 31)) & 1u;
     }
     ++visited;
     const int k0 = kt * 32;
@@ -181,15 +212,15 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
     f32x16 S1 = f32x16{}, S2 = f32x16{}, Dp = f32x16{};
     if (use1) {
       const T* r = (j < Nk) ? k1.row(b, h, j) : nullptr;
-      S1 = Pol::template mma_row<NT>(r, g, Q1, S1);
+      S1 = mma_rows2<Pol, NT>(r, qr1, g, S1);
     }
     if (BR == 2 && use2) {
       const T* r = (j < Nk) ? k2.row(b, h, j) : nullptr;
-      S2 = Pol::template mma_row<NT>(r, g, Q2, S2);
+      S2 = mma_rows2<Pol, NT>(r, qr2, g, S2);
     }
     {
       const T* r = (j < Nk) ? vv.row(b, h, j) : nullptr;
-      Dp = Pol::template mma_row<NT>(r, g, DO, Dp);
+      Dp = mma_rows2<Pol, NT>(r, dor, g, Dp);
     }
     f32x16 E1, E2;
     bool any = false;
@@ -293,19 +324,9 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
   const TRef<T> dk2{(T*)P.grad[3], P.s[B_DK2][0], P.s[B_DK2][1], P.s[B_DK2][2]};
   const TRef<T> dvv{(T*)P.grad[4], P.s[B_DV][0], P.s[B_DV][1], P.s[B_DV][2]};
 
-  frag K1[NT], K2[NT], V[NT];
-  {
-    const T* r1 = kvalid ? k1.row(b, h, j) : nullptr;
-    const T* rv = kvalid ? vv.row(b, h, j) : nullptr;
-    {
-      Pol::template load_rows<NT>(r1, g, K1);
-      Pol::template load_rows<NT>(rv, g, V);
-    }
-    if constexpr (BR == 2) {
-      const T* r2 = kvalid ? k2.row(b, h, j) : nullptr;
-      Pol::template load_rows<NT>(r2, g, K2);
-    }
-  }
+  const T* kr1 = kvalid ? k1.row(b, h, j) : nullptr;  // this lane's rows (B operands, streamed)
+  const T* kr2 = (BR == 2 && kvalid) ? k2.row(b, h, j) : nullptr;
+  const T* vr = kvalid ? vv.row(b, h, j) : nullptr;
   float rk1 = 1.f, rk2 = 1.f;
   if constexpr (NORM) {
     if (kvalid) {
@@ -331,14 +352,36 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
   const uint32_t* occcol = P.occ ? P.occ + (int64_t)bh * P.nqt * P.occ_w + (kt >> 5) : nullptr;
   const int64_t occ_br = (int64_t)BH * P.nqt * P.occ_w;  // branch-plane distance of the bitmask
 
-  for (int qt = qt_first(kt, qoff); qt < P.nqt; ++qt) {
+  // With the bitmask the wave visits only the query tiles with the key tile's bit set in either
+  // branch: the bits of 64 query tiles come in one lane-parallel load round and two ballots.
+  int cb = -1;
+  uint64_t m1 = 0ull, m2 = 0ull;  // the branches' bits of query tiles cb .. cb + 63
+  auto next_qt = [&](int qt) {
+    if (!occcol) return qt;
+    while (qt < P.nqt) {
+      if ((qt & ~63) != cb) {
+        cb = qt & ~63;
+        const int qq = cb + l;
+        uint32_t a = 0u, c = 0u;
+        if (qq < P.nqt) {
+          a = occcol[(int64_t)qq * P.occ_w];
+          if constexpr (BR == 2) c = occcol[occ_br + (int64_t)qq * P.occ_w];
+        }
+        m1 = wave_ballot((a >> (kt & 31)) & 1u);
+        m2 = BR == 2 ? wave_ballot((c >> (kt & 31)) & 1u) : 0ull;
+      }
+      const uint64_t m = (m1 | m2) >> (qt & 63);
+      if (m) return qt + (int)__builtin_ctzll(m);
+      qt = (qt | 63) + 1;
+    }
+    return qt;
+  };
+  for (int qt = next_qt(qt_first(kt, qoff)); qt < P.nqt; qt = next_qt(qt + 1)) {
     // with the bitmask: the branches holding a non-zero weight in the tile (see bwd_dq)
     bool use1 = true, use2 = BR == 2;
     if (occcol) {
-      use1 = (__builtin_amdgcn_readfirstlane((int)occcol[(int64_t)qt * P.occ_w]) >> (kt & 31)) & 1;
-      if constexpr (BR == 2)
-        use2 = (__builtin_amdgcn_readfirstlane((int)occcol[occ_br + (int64_t)qt * P.occ_w]) >> (kt & 31)) & 1;
-      if (!use1 && !use2) continue;
+      use1 = (m1 >> (qt & 63)) & 1ull;
+      if constexpr (BR == 2) use2 = (m2 >> (qt & 63)) & 1ull;
     }
     ++visited;
     const int q0 = qt * 32;
@@ -346,15 +389,15 @@ __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
     f32x16 S1 = f32x16{}, S2 = f32x16{}, Dp = f32x16{};
     if (use1) {
       const T* r = (ia < Nq) ? q1.row(b, h, ia) : nullptr;
-      S1 = Pol::template mma_row<NT>(r, g, K1, S1);
+      S1 = mma_rows2<Pol, NT>(r, kr1, g, S1);
     }
     if (BR == 2 && use2) {
       const T* r = (ia < Nq) ? q2.row(b, h, ia) : nullptr;
-      S2 = Pol::template mma_row<NT>(r, g, K2, S2);
+      S2 = mma_rows2<Pol, NT>(r, kr2, g, S2);
     }
     {
       const T* r = (ia < Nq) ? dO.row(b, h, ia) : nullptr;
-      Dp = Pol::template mma_row<NT>(r, g, V, Dp);
+      Dp = mma_rows2<Pol, NT>(r, vr, g, Dp);
     }
     f32x16 EV, E1, E2;
     bool any = false;

@@ -7,6 +7,8 @@
 // product is issued only when a wave-wide ballot finds a non-zero entry (ReLU leaves almost
 // every tile empty: TDA is ultra-sparse).  The two branches share one accumulator:
 // out = sum_j (A1_ij - clamp(lambda) A2_ij) v_j, so the differential combine is free.
+#include <type_traits>
+
 #include "tda_common.hpp"
 #include "tda_params.hpp"
 #include "tda_pos.hpp"
@@ -30,8 +32,32 @@ template <int D> struct TTileSel<PolF32, D> { using type = TTileF32<D>; };
 // bitmask names every key tile holding a non-zero weight (a superset), so the wave visits only
 // those tiles; the inverse norms come from the table the screen and key_prep wrote (the values
 // the screen's bound is stated for), and the bitmask words are rewritten exactly.
-template <class Pol, int D, int BR, int PK, bool NORM, bool SCR = false>
+//
+// QUEUE (with SCR): only the query tiles the fp32 candidate pass (fwd_cand_f32) queued, whose
+// candidate lists did not fit; the waves take them in turn.
+template <class Pol, int D, int BR, int PK, bool NORM, bool SCR>
+__device__ __forceinline__ void fwd_wave_tile(const FwdParams& P, int qt, int bh, int wv);
+
+template <class Pol, int D, int BR, int PK, bool NORM, bool SCR = false, bool QUEUE = false>
 __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
+  static_assert(!QUEUE || SCR, "the queue comes from the screened candidate pass");
+  const int wv = threadIdx.x >> 6;
+  const int BH = P.B * P.H;
+  if constexpr (QUEUE) {
+    const uint32_t queued = P.pvq[0];
+    for (uint32_t k = blockIdx.x * 4u + (uint32_t)wv; k < queued; k += gridDim.x * 4u) {
+      const int v = (int)P.pvq[1 + k];
+      fwd_wave_tile<Pol, D, BR, PK, NORM, SCR>(P, v % P.nqt, v / P.nqt, wv);
+    }
+    return;
+  }
+  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+  if (item >= (int64_t)BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
+  fwd_wave_tile<Pol, D, BR, PK, NORM, SCR>(P, P.nqt - 1 - (int)(item / BH), (int)(item % BH), wv);
+}
+
+template <class Pol, int D, int BR, int PK, bool NORM, bool SCR>
+__device__ __forceinline__ void fwd_wave_tile(const FwdParams& P, int qt, int bh, int wv) {
   static_assert(!SCR || NORM, "the screened pass is the normalised one");
   using T = typename Pol::T;
   using frag = typename Pol::frag;
@@ -40,12 +66,8 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
   constexpr int ND = D / 32;       // 32-wide column blocks of the output
   using TT = typename TTileSel<Pol, D>::type;
 
-  const int l = lane_id(), n32 = l & 31, g = l >> 5, wv = threadIdx.x >> 6;
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int BH = P.B * P.H;
-  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
-  if (item >= (int64_t)BH * P.nqt) return;  // whole wave leaves; no workgroup barriers below
-  const int qt = P.nqt - 1 - (int)(item / BH);
-  const int bh = (int)(item % BH);
   const int b = bh / P.H, h = bh % P.H;
   const int Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
   const int i = qt * 32 + n32;  // this lane's query row
@@ -265,18 +287,212 @@ __global__ void __launch_bounds__(256) fwd_wave(FwdParams P) {
   }
 }
 
+// ------------------------------------------------------------------ fwd_cand_f32
+// The fp32 exact pass over the screen's candidate keys (normalised, more than one query tile):
+// one workgroup per query tile whose candidate lists (every branch) fit, one wave per branch.
+// The score tile of the query rows against the candidate keys (row c = candidate c; rows past
+// the count zero) takes the operands straight from the rows, in the element order of fwd_wave's
+// row fragments (lane half g: elements g d/2 + t, step t), so each score is bitwise the one
+// fwd_wave and the backward compute for that pair; the weights ReLU(x)^p with x = fma(s rk, rq,
+// -tau) and the causal mask accumulate coef A V over the candidates with a non-zero weight, one
+// fused multiply-add per output element and candidate in key order (the sums do not depend on the
+// list's other keys).  The bitmask row is rewritten from the key tiles holding a
+// non-zero weight.  A query tile whose list overflowed goes to the queue of fwd_wave<QUEUE>.  With
+// two branches the second wave's sum is added to the first's through LDS.
+template <int D, int BR, int PK>
+__global__ void __launch_bounds__(64 * BR) fwd_cand_f32(FwdParams P) {
+  constexpr int NT = D / 2, ND = D / 32;
+  __shared__ int ckeys[BR][32];     // candidate keys (-1: none)
+  __shared__ float crks[BR][32];    // their inverse norms
+  __shared__ float xch[BR == 2 ? 16 * ND * 64 : 1];
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = BR == 2 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;  // = its branch
+  const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
+  int bh, qt;
+  {
+    const int bid = blockIdx.x;  // one head's query tiles consecutive on one XCD
+    if (BH % 8 == 0) {
+      const int x = bid & 7, j = bid >> 3;
+      bh = x + 8 * (j / nqt);
+      qt = j % nqt;
+    } else {
+      bh = bid / nqt;
+      qt = bid % nqt;
+    }
+  }
+  if (bh >= BH) return;  // the same for both waves
+  const uint32_t* counts = P.cand + pair_lists(BR, BH, nqt) * kCandCap;
+  uint32_t nc[BR];
+#pragma unroll
+  for (int br = 0; br < BR; ++br) nc[br] = counts[((int64_t)br * BH + bh) * nqt + qt];
+  bool fit = true;
+#pragma unroll
+  for (int br = 0; br < BR; ++br) fit = fit && nc[br] <= (uint32_t)kCandCap;
+  if (!fit) {  // fwd_wave<QUEUE> walks the bitmask tiles (both waves leave: the test is the same)
+    if (l == 0 && wv == 0) P.pvq[1 + atomicAdd(P.pvq, 1u)] = (uint32_t)(bh * nqt + qt);
+    return;
+  }
+  const int br = wv;
+  const uint32_t n = nc[br];
+  const int64_t lidx = ((int64_t)br * BH + bh) * nqt + qt;
+  int kraw = (int)P.cand[lidx * kCandCap + (l & 31)];
+  if (P.screen_items > (Nq + 255) / 256) {
+    // the screen split some key ranges over several items, which append in any order: sort the
+    // list (its keys are distinct) by rank, so the sums run in key order
+    int rank = l & 31;
+    if ((uint32_t)(l & 31) < n) {
+      rank = 0;
+      for (int f = 0; f < 32; ++f) {
+        const int a = __builtin_amdgcn_readlane(kraw, f);
+        rank += ((uint32_t)f < n && a < kraw) ? 1 : 0;
+      }
+    }
+    kraw = __builtin_amdgcn_ds_permute(4 * rank, kraw);
+  }
+
+  const int b = bh / P.H, h = bh % P.H;
+  const int iq = 32 * qt + n32;
+  const bool valid = iq < Nq;
+  const int pq = qoff + iq;
+  const int klast = kt_last(qt, qoff, P.nkt);
+  const int nw = (klast >> 5) + 1;  // bitmask words of the row
+  const float tau = *P.beta * tau_coeff(pq, P.inv_d);
+  const float pw = P.p;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+  int* ckey = ckeys[br];
+  float* crk = crks[br];
+  uint32_t* orow = P.occ + lidx * P.occ_w;
+  unsigned computed = 0, checked = 0;
+
+  f32x16 O[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) O[c] = f32x16{};
+  if (n > 0) {
+    const int qslot = br ? F_Q2 : F_Q1, kslot = br ? F_K2 : F_K1;
+    const float* qhead = (const float*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
+    const float* khead = (const float*)P.in[kslot] + (int64_t)b * P.s[kslot][0] + (int64_t)h * P.s[kslot][1];
+    const float* vhead = (const float*)P.in[F_V] + (int64_t)b * P.s[F_V][0] + (int64_t)h * P.s[F_V][1];
+    const int64_t sq = P.s[qslot][2], sk = P.s[kslot][2], sv = P.s[F_V][2];
+    const float coef = br == 0 ? 1.f : -lam;
+    const int key_l = l < (int)n && kraw >= 0 && kraw < Nk ? kraw : -1;  // lanes 0..31: candidate l
+    const float rk_l = key_l >= 0 ? P.norms[norm_base(P, br ? N_K2 : N_K1, bh) + key_l] : 0.f;
+    const float rq = P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + min(iq, Nq - 1)];
+    if (l < 32) {
+      ckey[l] = key_l;
+      crk[l] = rk_l;
+    }
+    const int key_m = __shfl(key_l, n32);  // the candidate this lane supplies to the A operand
+    const float* krow = key_m >= 0 ? khead + (int64_t)key_m * sk + g * NT : nullptr;
+    const float* qrow = qhead + (int64_t)min(iq, Nq - 1) * sq + g * NT;
+    f32x16 S = {};
+#pragma unroll
+    for (int m = 0; m < NT / 4; ++m) {
+      const f32x4 a = krow ? *reinterpret_cast<const f32x4*>(krow + 4 * m) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 q = *reinterpret_cast<const f32x4*>(qrow + 4 * m);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S = PolF32::mma(a[e], q[e], S);
+    }
+    wave_lds_sync();
+    uint32_t cnz = 0u;  // candidates with a non-zero weight
+    f32x16 C;           // value r: the weight of candidate crow(r, g) for the lane's query
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = crow(r, g);
+      const int key = ckey[c];
+      const float x = __builtin_fmaf(S[r] * crk[c], rq, -tau);
+      const bool pos = key >= 0 && key <= pq && key < Nk && x > 0.f;
+      C[r] = pos ? coef * pow_p<PK>(x, pw) : 0.f;
+      const uint64_t bal = wave_ballot(valid && pos);
+      cnz |= ((uint32_t)bal ? 1u << crow(r, 0) : 0u) | ((uint32_t)(bal >> 32) ? 1u << crow(r, 1) : 0u);
+    }
+    // out_i += w_ic v_c over the candidates with a non-zero weight, one fused multiply-add per
+    // element in increasing key order: each row's sum takes exactly its own non-zero terms in key
+    // order (the other candidates add w = 0), so it does not depend on which other keys the
+    // tile's list holds (another tiling, keys past the last position).  Lane (n, g) holds the
+    // elements 32 c + 8 u + 4 g .. + 3 of row n.
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      if (!((cnz >> c) & 1u)) continue;
+      const int r = (c & 3) | ((c >> 3) << 2), gc = (c >> 2) & 1;  // crow(r, gc) = c
+      const float w = __shfl(C[r], n32 + 32 * gc);
+      const float* vrow = vhead + (int64_t)__builtin_amdgcn_readfirstlane(ckey[c]) * sv + 4 * g;
+#pragma unroll
+      for (int cb = 0; cb < ND; ++cb)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const f32x4 vv4 = *reinterpret_cast<const f32x4*>(vrow + 32 * cb + 8 * u);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) O[cb][4 * u + e] = __builtin_fmaf(w, vv4[e], O[cb][4 * u + e]);
+        }
+    }
+    // the bitmask row: lane w rewrites word w from the key tiles of the candidates with a
+    // non-zero weight (the screen's words cover the key tiles of all candidates, nothing else)
+    for (int w0 = 0; w0 < nw; w0 += 64) {
+      uint32_t word = 0u;
+      for (uint32_t m = cnz; m; m &= m - 1u) {
+        const int kt = __builtin_amdgcn_readfirstlane(ckey[__builtin_ctz(m)]) >> 5;
+        word |= (kt >> 5) == w0 + l ? 1u << (kt & 31) : 0u;
+      }
+      if (w0 + l < nw) {
+        if (P.stats) checked += (unsigned)__builtin_popcount(orow[w0 + l]);
+        orow[w0 + l] = word;
+      }
+      computed += (unsigned)__builtin_popcount(word);
+    }
+  }
+  if (P.stats) {
+    const float cs = wave_sum((float)computed), ks = wave_sum((float)checked);
+    if (l == 0 && ks > 0.f) {
+      atomicAdd(P.stats + 1, (unsigned long long)cs);
+      atomicAdd(P.stats + 2, (unsigned long long)ks);
+    }
+  }
+  if constexpr (BR == 2) {
+    // out = O (branch 0's wave) + O (branch 1's wave, -lambda A2 V), added through LDS
+    __syncthreads();
+    if (wv == 1) {
+#pragma unroll
+      for (int c = 0; c < ND; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xch[(16 * c + r) * 64 + l] = O[c][r];
+    }
+    __syncthreads();
+    if (wv == 1) return;
+#pragma unroll
+    for (int c = 0; c < ND; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) O[c][r] += xch[(16 * c + r) * 64 + l];
+  }
+  if (valid) {
+    float* orow_out = (float*)P.out + (int64_t)b * P.s[F_OUT][0] + (int64_t)h * P.s[F_OUT][1] + (int64_t)iq * P.s[F_OUT][2];
+#pragma unroll
+    for (int c = 0; c < ND; ++c)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        store4(orow_out + 32 * c + 8 * u + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2], O[c][4 * u + 3]);
+  }
+}
+
 // ------------------------------------------------------------------ dispatch
 // Normalised fp32 calls with more than one query tile and the int8 keys' workspace run the int8
 // screen first (key_prep and fwd_screen_i8 on the fp32 rows, tda_fwd_sparse.hip), then the
 // screened fwd_wave.
 template <class Pol, int D, int BR, int PK, bool NORM>
 static int launch_fwd_t(const FwdParams& p, const KernelKey& k, void* stream) {
+  static_assert(std::is_same<Pol, PolF32>::value, "the fp32 dispatch (bf16 runs tda_fwd_sparse.hip)");
   const int64_t items = (int64_t)p.B * p.H * p.nqt;
   const unsigned grid = (unsigned)((items + 3) / 4);
-  if (NORM && p.k8 && p.nqt > 1) {
+  if (NORM && p.k8 && p.nqt > 1 && p.cand) {
+    // the int8 screen with candidate lists, the candidate pass, then the tile pass over the query
+    // tiles whose lists overflowed
     const int e = launch_fwd_screen_f32(p, k, stream);
     if (e) return e;
-    hipLaunchKernelGGL((fwd_wave<Pol, D, BR, PK, NORM, NORM>), dim3(grid), dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((fwd_cand_f32<D, BR, PK>), dim3((unsigned)items), dim3(64 * BR), 0, (hipStream_t)stream, p);
+    launched(stream, "fwd_cand_f32");
+    const unsigned qgrid = (unsigned)(((items < 2048 ? items : 2048) + 3) / 4);
+    hipLaunchKernelGGL((fwd_wave<Pol, D, BR, PK, NORM, NORM, NORM>), dim3(qgrid), dim3(256), 0, (hipStream_t)stream, p);
   } else {
     hipLaunchKernelGGL((fwd_wave<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, (hipStream_t)stream, p);
   }

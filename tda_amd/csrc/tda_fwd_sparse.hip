@@ -186,6 +186,10 @@ __device__ __forceinline__ void screen_flush(const FwdParams& P, int BR, const S
       // a padding key (past Nk, in the last key tile) scores 0 and passes a threshold below 0
       // (the query tile at position 0, beta <= 0): it holds no weight and must not be listed
       if ((kt >> 5) == (kpad >> 5) && n32 >= Nk - 32 * kpad) w &= ~(1u << (kpad & 31));
+      // nor is a key after the query tile's last position (its diagonal key tile): no row of the
+      // tile sees it, so the lists hold the same keys whatever follows the tile's rows
+      const int lastk = P.qoff + min(32 * (qt0 + s) + 31, P.Nq - 1), kdiag = lastk >> 5;
+      if ((kt >> 5) == (kdiag >> 5) && 32 * kdiag + n32 > lastk) w &= ~(1u << (kdiag & 31));
     }
     const uint32_t hm = w | (uint32_t)__shfl_xor((int)w, 32);  // lane n32: tiles its key passed
 #pragma unroll
@@ -295,9 +299,10 @@ __device__ __forceinline__ int pack4_rint(float a, float b, float c, float d) {
 }
 
 __device__ __forceinline__ int max16i(const i32x16& v) {
+  // five three-input maxima, two more, one max: 8 instructions
   const int a = max(max(v[0], v[1]), v[2]), b = max(max(v[3], v[4]), v[5]), c = max(max(v[6], v[7]), v[8]);
   const int d = max(max(v[9], v[10]), v[11]), e = max(max(v[12], v[13]), v[14]);
-  return max(max(max(a, b), max(c, d)), max(e, v[15]));
+  return max(max(max(a, b), c), max(max(d, e), v[15]));
 }
 
 // ------------------------------------------------------------------ key_prep
@@ -582,14 +587,8 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
 // tile is S = A B^T: each lane holds one key j and 16 query rows, and the test (the int8 bound
 // above) is "float(max_i A_ij) * (sq s_j) > thr_j", a few operations per lane and query tile.
 // Hit bits give the bitmask words and the candidate keys (screen_flush).
-#ifndef TDA_I8_STAGES
-#define TDA_I8_STAGES 4
-#endif
-#ifndef TDA_I8_TPI
-#define TDA_I8_TPI 2
-#endif
-constexpr int I8_STAGES = TDA_I8_STAGES;
-constexpr int I8_TPI = TDA_I8_TPI;       // key tiles per stage (a divisor of 32)
+constexpr int I8_STAGES = 4;
+constexpr int I8_TPI = 2;                // key tiles per stage (a divisor of 32)
 constexpr int I8_AHEAD = I8_STAGES - 1;  // stages in flight past the one being tested
 static_assert(32 % I8_TPI == 0 && I8_TPI <= 4, "stages of whole parts of a bitmask word");
 // Chunk swizzle of an int8 key tile row (16-byte chunks): conflict-free fragment reads, where
@@ -797,21 +796,25 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
   uint32_t hb[QPW], cn[QPW];  // hit bits; candidate keys met per query tile (may pass the cap)
 #pragma unroll
   for (int s = 0; s < QPW; ++s) hb[s] = cn[s] = 0u;
-  uint32_t koff[NK];  // this lane's fragment chunks in a tile: row n32, chunk 2 t + g
+  // LDS addresses of this lane's fragment chunks in ring slot 0, tile 0 (row n32, chunk 2 t + g)
+  // and of its key's {s_j, ek_j}; the slot and tile go into the instructions' offset fields
+  uint32_t kaddr[NK];
 #pragma unroll
-  for (int t = 0; t < NK; ++t) koff[t] = (uint32_t)(n32 * D + 16 * ((2 * t + g) ^ i8swz<D>(n32)));
+  for (int t = 0; t < NK; ++t) kaddr[t] = lds_addr(&kst[0][0]) + (uint32_t)(n32 * D + 16 * ((2 * t + g) ^ i8swz<D>(n32)));
+  const uint32_t saddr = lds_addr(&ksc[0][0]) + 8u * (uint32_t)n32;
 
   // One tile: the fragment reads are inline asm (the compiler orders every LDS read after all
   // outstanding direct-to-LDS loads, vmcnt(0), which would drain the ring each tile, while
   // wait_stage and the barrier already order this stage's loads before them); the wait that ends
   // them takes the fragments as operands, so no use of them is scheduled before it.
-  auto process = [&](int kt, uint32_t tbase, uint32_t sbase) {
+  auto process = [&](int kt, auto TOFF, auto SOFF) {
+    constexpr uint32_t toff = decltype(TOFF)::value, soff_ = decltype(SOFF)::value;
     i32x4 fk[NK];
 #pragma unroll
     for (int t = 0; t < NK; ++t)
-      asm volatile("ds_read_b128 %0, %1" : "=v"(fk[t]) : "v"(tbase + koff[t]) : "memory");
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(fk[t]) : "v"(kaddr[t]), "i"(toff) : "memory");
     float2 kq;  // the lane's key: {s_j, ek_j} (0 past Nk)
-    asm volatile("ds_read_b64 %0, %1" : "=v"(kq) : "v"(sbase + 8u * (uint32_t)n32) : "memory");
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(kq) : "v"(saddr), "i"(soff_) : "memory");
     if constexpr (NK == 4)
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fk[0]), "+v"(fk[1]), "+v"(fk[2]), "+v"(fk[3]), "+v"(kq) : : "memory");
     else
@@ -838,19 +841,29 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
   // the last stage with a tile some query tile of the wave sees (later tiles of a stage are
   // masked in the test)
   const int jl = live[0] ? (ktl[QPW - 1] - k0) / TPI : -1;
-  for (int j = 0; j < nst; ++j) {
+  // stage j sits in ring slot j % I8_STAGES: the loop is unrolled over the slots so that every
+  // slot's LDS offsets are constants
+  static_assert(I8_STAGES == 4 && TPI == 2, "unrolled for a 4-slot ring of 2-tile stages");
+  auto stage = [&](int j, auto SLOT) {
+    constexpr int st = decltype(SLOT)::value;
     wait_stage(j);
     __syncthreads();  // stage j is in LDS; every wave is past stage j - 1, whose slot is reloaded
     if (j + I8_AHEAD < nst) issue(j + I8_AHEAD);
     if (P.zero) zs.clear<NTHR>(P, TPI * j, tid, min(TPI, nit - TPI * j));
     if (j <= jl) {
-      const int st = j % I8_STAGES;
-      const uint32_t kb = lds_addr(&kst[st][0]), sb = lds_addr(&ksc[st][0]);
-#pragma unroll
-      for (int u = 0; u < TPI; ++u) process(k0 + TPI * j + u, kb + (uint32_t)(u * TB), sb + (uint32_t)(u * 256));
+      process(k0 + TPI * j, std::integral_constant<uint32_t, st * TPI * TB>{},
+              std::integral_constant<uint32_t, st * TPI * 256>{});
+      process(k0 + TPI * j + 1, std::integral_constant<uint32_t, st * TPI * TB + TB>{},
+              std::integral_constant<uint32_t, st * TPI * 256 + 256>{});
     }
     // the stage's last tile of the item (stages never straddle a bitmask word)
     screen_flush<QPW, true>(P, BR, it, qt0, live, hb, cn, min(k0 + TPI * j + TPI - 1, k1 - 1));
+  };
+  for (int j = 0; j < nst; j += I8_STAGES) {
+    stage(j, std::integral_constant<int, 0>{});
+    if (j + 1 < nst) stage(j + 1, std::integral_constant<int, 1>{});
+    if (j + 2 < nst) stage(j + 2, std::integral_constant<int, 2>{});
+    if (j + 3 < nst) stage(j + 3, std::integral_constant<int, 3>{});
   }
   screen_counts<QPW>(P, BR, it, qt0, live, cn);
   screen_count<QPW>(P, it, live, ktl);
@@ -1442,8 +1455,7 @@ int launch_fwd_sparse(const FwdParams& p, const KernelKey& k, void* stream) {
 // walks the bitmask.
 int launch_fwd_screen_f32(const FwdParams& p0, const KernelKey& k, void* stream) {
   hipStream_t s = (hipStream_t)stream;
-  FwdParams p = p0;
-  p.cand = nullptr;
+  FwdParams p = p0;  // with candidate lists: the fp32 candidate pass reads them
   const int BR = k.branches, BH = p.B * p.H;
   const dim3 grid((unsigned)(BR * BH) * (unsigned)p.screen_items);
   auto run = [&](auto dc) {

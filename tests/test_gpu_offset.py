@@ -47,6 +47,11 @@ def test_rows_of_full_pass_equal_offset_block(dt, o, m):
         # few ulps apart, which weights just above tau amplify (x^p of a small x); both within the
         # fp32 parity tolerance
         assert rel_err(blk, full[:, :, o:o + m]) <= 1e-4
+    elif dt == "f32" and o % 32:
+        # fp32: a query tile whose candidate list overflows takes the tile pass, whose sums run
+        # in another order than the candidate pass's; a block not aligned to the full call's
+        # query tiles has other tiles, so other overflows (aligned blocks: bitwise, above)
+        assert rel_err(blk, full[:, :, o:o + m]) <= 1e-4
     else:
         assert torch.equal(blk, full[:, :, o:o + m])
     # keys after the block's last position are never read
