@@ -293,16 +293,21 @@ def fp32_figures(dev, stream):
     beta, lam = torch.tensor(BETA, device=dev), torch.tensor(LAM, device=dev)
     fwd = lambda: ops.forward(q1, k1, q2, k2, v, beta, lam, POWER, True, 2)  # noqa: E731
     with torch.no_grad():
-        ms_f = time_calls(stream, fwd, 3, 1)
+        ms_f = time_calls(stream, fwd, 10, 2)
+    # the backward as a training step runs it: on the side outputs and pair lists of its forward
     norms, occ = ops.side_buffers(SHAPE, 2, True, dev)
+    pairs = ops.pair_buffer(SHAPE, 2, dev)
     with torch.no_grad():
-        ops.forward(q1, k1, q2, k2, v, beta, lam, POWER, True, 2, norms, occ)
-        ms_b = time_calls(stream, lambda: ops.backward(q1, k1, q2, k2, v, do, beta, lam, POWER, True, 2, norms, occ),
-                          2, 1)
+        ops.forward(q1, k1, q2, k2, v, beta, lam, POWER, True, 2, norms, occ, pairs=pairs)
+        bwd = lambda: ops.backward(q1, k1, q2, k2, v, do, beta, lam, POWER, True, 2, norms, occ,  # noqa: E731
+                                   pairs=pairs)
+        ms_b = time_calls(stream, bwd, 10, 2)
+        bwd_launch_us, _ = time_launches(bwd, 5, 1)
     out["c2_tda"] = {"workload": "TDA fp32 (4,16,4096,128) seed 2, beta=1, lambda=0.5, p=2, normalize",
                      "fwd_ms": ms_f, "fwd_tflops": units(SHAPE, 3.0) / (ms_f * 1e-3) / 1e12,
                      "fwd_pct_f32_peak": 100.0 * units(SHAPE, 3.0) / (ms_f * 1e-3) / 1e12 / PEAK_F32_TFLOPS,
-                     "bwd_ms": ms_b, "fwd_bwd_ms": ms_f + ms_b,
+                     "bwd_ms": ms_b, "bwd_launch_us": {k: round(t, 2) for k, t in bwd_launch_us.items()},
+                     "fwd_bwd_ms": ms_f + ms_b,
                      "fwd_bwd_tflops": units(SHAPE, 11.0) / ((ms_f + ms_b) * 1e-3) / 1e12,
                      "fwd_bwd_pct_f32_peak": (100.0 * units(SHAPE, 11.0) / ((ms_f + ms_b) * 1e-3) / 1e12
                                               / PEAK_F32_TFLOPS)}

@@ -121,20 +121,42 @@ __device__ __forceinline__ void finish_rows(const f32x16 (&acc)[D / 32], const t
 // formed as in the forward (S^T = K Q^T: lane = query, values = keys); the gradient tile
 // dS * rk packs into the B operand of dq^T += K^T (dS rk)^T, with K^T staged as a
 // transposed tile.
-template <class Pol, int D, int BR, int PK, bool NORM>
+//
+// LISTS (fp32 with the forward's pair lists): one wave per (branch, query tile) list that did
+// not fit (the pair pass bwd_dq_pairs took the others): only that branch's scores, dq rows and
+// dbeta / dlambda partials (the list's workspace slot, as the pair pass's).
+template <class Pol, int D, int BR, int PK, bool NORM, bool LISTS>
+__device__ __forceinline__ void bwd_dq_item(const BwdParams& P, int qt, int bh, int lbr, int64_t slot, int wv);
+
+template <class Pol, int D, int BR, int PK, bool NORM, bool LISTS = false>
 __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
+  const int wv = threadIdx.x >> 6;
+  const int BH = P.B * P.H;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+  if constexpr (LISTS) {
+    if (item >= (int64_t)BR * BH * P.nqt) return;
+    const int br = BR == 2 ? (int)(item & 1) : 0;  // the item order of bwd_dq_pairs
+    const int64_t rest = BR == 2 ? item >> 1 : item;
+    const int qt = (int)(rest / BH), bh = (int)(rest % BH);
+    const int64_t lidx = ((int64_t)br * BH + bh) * P.nqt + qt;
+    if (P.pairs[pair_lists(BR, BH, P.nqt) * 4 * kPairCap + lidx] <= (uint32_t)kPairCap) return;
+    bwd_dq_item<Pol, D, BR, PK, NORM, true>(P, qt, bh, br, lidx, wv);
+  } else {
+    if (item >= (int64_t)BH * P.nqt) return;
+    bwd_dq_item<Pol, D, BR, PK, NORM, false>(P, P.nqt - 1 - (int)(item / BH), (int)(item % BH), 0, item, wv);
+  }
+}
+
+template <class Pol, int D, int BR, int PK, bool NORM, bool LISTS>
+__device__ __forceinline__ void bwd_dq_item(const BwdParams& P, int qt, int bh, int lbr, int64_t slot, int wv) {
   using T = typename Pol::T;
   using frag = typename Pol::frag;
   constexpr int NT = D / Pol::KS, NS = 32 / Pol::KS, ND = D / 32;
   using TT = typename TTileSelB<Pol, D>::type;
 
-  const int l = lane_id(), n32 = l & 31, g = l >> 5, wv = threadIdx.x >> 6;
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int BH = P.B * P.H;
-  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
-  if (item >= (int64_t)BH * P.nqt) return;
-  const int qt = P.nqt - 1 - (int)(item / BH);
   const int ktl = kt_last(qt, P.qoff, P.nkt);  // last key tile the query tile sees
-  const int bh = (int)(item % BH);
   const int b = bh / P.H, h = bh % P.H;
   const int Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
   const int i = qt * 32 + n32;
@@ -189,8 +211,9 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
     while (kt <= ktl) {
       if ((kt >> 5) != cw) {
         cw = kt >> 5;
-        w1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)occrow[cw]);
-        if constexpr (BR == 2) w2 = (uint32_t)__builtin_amdgcn_readfirstlane((int)occrow[occ_br + cw]);
+        w1 = (!LISTS || lbr == 0) ? (uint32_t)__builtin_amdgcn_readfirstlane((int)occrow[cw]) : 0u;
+        if constexpr (BR == 2)
+          w2 = (!LISTS || lbr == 1) ? (uint32_t)__builtin_amdgcn_readfirstlane((int)occrow[occ_br + cw]) : 0u;
       }
       const uint32_t m = (w1 | w2) >> (kt & 31);
       if (m) return kt + __builtin_ctz(m);
@@ -273,8 +296,9 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
     }
   }
 
-  finish_rows<Pol, D, NORM>(A1, qvalid ? q1.row(b, h, i) : nullptr, qvalid ? dq1.row(b, h, i) : nullptr, rq1);
-  if constexpr (BR == 2)
+  if (!LISTS || lbr == 0)
+    finish_rows<Pol, D, NORM>(A1, qvalid ? q1.row(b, h, i) : nullptr, qvalid ? dq1.row(b, h, i) : nullptr, rq1);
+  if (BR == 2 && (!LISTS || lbr == 1))
     finish_rows<Pol, D, NORM>(A2, qvalid ? q2.row(b, h, i) : nullptr, qvalid ? dq2.row(b, h, i) : nullptr, rq2);
 
   // per-wave dbeta / dlambda partials (lanes with g == 1 hold the same query as g == 0 but
@@ -282,8 +306,8 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
   const float pb = wave_sum(-ci * bsum);
   const float pl = wave_sum(-lsum);
   if (l == 0) {
-    P.ws[2 * item + 0] = pb;
-    P.ws[2 * item + 1] = pl;
+    P.ws[2 * slot + 0] = pb;
+    P.ws[2 * slot + 1] = pl;
     if (P.stats) {
       atomicAdd(P.stats + 0, (unsigned long long)visited);
       atomicAdd(P.stats + 1, (unsigned long long)computed);
@@ -296,17 +320,36 @@ __global__ void __launch_bounds__(256) bwd_dq(BwdParams P) {
 // most query tiles).  Scores are formed as S = Q K^T (lane = key, values = queries) so that the
 // probability and gradient tiles pack into the B operand of dv^T += dO^T A and
 // dk^T += Q^T (dS rq), with dO^T and Q^T staged as transposed tiles.
+//
+// QUEUE (fp32 with the forward's pair lists): only the key tiles the key-major pair pass
+// (bwd_dkv_pairs) queued, whose columns hold a list that did not fit; the waves take them in turn.
 template <class Pol, int D, int BR, int PK, bool NORM>
+__device__ __forceinline__ void bwd_dkv_item(const BwdParams& P, int64_t item, int wv);
+
+template <class Pol, int D, int BR, int PK, bool NORM, bool QUEUE = false>
 __global__ void __launch_bounds__(256) bwd_dkv(BwdParams P) {
+  const int wv = threadIdx.x >> 6;
+  const int BH = P.B * P.H;
+  if constexpr (QUEUE) {
+    const uint32_t queued = P.dkvq[0];
+    for (uint32_t k = blockIdx.x * 4u + (uint32_t)wv; k < queued; k += gridDim.x * 4u)
+      bwd_dkv_item<Pol, D, BR, PK, NORM>(P, (int64_t)P.dkvq[1 + k], wv);
+    return;
+  }
+  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
+  if (item >= (int64_t)BH * P.nkt) return;
+  bwd_dkv_item<Pol, D, BR, PK, NORM>(P, item, wv);
+}
+
+template <class Pol, int D, int BR, int PK, bool NORM>
+__device__ __forceinline__ void bwd_dkv_item(const BwdParams& P, int64_t item, int wv) {
   using T = typename Pol::T;
   using frag = typename Pol::frag;
   constexpr int NT = D / Pol::KS, NS = 32 / Pol::KS, ND = D / 32;
   using TT = typename TTileSelB<Pol, D>::type;
 
-  const int l = lane_id(), n32 = l & 31, g = l >> 5, wv = threadIdx.x >> 6;
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int BH = P.B * P.H;
-  const int64_t item = (int64_t)blockIdx.x * 4 + wv;
-  if (item >= (int64_t)BH * P.nkt) return;
   const int kt = (int)(item / BH);
   const int bh = (int)(item % BH);
   const int b = bh / P.H, h = bh % P.H;
@@ -491,6 +534,21 @@ template <class Pol, int D, int BR, int PK, bool NORM>
 static int launch_bwd_t(const BwdParams& p, void* stream) {
   const int64_t qitems = (int64_t)p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
+  if (p.pairs && p.dkvq) {
+    // the forward's pair lists (the fp32 candidate pass): the pair passes (tda_bwd_fast.hip),
+    // then the tile passes over the lists and key tiles they left, then the sum over the lists'
+    // partial slots
+    int e = launch_bwd_pairs_f32(p, KernelKey{0, D, BR, PK, NORM ? 1 : 0}, stream);
+    if (e) return e;
+    const int64_t lists = (int64_t)BR * qitems;
+    hipLaunchKernelGGL((bwd_dq<Pol, D, BR, PK, NORM, true>), dim3((unsigned)((lists + 3) / 4)), dim3(256), 0, s, p);
+    launched(s, "bwd_dq");
+    const unsigned qgrid = (unsigned)(((kitems < 2048 ? kitems : 2048) + 3) / 4);
+    hipLaunchKernelGGL((bwd_dkv<Pol, D, BR, PK, NORM, true>), dim3(qgrid), dim3(256), 0, s, p);
+    launched(s, "bwd_dkv");
+    e = (int)hipGetLastError();
+    return e ? e : launch_bwd_finish(p, BR, lists, stream);
+  }
   hipLaunchKernelGGL((bwd_dq<Pol, D, BR, PK, NORM>), dim3((unsigned)((qitems + 3) / 4)), dim3(256), 0, s, p);
   launched(s, "bwd_dq");
   hipLaunchKernelGGL((bwd_dkv<Pol, D, BR, PK, NORM>), dim3((unsigned)((kitems + 3) / 4)), dim3(256), 0, s, p);

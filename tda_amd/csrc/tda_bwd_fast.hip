@@ -372,23 +372,57 @@ __device__ __forceinline__ RowVec<D> load_rowvec(const bf16* row) {
   }
   return r;
 }
-// The lane's D/64 elements of a row as loaded (bf16 bits, element 2l in the low half for
-// D = 128): one register per row while loads are in flight.
 template <int D>
-struct RowRaw {
+__device__ __forceinline__ RowVec<D> load_rowvec(const float* row) {
+  RowVec<D> r;
+  const int l = lane_id();
+  if constexpr (D == 128) {
+    const float2 x = *reinterpret_cast<const float2*>(row + 2 * l);
+    r.v[0] = x.x;
+    r.v[1] = x.y;
+  } else {
+    r.v[0] = row[l];
+  }
+  return r;
+}
+// The lane's D/64 elements of a row as loaded (bf16: the bits, element 2l in the low half for
+// D = 128, one register per row while loads are in flight; fp32: the values).
+template <int D, class T>
+struct RowRaw;
+template <int D>
+struct RowRaw<D, bf16> {
   uint32_t u;
 };
 template <int D>
-__device__ __forceinline__ RowRaw<D> load_rowraw(const bf16* row) {
+struct RowRaw<D, float> {
+  float v[D / 64];
+};
+template <int D>
+__device__ __forceinline__ RowRaw<D, bf16> load_rowraw(const bf16* row) {
   const int l = lane_id();
-  if constexpr (D == 128) return RowRaw<D>{*reinterpret_cast<const uint32_t*>(row + 2 * l)};
-  else return RowRaw<D>{(uint32_t)*reinterpret_cast<const uint16_t*>(row + l)};
+  if constexpr (D == 128) return RowRaw<D, bf16>{*reinterpret_cast<const uint32_t*>(row + 2 * l)};
+  else return RowRaw<D, bf16>{(uint32_t)*reinterpret_cast<const uint16_t*>(row + l)};
 }
 template <int D>
-__device__ __forceinline__ RowVec<D> unpack(RowRaw<D> r) {
+__device__ __forceinline__ RowRaw<D, float> load_rowraw(const float* row) {
+  RowRaw<D, float> r;
+  const RowVec<D> v = load_rowvec<D>(row);
+#pragma unroll
+  for (int e = 0; e < D / 64; ++e) r.v[e] = v.v[e];
+  return r;
+}
+template <int D>
+__device__ __forceinline__ RowVec<D> unpack(RowRaw<D, bf16> r) {
   RowVec<D> v;
   v.v[0] = __uint_as_float(r.u << 16);
   if constexpr (D == 128) v.v[1] = __uint_as_float(r.u & 0xffff0000u);
+  return v;
+}
+template <int D>
+__device__ __forceinline__ RowVec<D> unpack(RowRaw<D, float> r) {
+  RowVec<D> v;
+#pragma unroll
+  for (int e = 0; e < D / 64; ++e) v.v[e] = r.v[e];
   return v;
 }
 template <int D>
@@ -398,6 +432,14 @@ __device__ __forceinline__ void store_rowvec(bf16* row, const RowVec<D>& r) {
     __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, bf16x2{(bf16)r.v[0], (bf16)r.v[1]}),
                                 reinterpret_cast<uint32_t*>(row + 2 * l));
   else row[l] = (bf16)r.v[0];
+}
+template <int D>
+__device__ __forceinline__ void store_rowvec(float* row, const RowVec<D>& r) {
+  const int l = lane_id();
+  if constexpr (D == 128)
+    __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, float2{r.v[0], r.v[1]}),
+                                reinterpret_cast<uint64_t*>(row + 2 * l));
+  else __builtin_nontemporal_store(r.v[0], row + l);
 }
 template <int D>
 __device__ __forceinline__ float row_dot(const RowVec<D>& a, const RowVec<D>& b) {
@@ -420,15 +462,16 @@ __device__ __forceinline__ RowVec<D> normalize_back(const RowVec<D>& g, const Ro
   return o;
 }
 // Zero rows 0..nrows-1 of a 32-row tile except those in `keep` (16 bytes per lane and store).
-template <int D>
-__device__ __forceinline__ void zero_rows(bf16* tile0, int64_t st, int nrows, uint32_t keep) {
-  constexpr int CH = D / 8, RPI = 64 / CH;
+template <int D, class T>
+__device__ __forceinline__ void zero_rows(T* tile0, int64_t st, int nrows, uint32_t keep) {
+  constexpr int EPC = 16 / sizeof(T), CH = D / EPC, RPI = 64 / CH;  // elements per chunk, chunks per row
   const int l = lane_id();
 #pragma unroll
   for (int u = 0; u < 32 / RPI; ++u) {
     const int r = u * RPI + l / CH;
     if (r < nrows && !((keep >> r) & 1u))  // streaming stores: nothing reads them soon
-      __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u}, reinterpret_cast<u32x4*>(tile0 + (int64_t)r * st + 8 * (l % CH)));
+      __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u},
+                                  reinterpret_cast<u32x4*>(tile0 + (int64_t)r * st + EPC * (l % CH)));
   }
 }
 
@@ -463,7 +506,7 @@ __device__ __forceinline__ SortedPairs sort_pairs(const PairLanes& PL, uint32_t 
   return S;
 }
 
-template <int D, int BR, int PK, bool NORM>
+template <int D, int BR, int PK, bool NORM, class T = bf16>
 __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   const int l = lane_id();
   const int BH = P.B * P.H;
@@ -484,15 +527,15 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   if (npairs > (uint32_t)kPairCap) return;  // bwd_dq_fast walks the tiles
 
   auto base = [&](int slot) {
-    return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
+    return (const T*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
   };
   const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2, gslot = br == 0 ? B_DQ1 : B_DQ2;
   const int64_t sq = P.s[qslot][2], sk = P.s[kslot][2], sv = P.s[B_V][2], sdo = P.s[B_DO][2], sg = P.s[gslot][2];
-  const bf16* qb = base(qslot);
-  const bf16* kb = base(kslot);
-  const bf16* vb = base(B_V);
-  const bf16* dob = base(B_DO);
-  bf16* gb = (bf16*)P.grad[br == 0 ? 0 : 2] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1];
+  const T* qb = base(qslot);
+  const T* kb = base(kslot);
+  const T* vb = base(B_V);
+  const T* dob = base(B_DO);
+  T* gb = (T*)P.grad[br == 0 ? 0 : 2] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1];
   const float* nq = NORM ? P.norms + norm_base(P, br == 0 ? N_Q1 : N_Q2, bh) : nullptr;
   const float* nk = NORM ? P.norms + norm_base(P, br == 0 ? N_K1 : N_K2, bh) : nullptr;
   const float pw = P.p;
@@ -529,7 +572,7 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
   for (uint32_t s0 = 0; s0 < npairs; s0 += kRowBatch) {
     int il[kRowBatch], jj[kRowBatch];
     float rq[kRowBatch], rk[kRowBatch];
-    RowRaw<D> dor[kRowBatch], qr[kRowBatch], kr[kRowBatch], vr[kRowBatch];
+    RowRaw<D, T> dor[kRowBatch], qr[kRowBatch], kr[kRowBatch], vr[kRowBatch];
 #pragma unroll
     for (int u = 0; u < kRowBatch; ++u) {
       const int s = (int)s0 + u;
@@ -540,7 +583,7 @@ __global__ void __launch_bounds__(64) bwd_dq_pairs(BwdParams P) {
       dor[u] = load_rowraw<D>(dob + (int64_t)i * sdo);
       kr[u] = load_rowraw<D>(kb + (int64_t)jj[u] * sk);
       vr[u] = load_rowraw<D>(vb + (int64_t)jj[u] * sv);
-      qr[u] = RowRaw<D>{0u};
+      qr[u] = RowRaw<D, T>{};
       rq[u] = rk[u] = 1.f;
       if constexpr (NORM) {
         qr[u] = load_rowraw<D>(qb + (int64_t)i * sq);
@@ -644,7 +687,7 @@ struct ColEntry {
 // or, from a bucket, in the order (branch, query row).
 // Up to kColPairs pairs are gathered into LDS slots in one walk; a column with more walks its
 // lists once per named row.  No matrix cores and no V: per pair two row loads.
-template <int D, int BR, int PK, bool NORM>
+template <int D, int BR, int PK, bool NORM, class T = bf16>
 __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
   __shared__ int ps_i[kColPairs];    // query row, branch in bit 31
   __shared__ int ps_jl[kColPairs];   // key row within the tile
@@ -660,10 +703,10 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
   const int qtf = qt_first(kt, P.qoff);
 
   auto base = [&](int slot) {
-    return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
+    return (const T*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
   };
   auto gbase = [&](int slot, int gi) {
-    return (bf16*)P.grad[gi] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
+    return (T*)P.grad[gi] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
   };
   const uint32_t* counts = P.pairs + pair_lists(BR, BH, P.nqt) * 4 * kPairCap;
   const float pw = P.p;
@@ -818,7 +861,7 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
   // ---- rows: zeros for the rows no pair names, then each named key row
   const int nrows = min(32, P.Nk - 32 * kt);
   const uint32_t uall = BR == 2 ? used[0] | used[BR - 1] : used[0];
-  bf16* dvb = gbase(B_DV, 4);
+  T* dvb = gbase(B_DV, 4);
   const int64_t sdv = P.s[B_DV][2];
   if (!P.grads_zeroed) {
     zero_rows<D>(dvb + (int64_t)(32 * kt) * sdv, sdv, nrows, uall);
@@ -828,7 +871,7 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
       zero_rows<D>(gbase(gslot, br == 0 ? 1 : 3) + (int64_t)(32 * kt) * P.s[gslot][2], P.s[gslot][2], nrows, used[br]);
     }
   }
-  const bf16* dob = base(B_DO);
+  const T* dob = base(B_DO);
   const int64_t sdo = P.s[B_DO][2];
   // key row jl's finished rows: dv, and dk of each branch whose pairs name it (the others were
   // stored as zeros above)
@@ -845,11 +888,11 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
     }
   };
   // the same, packed (rows zero, norms 1 where not needed)
-  auto load_key_raw = [&](int jl, RowRaw<D>(&kx)[BR], float(&rk)[BR]) {
+  auto load_key_raw = [&](int jl, RowRaw<D, T>(&kx)[BR], float(&rk)[BR]) {
     const int j = 32 * kt + jl;
 #pragma unroll
     for (int br = 0; br < BR; ++br) {
-      kx[br] = RowRaw<D>{0u};
+      kx[br] = RowRaw<D, T>{};
       rk[br] = 1.f;
       if constexpr (NORM)
         if ((used[br] >> jl) & 1u) {
@@ -910,7 +953,7 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
     }
     for (uint32_t s0 = 0; s0 < np; s0 += kColBatch) {
       int jl[kColBatch], ibr[kColBatch];
-      RowRaw<D> dor[kColBatch], qr[kColBatch], kxu[kColBatch][BR];
+      RowRaw<D, T> dor[kColBatch], qr[kColBatch], kxu[kColBatch][BR];
       float rku[kColBatch][BR];
 #pragma unroll
       for (int u = 0; u < kColBatch; ++u) {
@@ -1299,6 +1342,38 @@ static int sel_br(const BwdParams& p, const KernelKey& k, void* s) {
 
 int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream) {
   return k.d == 128 ? sel_br<128>(p, k, stream) : sel_br<64>(p, k, stream);
+}
+
+// The pair passes on fp32 rows (the fp32 backward's launcher in tda_bwd.hip runs the tile passes
+// for what they leave).
+template <int D, int BR, int PK, bool NORM>
+static int pairs_f32_t(const BwdParams& p, hipStream_t s) {
+  const int64_t qitems = (int64_t)BR * p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
+  hipLaunchKernelGGL((bwd_dq_pairs<D, BR, PK, NORM, float>), dim3((unsigned)qitems), dim3(64), 0, s, p);
+  launched(s, "bwd_dq_pairs");
+  hipLaunchKernelGGL((bwd_dkv_pairs<D, BR, PK, NORM, float>), dim3((unsigned)kitems), dim3(64), 0, s, p);
+  launched(s, "bwd_dkv_pairs");
+  return (int)hipGetLastError();
+}
+template <int D, int BR, int PK>
+static int pairs_f32_norm(const BwdParams& p, const KernelKey& k, hipStream_t s) {
+  return k.normalize ? pairs_f32_t<D, BR, PK, true>(p, s) : pairs_f32_t<D, BR, PK, false>(p, s);
+}
+template <int D, int BR>
+static int pairs_f32_pk(const BwdParams& p, const KernelKey& k, hipStream_t s) {
+  switch (k.pkind) {
+    case 2: return pairs_f32_norm<D, BR, 2>(p, k, s);
+    case 1: return pairs_f32_norm<D, BR, 1>(p, k, s);
+    default: return pairs_f32_norm<D, BR, 0>(p, k, s);
+  }
+}
+template <int D>
+static int pairs_f32_br(const BwdParams& p, const KernelKey& k, hipStream_t s) {
+  return k.branches == 2 ? pairs_f32_pk<D, 2>(p, k, s) : pairs_f32_pk<D, 1>(p, k, s);
+}
+int launch_bwd_pairs_f32(const BwdParams& p, const KernelKey& k, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  return k.d == 128 ? pairs_f32_br<128>(p, k, s) : pairs_f32_br<64>(p, k, s);
 }
 
 }  // namespace tda

@@ -207,6 +207,8 @@ __device__ __forceinline__ void fwd_wave_tile(const FwdParams& P, int qt, int bh
     computed += (any1 ? 1 : 0) + (any2 ? 1 : 0);
     if (any1) word |= 1u << (kt & 31);
     if (any2) word2 |= 1u << (kt & 31);
+    // the query tile's pairs are in no list: the column bucket of the key tile is incomplete
+    if (P.colcnt && (any1 || any2) && l == 0) atomicOr(P.colcnt + (int64_t)bh * P.nkt + kt, kColTaint);
     if (any1 || any2) {
       f32x16 C;
 #pragma unroll
@@ -249,6 +251,11 @@ __device__ __forceinline__ void fwd_wave_tile(const FwdParams& P, int qt, int bh
       occrow[w] = 0u;
       if constexpr (BR == 2) occrow[occ_br + w] = 0u;
     }
+  }
+  if (P.pairs && l == 0) {  // this pass writes no pair list: the backward walks the tiles
+#pragma unroll
+    for (int br = 0; br < BR; ++br)
+      P.pairs[pair_lists(BR, BH, P.nqt) * 4 * kPairCap + ((int64_t)br * BH + bh) * P.nqt + qt] = kPairOverflow;
   }
 
   // Key tiles no query tile sees (keys past the last query position): their inverse norms
@@ -305,6 +312,7 @@ __global__ void __launch_bounds__(64 * BR) fwd_cand_f32(FwdParams P) {
   __shared__ int ckeys[BR][32];     // candidate keys (-1: none)
   __shared__ float crks[BR][32];    // their inverse norms
   __shared__ float xch[BR == 2 ? 16 * ND * 64 : 1];
+  __shared__ __attribute__((aligned(16))) u32x4 plists[BR][kPairCap];  // the branch's pair list
 
   const int l = lane_id(), n32 = l & 31, g = l >> 5;
   const int wv = BR == 2 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;  // = its branch
@@ -365,6 +373,7 @@ __global__ void __launch_bounds__(64 * BR) fwd_cand_f32(FwdParams P) {
   float* crk = crks[br];
   uint32_t* orow = P.occ + lidx * P.occ_w;
   unsigned computed = 0, checked = 0;
+  uint32_t npairs = 0;
 
   f32x16 O[ND];
 #pragma unroll
@@ -397,6 +406,8 @@ __global__ void __launch_bounds__(64 * BR) fwd_cand_f32(FwdParams P) {
     wave_lds_sync();
     uint32_t cnz = 0u;  // candidates with a non-zero weight
     f32x16 C;           // value r: the weight of candidate crow(r, g) for the lane's query
+    u32x4* plist = plists[br];
+    uint32_t* pent = P.pairs ? P.pairs + lidx * (4 * kPairCap) : nullptr;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int c = crow(r, g);
@@ -404,8 +415,36 @@ __global__ void __launch_bounds__(64 * BR) fwd_cand_f32(FwdParams P) {
       const float x = __builtin_fmaf(S[r] * crk[c], rq, -tau);
       const bool pos = key >= 0 && key <= pq && key < Nk && x > 0.f;
       C[r] = pos ? coef * pow_p<PK>(x, pw) : 0.f;
-      const uint64_t bal = wave_ballot(valid && pos);
+      const bool hit = valid && pos;
+      const uint64_t bal = wave_ballot(hit);
       cnz |= ((uint32_t)bal ? 1u << crow(r, 0) : 0u) | ((uint32_t)(bal >> 32) ? 1u << crow(r, 1) : 0u);
+      if (pent) {  // the pair list: the non-zero weights in the order (value r, lane)
+        const uint32_t slot = npairs + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (hit && slot < (uint32_t)kPairCap)
+          plist[slot] = u32x4{(uint32_t)key, (uint32_t)n32, __builtin_bit_cast(uint32_t, x), kNoSlot};
+        npairs += (uint32_t)__builtin_popcountll(bal);
+      }
+    }
+    // The list's entries, lane e for entry e: with column buckets each takes a slot in the bucket
+    // of its key tile and the entry records it; a list past the cap taints the columns of every
+    // candidate with a non-zero weight instead (its pairs past the cap are in no list).
+    const uint32_t ne = min(npairs, (uint32_t)kPairCap);
+    u32x4 pe = u32x4{0u, 0u, 0u, kNoSlot};
+    uint32_t* ccol = P.colcnt ? P.colcnt + (int64_t)bh * P.nkt : nullptr;
+    if (pent) {
+      wave_lds_sync();
+      if ((uint32_t)l < ne) {
+        pe = plist[l];
+        if (ccol) pe[3] = atomicAdd(ccol + ((int)pe[0] >> 5), 1u) & ~kColTaint;  // the slot
+      }
+      if (ccol && npairs > (uint32_t)kPairCap && l < 32 && ((cnz >> l) & 1u)) atomicOr(ccol + (ckey[l] >> 5), kColTaint);
+      if ((uint32_t)l < ne) {
+        *reinterpret_cast<u32x4*>(pent + 4 * l) = pe;
+        if (ccol && pe[3] < (uint32_t)kColCap)
+          *reinterpret_cast<u32x4*>(P.colbuf + (((int64_t)bh * P.nkt + ((int)pe[0] >> 5)) * kColCap + pe[3]) * 4) =
+              u32x4{((uint32_t)(32 * qt) + pe[1]) | (br ? 0x80000000u : 0u), pe[0] & 31u, pe[2], 0u};
+      }
     }
     // out_i += w_ic v_c over the candidates with a non-zero weight, one fused multiply-add per
     // element in increasing key order: each row's sum takes exactly its own non-zero terms in key
@@ -442,6 +481,7 @@ __global__ void __launch_bounds__(64 * BR) fwd_cand_f32(FwdParams P) {
       computed += (unsigned)__builtin_popcount(word);
     }
   }
+  if (P.pairs && l == 0) P.pairs[pair_lists(P.nbr, BH, nqt) * 4 * kPairCap + lidx] = npairs;
   if (P.stats) {
     const float cs = wave_sum((float)computed), ks = wave_sum((float)checked);
     if (l == 0 && ks > 0.f) {

@@ -133,11 +133,13 @@ void record_hip_error(int e) { g_last_hip_error = e; }
 }  // namespace tda
 
 // The column buckets of the pair buffer (tda_params.hpp), on both sides of a training step under
-// the same condition: bf16 with normalisation and more than one query tile (the candidate pass
-// writes them) and no more key tiles than query tiles (the buffer is sized for nqt columns).
+// the same condition: normalisation, head_dim up to 128 and more than one query tile (the bf16
+// and fp32 candidate passes write them) and no more key tiles than query tiles (the buffer is
+// sized for nqt columns).
 template <class Params>
-static void set_columns(Params& p, int64_t bh, int32_t branches, int32_t normalize, int32_t dtype, int64_t seq_len) {
-  if (!p.pairs || !normalize || dtype != TDA_DTYPE_BF16 || seq_len <= 32 || p.nkt > p.nqt) return;
+static void set_columns(Params& p, int64_t bh, int32_t branches, int32_t normalize, int64_t head_dim,
+                        int64_t seq_len) {
+  if (!p.pairs || !normalize || head_dim > 128 || seq_len <= 32 || p.nkt > p.nqt) return;
   uint32_t* cc = const_cast<uint32_t*>(p.pairs) + tda::pair_list_words(branches, bh, p.nqt);
   p.colcnt = cc;
   p.colbuf = cc + tda::col_count_words(bh, p.nqt);
@@ -311,7 +313,7 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
   p.stats = a->stats;
   p.pairs = a->pairs;
   p.nbr = a->branches;
-  set_columns(p, a->batch * a->heads, a->branches, a->normalize, a->dtype, a->seq_len);
+  set_columns(p, a->batch * a->heads, a->branches, a->normalize, a->head_dim, a->seq_len);
   {
     // screen work items: a 256-row block's key tiles 0 .. n - 1 (n grows with the block) cut
     // into chunks of kc tiles; kc is the largest multiple of 32 (whole bitmask words) that still
@@ -409,7 +411,7 @@ int32_t tda_bwd(const tda_bwd_args* a, void* stream) {
   p.stats = a->stats;
   p.pairs = a->occupancy ? a->pairs : nullptr;  // the key-major pass finds the lists through the bitmask
   p.grads_zeroed = a->grads_zeroed ? 1 : 0;
-  set_columns(p, (int64_t)a->batch * a->heads, a->branches, a->normalize, a->dtype, a->seq_len);
+  set_columns(p, (int64_t)a->batch * a->heads, a->branches, a->normalize, a->head_dim, a->seq_len);
   // the key-tile queue, when it holds every key tile
   if (p.pairs && (int64_t)a->batch * a->heads * p.nkt <= lists * tda::kPairCap)
     p.dkvq = reinterpret_cast<uint32_t*>(p.pws + lists * tda::kPairCap);

@@ -140,6 +140,8 @@ int launch_fwd_screen_f32(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_fwd_decode(const FwdParams& p, const KernelKey& k, float* part, void* stream);
 int launch_bwd(const BwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_fast(const BwdParams& p, const KernelKey& k, void* stream);
+// fp32 with the forward's pair lists: the query-major and key-major pair passes (tda_bwd_fast.hip)
+int launch_bwd_pairs_f32(const BwdParams& p, const KernelKey& k, void* stream);
 // head_dim 256 (tda_wide.hip): the column-split forward and backward
 int launch_fwd_wide(const FwdParams& p, const KernelKey& k, void* stream);
 int launch_bwd_wide(const BwdParams& p, const KernelKey& k, void* stream);

@@ -443,8 +443,11 @@ class TDAFunction(torch.autograd.Function):
         bf16 = q1.dtype == torch.bfloat16
         saved = gbuf = None
         norms_p = occ_p = pairs_p = zero_p = zero_bytes = 0
+        # pair lists: written by the bf16 forward and by the fp32 candidate pass (normalised, more
+        # than one query tile); head_dim 256 has its own kernels, which use none
+        want_pairs = need and q1.shape[3] <= 128 and (bf16 or (normalize and q1.shape[2] > 32))
         if need or normalize:
-            (o_n, o_o, o_p), total = _saved_layout(q1.shape, nk, branches, normalize, need and bf16)
+            (o_n, o_o, o_p), total = _saved_layout(q1.shape, nk, branches, normalize, want_pairs)
             saved = torch.empty(total, dtype=torch.uint8, device=dev)
             base = saved.data_ptr()
             norms_p = base + o_n if o_n >= 0 else 0

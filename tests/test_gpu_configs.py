@@ -226,3 +226,56 @@ def test_c2_tda_forward_fp32():
     nt = 4096 // 32
     assert visited == 2 * 64 * nt * (nt + 1) // 2
     assert 0 < computed <= checked < visited // 10
+
+
+def test_c3_tda_gradients_fp32():
+    """The configs[3] shape and inputs in float32 through the public function and autograd: the
+    fp32 forward's candidate pass writes pair lists and the backward runs the pair passes (the
+    tile passes for what they leave).  Sixteen heads covering every b and every h index against
+    fp64 autograd of the formula at the fp32 tolerance 1e-4 (output and every gradient); the
+    totals d beta and d lambda against the sum over all 64 heads (those sixteen in fp64, the rest
+    in fp32) at 1e-4; and the gradients of a head computed alone bitwise equal to the same head of
+    the full call."""
+    shape = (4, 16, 4096, 128)
+    xs = make_inputs(shape, 2, 5, torch.float32)
+    (do,) = make_inputs(shape, 3, 1, torch.float32)
+    leaves = [x.clone().requires_grad_(True) for x in xs]
+    bt = torch.tensor(1.0, device="cuda", requires_grad=True)
+    lt = torch.tensor(0.5, device="cuda", requires_grad=True)
+    out = _tda(*leaves, bt, lt, relu_power=2.0, normalize=True)
+    out.backward(do)
+    names = ["dq1", "dq2", "dk1", "dk2", "dv"]
+    grads_h = [x.grad.cpu() for x in leaves]
+    out_h = out.detach().cpu()
+    want_b = want_l = 0.0
+    checked = set()
+    for b in range(shape[0]):
+        for h in range(shape[1]):
+            sel = h % 4 == b  # every b and every h index among the checked heads
+            dt = torch.float64 if sel else torch.float32
+            ref = tda_grads(*(host(x[b:b + 1, h:h + 1], dt) for x in xs), host(do[b:b + 1, h:h + 1], dt), 1.0, 0.5,
+                            2.0, True, 2, dtype=dt)
+            want_b += ref["dbeta"].item()
+            want_l += ref["dlambda"].item()
+            if not sel:
+                continue
+            assert rel_err(out_h[b:b + 1, h:h + 1], ref["out"]) <= 1e-4, (b, h)
+            for g, name in zip(grads_h, names):
+                r = ref[name]
+                if r.abs().max() == 0:
+                    assert g[b, h].abs().max() == 0, (b, h, name)
+                else:
+                    e = rel_err(g[b:b + 1, h:h + 1], r)
+                    assert e <= 1e-4, (b, h, name, e)
+            checked.add((b, h))
+    assert {b for b, _ in checked} == set(range(4)) and {h for _, h in checked} == set(range(16))
+    assert abs(bt.grad.item() - want_b) <= 1e-4 * abs(want_b), (bt.grad.item(), want_b)
+    assert abs(lt.grad.item() - want_l) <= 1e-4 * abs(want_l), (lt.grad.item(), want_l)
+    # head equivariance: one head alone, bitwise
+    b, h = 3, 7
+    sub = [x[b:b + 1, h:h + 1].clone().requires_grad_(True) for x in xs]
+    bs = torch.tensor(1.0, device="cuda", requires_grad=True)
+    ls = torch.tensor(0.5, device="cuda", requires_grad=True)
+    _tda(*sub, bs, ls, relu_power=2.0, normalize=True).backward(do[b:b + 1, h:h + 1])
+    for s, g in zip(sub, leaves):
+        assert torch.equal(s.grad[0, 0], g.grad[b, h])
