@@ -123,7 +123,8 @@ typedef struct tda_fwd_args {
                                the tile bitmask when occupancy is NULL and, when seq_len <= 32,
                                the fp32 per-chunk partial outputs of the single-query-tile
                                (decode) kernels, else the screen's candidate keys per (branch,
-                               head, query tile) and, for bf16 with normalize, the key rows
+                               head, query tile) and, for normalised calls of either dtype at
+                               head_dim 64 or 128 with more than 32 query rows, the key rows
                                quantised to int8 for the screen (head_dim + 8 bytes per key row
                                and branch) */
   size_t workspace_bytes;
@@ -135,7 +136,11 @@ typedef struct tda_fwd_args {
                                non-zero weights (key index, row, exact threshold margin), which
                                lets the backward read only the rows they name, and (normalised,
                                more than 32 query rows, Nk <= Nq rounded up to 32) the same pairs
-                               bucketed by key tile; bf16 only (the f32 forward leaves it alone) */
+                               bucketed by key tile.  Written by the bf16 forward and by the f32
+                               forward when normalised with more than 32 query rows; the other
+                               f32 forwards mark every list "not written" (the backward then walks
+                               the tiles); head_dim 256 leaves it alone and its backward ignores
+                               it */
   void*    zero;            /* optional (may be NULL with zero_bytes == 0): a device range the
                                call sets to zero, 16-byte aligned, zero_bytes a multiple of 16.
                                For training: the buffer of the backward's gradients, zeroed while
@@ -221,11 +226,12 @@ int32_t tda_bwd(const tda_bwd_args* args, void* stream);
  * is a device array of the library, TDA_NOALLOC_SCRATCH_BYTES (16 MiB) per GPU, held from the
  * first call on that GPU until the process ends.  A call whose workspace
  * (tda_fwd_workspace_bytes_for) exceeds it returns TDA_ERR_SCRATCH before touching the GPU.
- * The normalised bf16 forward's workspace holds int8 copies of the key rows (head_dim + 8
- * bytes per key row and branch): TRA at B*H = 64, seq_len 2048, head_dim 64 needs 9.6 MiB and
- * fits; differential TDA at B*H = 64, seq_len 4096, head_dim 128 needs 70.3 MiB and does not;
- * without normalize the same call needs 2.3 MiB, and one query against B*H = 64 heads of 16384
- * keys 0.5 MiB.  Every call on one GPU shares that GPU's array, which keeps the last call's
+ * A normalised forward (bf16 or fp32, head_dim 64 or 128, more than 32 query rows) holds int8
+ * copies of the key rows in its workspace (head_dim + 8 bytes per key row and branch): TRA at
+ * B*H = 64, seq_len 2048, head_dim 64 needs 9.6 MiB and fits (in either dtype); fp32 TRA at
+ * B*H = 16, seq_len 4096, head_dim 128 needs 8.8 MiB and fits; differential TDA at B*H = 64,
+ * seq_len 4096, head_dim 128 needs 70.3 MiB and does not; without normalize the same call needs
+ * 2.3 MiB, and one query against B*H = 64 heads of 16384 keys 0.5 MiB.  Every call on one GPU shares that GPU's array, which keeps the last call's
  * contents: calls that overlap on one GPU (other streams, unordered host threads) race and
  * must be serialised by the caller.  The outputs (out, norms, occupancy, pairs, stats) are
  * the caller's as for tda_fwd. */

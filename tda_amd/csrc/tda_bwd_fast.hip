@@ -811,7 +811,7 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
   // ---- the column's bucket, when the forward filled it with every pair of the column (one
   // round of loads; the pairs are then taken in the order (key row, branch, query row))
   bool from_bucket = false;
-  if (P.colcnt && !P.stats) {
+  if (P.colcnt) {
     const int64_t col = (int64_t)bh * P.nkt + kt;
     const uint32_t cc = (uint32_t)__builtin_amdgcn_readfirstlane((int)P.colcnt[col]);
     const u32x4 be = *reinterpret_cast<const u32x4*>(P.colbuf + (col * kColCap + l) * 4);
@@ -828,6 +828,12 @@ __global__ void __launch_bounds__(64) bwd_dkv_pairs(BwdParams P) {
 #pragma unroll
       for (int br = 0; br < BR; ++br)
         used[br] = wave_or(in && (int)(((uint32_t)pi_l >> 31) & 1u) == br ? 1u << pjl_l : 0u);
+      if (P.stats) {  // the counters as the walk counts them: (branch, query tile) lists in the column
+        const int lk = (int)(((uint32_t)pi_l >> 31) << 30) | ((pi_l & 0x7fffffff) >> 5);
+        bool dup = false;
+        for (int f = 0; f < (int)np; ++f) dup = dup || (f < l && __builtin_amdgcn_readlane(lk, f) == lk);
+        visited = (unsigned)__builtin_popcountll(wave_ballot(in && !dup));
+      }
     }
   }
 

@@ -581,6 +581,15 @@ int launch_zero(const FwdParams& p, void* stream) {
 // when normalised with more than one query tile.  The screen clears the call's zero range; the
 // other paths launch zero_range.
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream) {
+  if (p.zero && p.zero_per_it == 0) {
+    // a zero range too large for the screen's per-item slices: cleared whole first
+    const int ez = launch_zero(p, stream);
+    if (ez) return ez;
+    FwdParams q = p;
+    q.zero = nullptr;
+    q.zero_units = 0;
+    return launch_fwd(q, k, stream);
+  }
   int e;
   if (k.d == 256) {  // both dtypes: the column-split kernels of tda_wide.hip (no screen)
     e = launch_fwd_wide(p, k, stream);

@@ -138,7 +138,8 @@ __device__ __forceinline__ ScreenItem screen_item(const FwdParams& P, int BR) {
 // The item's slice of the call's zero range (the backward's gradients in training): an item
 // clears zero_per_it 16-byte units per key tile it walks, from the steps of the items before it
 // in (stream, block, chunk) order.  Buffer stores over the slice: the hardware drops those past
-// its end (a slice is below 1 MiB, so 32-bit offsets); streaming (nt): the backward reads them
+// its end (the host hands the screen slices below 2^31 bytes, so 32-bit offsets; a larger range
+// is cleared whole by zero_range before the screen); streaming (nt): the backward reads them
 // much later.
 struct ZeroSlice {
   __amdgpu_buffer_rsrc_t r;

@@ -354,7 +354,11 @@ int32_t tda_fwd(const tda_fwd_args* a, void* stream) {
       steps += klast + 1;
     }
     steps *= (int64_t)a->branches * a->batch * a->heads;
-    p.zero_per_it = (int)((p.zero_units + steps - 1) / steps);
+    // an item's slice (zero_per_it units per key tile, at most screen_kc tiles) is addressed
+    // with 32-bit byte offsets: a range whose slices could reach 2^31 bytes (a large range
+    // against a small problem) is cleared whole by zero_range instead (zero_per_it 0)
+    const int64_t per_it = (p.zero_units + steps - 1) / steps;
+    p.zero_per_it = per_it * 16 * p.screen_kc < (int64_t(1) << 31) ? (int)per_it : 0;
   }
   const tda::KernelKey key{a->dtype, (int)a->head_dim, a->branches, pkind_of(a->relu_power), a->normalize ? 1 : 0};
   tda::timing_begin(stream);

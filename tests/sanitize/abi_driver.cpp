@@ -118,6 +118,21 @@ int main() {
     CHECK(p.zero_units == (int64_t)a.zero_bytes / 16);
     CHECK((int64_t)p.zero_per_it == (p.zero_units + steps - 1) / steps);
     CHECK((int64_t)p.zero_per_it * steps >= p.zero_units);
+    CHECK((int64_t)p.zero_per_it * 16 * p.screen_kc < (int64_t(1) << 31));
+  }
+  {
+    // a zero range far larger than the problem (two key-tile steps): the screen's 32-bit slice
+    // offsets would wrap, so the host leaves the whole range to zero_range (zero_per_it 0)
+    tda_fwd_args a = fwd_args(1, 1, 64, 128, 1);
+    a.workspace_bytes = tda_fwd_workspace_bytes(1, 1, 64, 1);
+    a.zero = FAKE;
+    a.zero_bytes = (uint64_t)1 << 33;
+    CHECK(tda_fwd(&a, nullptr) == TDA_OK);
+    CHECK(stub::last_fwd.zero == FAKE && stub::last_fwd.zero_units == (int64_t)1 << 29);
+    CHECK(stub::last_fwd.zero_per_it == 0);
+    a.zero_bytes = (uint64_t)1 << 20;  // a small range keeps the per-item slices
+    CHECK(tda_fwd(&a, nullptr) == TDA_OK);
+    CHECK(stub::last_fwd.zero_per_it > 0 && (int64_t)stub::last_fwd.zero_per_it * 16 * stub::last_fwd.screen_kc < (int64_t(1) << 31));
   }
   {
     tda_fwd_args a = fwd_args(1, 2, 5, 64, 1);  // one query tile: the decode partials

@@ -271,3 +271,25 @@ def test_column_buckets_hold_the_listed_pairs(shape, branches, beta):
     for a, b2 in zip(g1, g2):
         if a is not None:
             assert torch.equal(2 * a, b2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_counters_do_not_change_the_backward(dtype):
+    """The backward with the counters (stats) takes the same path as without them (the
+    key-major pair pass reads the column buckets either way): every gradient bitwise equal,
+    for both dtypes with pair lists (the fp32 forward's candidate pass writes them too)."""
+    from tda_amd import ops
+    shape = (2, 3, 400, 128)
+    q1, k1, q2, k2, v, do = make_inputs(shape, 81, 6, dtype)
+    bt = torch.full((), 0.5, device="cuda")
+    lt = torch.full((), 0.5, device="cuda")
+    norms, occ = ops.side_buffers(shape, 2, True, "cuda")
+    pairs = ops.pair_buffer(shape, 2, "cuda")
+    with torch.no_grad():
+        ops.forward(q1, k1, q2, k2, v, bt, lt, 2.0, True, 2, norms=norms, occupancy=occ, pairs=pairs)
+        plain = ops.backward(q1, k1, q2, k2, v, do, bt, lt, 2.0, True, 2, norms, occ, pairs=pairs)
+        st = torch.zeros(3, dtype=torch.int64, device="cuda")
+        counted = ops.backward(q1, k1, q2, k2, v, do, bt, lt, 2.0, True, 2, norms, occ, pairs=pairs, stats=st)
+    for a, b in zip(plain, counted):
+        assert torch.equal(a, b)
+    assert int(st[0]) > 0

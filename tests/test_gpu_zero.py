@@ -46,6 +46,22 @@ def test_forward_clears_its_zero_range(shape, nk, off, br, dtype, norm):
     assert int(torch.count_nonzero(zbuf)) == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_large_zero_range_against_small_problem(dtype):
+    """A zero range far larger than the problem (one head of 64 rows: two key-tile steps of the
+    screen for 192 MiB): the screen's per-item slices would pass its 32-bit offsets, so the range
+    is cleared whole first; it still ends all zeros and the output does not change."""
+    q1, q2, k1, k2, v = _inputs((1, 1, 64, 128), dtype, 22)
+    beta, lam = torch.tensor(0.4, device="cuda"), torch.tensor(0.5, device="cuda")
+    with torch.no_grad():
+        ref = ops.forward(q1, k1, q2, k2, v, beta, lam, 2.0, True, 2)
+        zbuf = torch.full((96 << 20,), 7.0, dtype=torch.bfloat16, device="cuda")
+        out = ops.forward(q1, k1, q2, k2, v, beta, lam, 2.0, True, 2, zero=zbuf)
+        torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert int(torch.count_nonzero(zbuf)) == 0
+
+
 @pytest.mark.parametrize("shape,br,norm,p", [((2, 3, 300, 128), 2, True, 2.0), ((1, 2, 200, 64), 1, True, 1.5),
                                             ((2, 2, 256, 64), 2, False, 2.0)])
 def test_backward_on_cleared_gradients_is_bitwise_the_full_store(shape, br, norm, p):
