@@ -265,7 +265,72 @@ def side_configs(steps: int, warmup: int):
                                                          q_offset=NK - 1), dev)}
     del qd1, qd2, kd1, kd2, vd
     res["fp32"] = fp32_figures(dev, stream)
+    res["dense"] = dense_figures(dev, stream, steps)
     return res
+
+
+def dense_figures(dev, stream, steps):
+    """The reference's default call (threshold_rela_triton(q, k, v, beta): no normalisation,
+    TTA:472-486, README.md:20-31) at the configs[1] shape (4, 16, 2048, 64), beta = 1, p = 2: raw
+    dot products of N(0, 1) rows pass their threshold about half the time, so every tile holds
+    weights (the dense regime).  bf16 forward and forward+backward (the step through autograd),
+    and fp32 the same.  Counted FLOPs: forward 2U (Q K^T and A V over the causal half), forward +
+    backward 7U (the backward's recomputed scores, dP = dO V^T, dQ, dK and dV).  The forward's
+    dominant kernel, the tile pass fwd_pv, against the bf16 peak on the work it executes (a score
+    tile and an A.V tile per non-zero tile, from the kernels' counters)."""
+    import torch
+
+    from tda_amd import ops, threshold_rela_triton
+
+    shape = (4, 16, 2048, 64)
+    out = {}
+    for name, dt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+        g = torch.Generator("cpu").manual_seed(1)
+        q, k, v = (torch.randn(shape, generator=g).to(dt).to(dev) for _ in range(3))
+        do = torch.randn(shape, generator=torch.Generator("cpu").manual_seed(3)).to(dt).to(dev)
+        beta = torch.tensor(1.0, device=dev)
+        fwd = lambda: ops.forward(q, k, None, None, v, beta, None, 2.0, False, 1)  # noqa: E731
+        with torch.no_grad():
+            ms_f = time_calls(stream, fwd, steps, 2)
+            lu, _ = time_launches(fwd, max(3, steps // 2), 1)
+        st = tile_stats(lambda s: ops.forward(q, k, None, None, v, beta, None, 2.0, False, 1, stats=s), dev)
+        leaves = [x.clone().requires_grad_(True) for x in (q, k, v)]
+
+        def step():
+            for t in leaves:
+                t.grad = None
+            threshold_rela_triton(*leaves, beta, relu_power=2.0).backward(do)
+
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_s = e0.elapsed_time(e1) / steps
+        peak = PEAK_BF16_TFLOPS if dt == torch.bfloat16 else PEAK_F32_TFLOPS
+        rec = {"workload": f"TRA {name} {shape} seed 1, beta=1, p=2, normalize=False (the reference's default call)",
+               "fwd_ms": ms_f, "fwd_tflops": units(shape, 2.0) / (ms_f * 1e-3) / 1e12,
+               "fwd_pct_peak": 100.0 * units(shape, 2.0) / (ms_f * 1e-3) / 1e12 / peak,
+               "fwd_launch_us": {kk: round(t, 2) for kk, t in lu.items()},
+               "fwd_bwd_ms": ms_s, "fwd_bwd_tflops": units(shape, 7.0) / (ms_s * 1e-3) / 1e12,
+               "fwd_bwd_pct_peak": 100.0 * units(shape, 7.0) / (ms_s * 1e-3) / 1e12 / peak,
+               "peak_tflops": peak, **st}
+        pv = lu.get("fwd_pv") or lu.get("fwd_wave")
+        if pv:
+            executed = st["tiles_nonzero"] * 2 * tile_flops(shape[3])
+            rec["tile_pass"] = {"kernel": "fwd_pv" if "fwd_pv" in lu else "fwd_wave", "launch_us": pv,
+                                "executed_gflop": executed / 1e9,
+                                "achieved_tflops": executed / (pv * 1e-6) / 1e12,
+                                "frac_of_peak": executed / (pv * 1e-6) / 1e12 / peak,
+                                "note": "a score tile and an A.V tile per non-zero tile (the fp32 pass also "
+                                        "scores every causal tile: executed counts the non-zero ones only)"}
+        out[name] = rec
+        del q, k, v, do, leaves
+    return out
 
 
 def fp32_figures(dev, stream):
