@@ -199,6 +199,24 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += __shfl_xor(v, 16);
   return v + __shfl_xor(v, 32);
 }
+// Workgroup barrier for hand-offs through LDS only: the wave's LDS operations complete
+// (lgkmcnt(0)), then s_barrier; the wavefront-scope fences keep the compiler from moving memory
+// operations across it.  __syncthreads()'s workgroup release fence also waits for every
+// outstanding global load and store (vmcnt(0)), which would drain loads issued ahead (into
+// registers, or into LDS by direct loads whose own completion the caller waits for); here they
+// stay in flight.  Not for data handed over through global memory.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt at their maxima (no wait)
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+// Wave-wide integer sum (every lane ends with the total).  Call with every lane active.
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += (uint32_t)__shfl_xor((int)v, m);
+  return v;
+}
 // Wave-wide OR, the same way.
 __device__ __forceinline__ uint32_t wave_or(uint32_t v) {
   v |= (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);

@@ -559,7 +559,7 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
   fetch(0);
   commit(0);
   if (nit > 1) fetch(1);
-  __syncthreads();
+  lds_barrier();
   for (int i = 0; i < nit; ++i) {
 #pragma unroll
     for (int j = 0; j < TPB; ++j) {
@@ -572,7 +572,7 @@ __global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) 
     // the other super-stage was last read before the previous barrier
     if (i + 1 < nit) commit(i + 1);
     if (i + 2 < nit) fetch(i + 2);
-    __syncthreads();
+    lds_barrier();  // the fetch stays in flight across it
   }
   screen_count<QPW>(P, it, live, ktl);
 }
@@ -848,7 +848,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
   auto stage = [&](int j, auto SLOT) {
     constexpr int st = decltype(SLOT)::value;
     wait_stage(j);
-    __syncthreads();  // stage j is in LDS; every wave is past stage j - 1, whose slot is reloaded
+    lds_barrier();  // stage j is in LDS; every wave is past stage j - 1, whose slot is reloaded
     if (j + I8_AHEAD < nst) issue(j + I8_AHEAD);
     if (P.zero) zs.clear<NTHR>(P, TPI * j, tid, min(TPI, nit - TPI * j));
     if (j <= jl) {
@@ -1107,6 +1107,298 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
     int bh, qt;
     pv_item(first + __builtin_ctzll(m), BH, nqt, bh, qt);
     fwd_pv_tile<D, BR, PK, NORM>(P, vst, kst, bh, qt);
+  }
+}
+
+// ------------------------------------------------------------------ fwd_pv_blk
+// The tile pass of the forwards without candidate lists (every query tile runs), over kBlkTiles
+// consecutive query tiles of one head, one wave each.  The waves walk the union of their bitmask
+// rows' kept key tiles in step and share each key tile's K and V rows (and key norms): the
+// workgroup loads them once, each wave a quarter of the rows, one tile ahead into registers,
+// then into a two-stage LDS ring (one barrier per tile: a stage is rewritten two tiles after it
+// was read, and every wave has passed the barrier between).  A wave computes only the tiles its
+// own row keeps, exactly as fwd_pv_tile does (the same MFMA sequence on the same operands: the
+// same rows, bitmask rewrite, pair lists and counters).  Once a pair list has passed its cap
+// the wave only counts its non-zero weights (one wave sum at the end) instead of placing them.
+constexpr int kBlkTiles = 4;
+
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(64 * kBlkTiles) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 2))) fwd_pv_blk(FwdParams P) {
+  constexpr int W = kBlkTiles;
+  constexpr int NT = D / 16, ND = D / 32;
+  constexpr int VS = D + 32;     // LDS row stride of a V tile: conflict-free transpose reads
+  constexpr int KS = D + 8;      // LDS row stride of a K tile: conflict-free row-fragment reads
+  constexpr int CPR = D / 8;     // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;  // rows per load instruction
+  constexpr int LPW = 32 / RPI / W;  // load instructions per wave, K and V each
+  static_assert(LPW >= 1 && LPW * RPI * W == 32, "K/V tile rows split evenly over the waves");
+  constexpr int STAGE = 32 * KS + 32 * VS;
+  static_assert(2 * STAGE >= W * 32 * KS, "the ring holds the waves' output rows");
+  __shared__ __attribute__((aligned(16))) bf16 ring[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) float nring[2][32];
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
+  const int nqb = (nqt + W - 1) / W;
+  int bh, jb;
+  {
+    // longest blocks (last query tiles) of every head first; one head's blocks on one XCD when
+    // the heads fill the eight XCDs
+    const int bid = blockIdx.x;
+    if (BH % 8 == 0) {
+      const int x = bid & 7, j = bid >> 3, hg = BH / 8;
+      bh = x + 8 * (j % hg);
+      jb = nqb - 1 - j / hg;
+    } else {
+      bh = bid % BH;
+      jb = nqb - 1 - bid / BH;
+    }
+  }
+  const int b = bh / P.H, h = bh % P.H;
+  const int qt = W * jb + wv;
+  const bool act = qt < nqt;  // wave-uniform: waves past the last query tile only load
+  const int qtc = act ? qt : nqt - 1;
+  const int iq = 32 * qt + n32;
+  const bool valid = act && iq < Nq;
+  const bool rowpad = 32 * qt + 31 >= Nq;  // the query tile has rows past Nq (uniform)
+  const int pq = qoff + iq;  // the lane's query position
+  const int klast_b = kt_last(min(W * jb + W - 1, nqt - 1), qoff, P.nkt);  // the block's last key tile
+  const float tau = *P.beta * tau_coeff(pq, P.inv_d);
+  const float pw = P.p;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+
+  const int vrow0 = RPI * LPW * wv + l / CPR, vch = l % CPR;  // this wave's rows of the K/V tiles
+  const int bk = l >> 4, jj = l & 15;
+  const int voff = (4 * (bk >> 1) + (jj >> 2)) * VS + 16 * (bk & 1) + 4 * (jj & 3);
+
+  f32x16 O[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) O[c] = f32x16{};
+  unsigned computed = 0, checked = 0;
+  int it = 0;  // ring position, continued across the branches
+
+#pragma unroll
+  for (int br = 0; br < BR; ++br) {
+    const int qslot = br ? F_Q2 : F_Q1, kslot = br ? F_K2 : F_K1;
+    uint32_t* orow0 = P.occ + ((int64_t)(br * BH + bh) * nqt + W * jb) * P.occ_w;  // the block's first row
+    const bf16* khead = (const bf16*)P.in[kslot] + (int64_t)b * P.s[kslot][0] + (int64_t)h * P.s[kslot][1];
+    const bf16* vhead = (const bf16*)P.in[F_V] + (int64_t)b * P.s[F_V][0] + (int64_t)h * P.s[F_V][1];
+    const int64_t sk = P.s[kslot][2], sv = P.s[F_V][2];
+    const __amdgpu_buffer_rsrc_t rn =
+        make_rsrc(NORM ? P.norms + norm_base(P, br ? N_K2 : N_K1, bh) : nullptr, NORM ? (uint32_t)Nk * 4 : 0u);
+    const float coef = br == 0 ? 1.f : -lam;
+    // query fragments straight from the rows (rows past Nq read as zeros), the inverse norm
+    bf16x8 Q[NT];
+    {
+      const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
+      const int64_t sq = P.s[qslot][2];
+      const __amdgpu_buffer_rsrc_t rq_ = tile_rsrc<D>(qhead, sq, qtc, Nq);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        Q[t] = __builtin_bit_cast(bf16x8, buf_load16(rq_, (uint32_t)((n32 * sq + 16 * t + 8 * g) * 2)));
+    }
+    float rq = 1.f;
+    if constexpr (NORM) rq = P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + min(32 * qtc + n32, Nq - 1)];
+    const int64_t lidx = ((int64_t)br * BH + bh) * nqt + qtc;
+    uint32_t* pent = P.pairs && act ? P.pairs + lidx * (4 * kPairCap) : nullptr;
+    uint32_t npairs = 0, extra = 0;
+
+    // word w of row r of the block, masked to the key tiles the row sees (uniform)
+    auto row_word = [&](int r, int w) -> uint32_t {
+      const int q = W * jb + r;
+      if (q >= nqt) return 0u;
+      const int kl = kt_last(q, qoff, P.nkt);
+      if (w > (kl >> 5)) return 0u;
+      uint32_t x = (uint32_t)__builtin_amdgcn_readfirstlane((int)orow0[(int64_t)r * P.occ_w + w]);
+      if (w == (kl >> 5) && (kl & 31) != 31) x &= (2u << (kl & 31)) - 1u;
+      return x;
+    };
+    // the union walk: next key tile any row keeps, its word, and the own row's word
+    int sw = -1;
+    uint32_t ub = 0u, sown = 0u;
+    auto next_tile = [&](int& w_out, uint32_t& own_out) -> int {
+      while (ub == 0u) {
+        if (++sw > (klast_b >> 5)) return -1;
+        uint32_t u = 0u, o = 0u;
+#pragma unroll
+        for (int r = 0; r < W; ++r) {
+          const uint32_t x = row_word(r, sw);
+          u |= x;
+          o = r == wv ? x : o;
+        }
+        ub = u;
+        sown = o;
+      }
+      const int kt = 32 * sw + __builtin_ctz(ub);
+      ub &= ub - 1u;
+      w_out = sw;
+      own_out = sown;
+      return kt;
+    };
+    u32x4 kr[LPW], vr[LPW];
+    f32x4 nr = {};
+    auto issue = [&](int kt) {
+      const __amdgpu_buffer_rsrc_t rk = tile_rsrc<D>(khead, sk, kt, Nk);
+      const __amdgpu_buffer_rsrc_t rv = tile_rsrc<D>(vhead, sv, kt, Nk);
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) kr[i] = buf_load16(rk, (uint32_t)(((vrow0 + RPI * i) * sk + 8 * vch) * 2));
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) vr[i] = buf_load16(rv, (uint32_t)(((vrow0 + RPI * i) * sv + 8 * vch) * 2));
+      if (NORM && wv == 0 && l < 8) nr = __builtin_bit_cast(f32x4, buf_load16(rn, (uint32_t)(32 * kt + 4 * l) * 4));
+    };
+
+    int cw = 0;
+    uint32_t cown = 0u;
+    int kt = next_tile(cw, cown);
+    if (kt >= 0) issue(kt);
+    uint32_t keep = cown;  // own word cw with the tiles of no non-zero weight cleared
+    while (kt >= 0) {
+      bf16* kst = ring + (it & 1) * STAGE;
+      bf16* vst = kst + 32 * KS;
+      float* nst = nring[it & 1];
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) {
+        *reinterpret_cast<u32x4*>(kst + (vrow0 + RPI * i) * KS + 8 * vch) = kr[i];
+        *reinterpret_cast<u32x4*>(vst + (vrow0 + RPI * i) * VS + 8 * vch) = vr[i];
+      }
+      if (NORM && wv == 0 && l < 8) *reinterpret_cast<f32x4*>(nst + 4 * l) = nr;
+      int nw = 0;
+      uint32_t nown = 0u;
+      const int kt2 = next_tile(nw, nown);
+      if (kt2 >= 0) issue(kt2);  // in flight during this tile's work
+      lds_barrier();
+      ++it;
+      if ((cown >> (kt & 31)) & 1u) {
+        ++checked;
+        f32x16 S = {};
+        const bf16* kp = kst + n32 * KS + 8 * g;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) S = PolBF16::mma(*reinterpret_cast<const bf16x8*>(kp + 16 * t), Q[t], S);
+        f32x4 rk4[4] = {{1.f, 1.f, 1.f, 1.f}, {1.f, 1.f, 1.f, 1.f}, {1.f, 1.f, 1.f, 1.f}, {1.f, 1.f, 1.f, 1.f}};
+        if constexpr (NORM) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) rk4[u] = *reinterpret_cast<const f32x4*>(nst + 8 * u + 4 * g);
+        }
+        // exact values x, branch-free: keys after the query's position, padding keys past Nk
+        // and query rows past Nq are set to -1 (no weight).  Only tiles reaching past the
+        // position of the tile's first row or past Nk, and the last query tile when Nq is not a
+        // multiple of 32, have any.
+        f32x16 X;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) X[4 * u + e] = __builtin_fmaf(NORM ? S[4 * u + e] * rk4[u][e] : S[4 * u + e], rq, -tau);
+        if (32 * kt + 31 > min(qoff + 32 * qt, Nk - 1) || rowpad) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = 32 * kt + crow(r, g);
+            X[r] = valid && key <= pq && key < Nk ? X[r] : -1.f;
+          }
+        }
+        // weights coef relu(x)^p and the lane's largest x (some weight of the tile is non-zero
+        // iff a lane's is > 0), on the bits: a float is > 0 iff its bits as an int32 are, so the
+        // integer max(bits, 0) is relu(x) (no NaN handling to pay for in float max); p other than
+        // 1, 2 select on x > 0.  (Whole-vector bit casts: hipcc compiled a bit cast of one
+        // element of an ext_vector to element 0.)
+        typedef int i32x16 __attribute__((ext_vector_type(16)));
+        const i32x16 XB = __builtin_bit_cast(i32x16, X);
+        i32x16 TB;
+        int xmb = XB[0];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          TB[r] = max(XB[r], 0);
+          if (r) xmb = max(xmb, XB[r]);
+        }
+        const f32x16 T = __builtin_bit_cast(f32x16, TB);
+        f32x16 C;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          if constexpr (PK == 2) C[r] = T[r] * (coef * T[r]);
+          else if constexpr (PK == 1) C[r] = coef * T[r];
+          else C[r] = X[r] > 0.f ? coef * pow_p<PK>(X[r], pw) : 0.f;
+        }
+        const bool pos_any = xmb > 0;
+        if (pent) {
+          if (npairs < (uint32_t)kPairCap) {
+            // list entries of the non-zero weights, in the order (value r, lane); x's bits through
+            // a bit cast of the whole vector (hipcc compiled a bit cast of one element of an
+            // ext_vector to element 0)
+            typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+            const u32x16 XU = __builtin_bit_cast(u32x16, X);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const bool hit = X[r] > 0.f;
+              const uint64_t bal = wave_ballot(hit);
+              const uint32_t slot = npairs + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+              if (hit && slot < (uint32_t)kPairCap)
+                *reinterpret_cast<u32x4*>(pent + 4 * slot) =
+                    u32x4{(uint32_t)(32 * kt + crow(r, g)), (uint32_t)n32, XU[r], kNoSlot};
+              npairs += (uint32_t)__builtin_popcountll(bal);
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) extra += X[r] > 0.f ? 1u : 0u;
+          }
+        }
+        if (wave_ballot(pos_any) == 0ull) {
+          keep &= ~(1u << (kt & 31));
+        } else {
+          // pairs of the tile pass are in no column bucket: the key-major backward walks the lists
+          if (P.colcnt && l == 0) atomicOr(P.colcnt + (int64_t)bh * P.nkt + kt, kColTaint);
+          ++computed;
+        }
+        // A V on every tile the row keeps (a tile of zero weights adds zero products: the same
+        // sums bit for bit, and no branch around the accumulators)
+        const bf16x8 PF0 = PolBF16::pack_c(C, 0), PF1 = PolBF16::pack_c(C, 1);
+        const bf16* vp = vst + voff;
+#pragma unroll
+        for (int c = 0; c < ND; ++c) {
+          O[c] = PolBF16::mma(tr_frag<VS>(vp + 32 * c), PF0, O[c]);
+          O[c] = PolBF16::mma(tr_frag<VS>(vp + 32 * c + 16 * VS), PF1, O[c]);
+        }
+      }
+      if (kt2 < 0 || nw != cw) {  // the own row's word cw is done
+        if (act && keep != cown && l == 0) orow0[(int64_t)wv * P.occ_w + cw] = keep;
+        cw = nw;
+        cown = keep = nown;
+      }
+      kt = kt2;
+    }
+    if (pent) {
+      npairs += wave_sum_u32(extra);
+      if (l == 0) P.pairs[pair_lists(P.nbr, BH, nqt) * 4 * kPairCap + lidx] = npairs;
+    }
+  }
+
+  // Output rows through LDS (the wave's slice of the ring, free once every wave has passed the
+  // barrier below): lane (n, g) holds elements 32c + crow(r, g) of row n; stores then cover whole
+  // rows, 16 bytes per lane.
+  __syncthreads();
+  if (!act) return;
+  bf16* ost = ring + wv * 32 * KS;
+#pragma unroll
+  for (int c = 0; c < ND; ++c)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      store4(ost + n32 * KS + 32 * c + 8 * u + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2], O[c][4 * u + 3]);
+  wave_lds_sync();
+  {
+    bf16* ohead = (bf16*)P.out + (int64_t)b * P.s[F_OUT][0] + (int64_t)h * P.s[F_OUT][1];
+    constexpr int OL = 32 / RPI;
+#pragma unroll
+    for (int i = 0; i < OL; ++i) {
+      const int r = l / CPR + RPI * i, row = 32 * qt + r;
+      if (row < Nq)
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(ost + r * KS + 8 * vch),
+                                    reinterpret_cast<u32x4*>(ohead + (int64_t)row * P.s[F_OUT][2] + 8 * vch));
+    }
+  }
+  if (P.stats && l == 0 && checked) {
+    atomicAdd(P.stats + 1, (unsigned long long)computed);
+    atomicAdd(P.stats + 2, (unsigned long long)checked);
   }
 }
 
@@ -1419,8 +1711,9 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   if (NORM && p.cand) {  // the query tiles the candidate pass could not take, from its queue
     const int items = BH * p.nqt;
     hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)(items < 2048 ? items : 2048)), dim3(64), 0, s, p, 0);
-  } else {
-    hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)(BH * p.nqt)), dim3(64), 0, s, p, 1);
+  } else {  // every query tile runs: blocks of query tiles sharing their key tiles
+    const unsigned blocks = (unsigned)(BH * ((p.nqt + kBlkTiles - 1) / kBlkTiles));
+    hipLaunchKernelGGL((fwd_pv_blk<D, BR, PK, NORM>), dim3(blocks), dim3(64 * kBlkTiles), 0, s, p);
   }
   launched(s, "fwd_pv");
   return (int)hipGetLastError();
