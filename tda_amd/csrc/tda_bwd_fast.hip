@@ -1289,11 +1289,491 @@ __global__ void __launch_bounds__(64) bwd_tiles(BwdParams P) {
   for (uint32_t k = blockIdx.x; k < queued; k += gridDim.x) bwd_dkv_tile<D, BR, PK, NORM>(P, W, P.dkvq[1 + k]);
 }
 
+// ------------------------------------------------------------------ block tile passes
+// For the backwards whose forward ran the block tile pass (no candidate lists, every query tile
+// runs): kBwdBlk consecutive tiles of one head per workgroup, one wave each, walking the union of
+// their bitmask tiles in step; each streamed tile's rows are loaded once per workgroup (each wave
+// a quarter, one tile ahead into registers) into a two-stage LDS ring of swizzled tiles (the
+// layout of dma_tile_b: tile_row_frag / tile_tr_frag read it), one fence-free barrier per tile.
+// A wave computes only its own tiles, with the arithmetic of bwd_dq_tile / bwd_dkv_tile, the
+// masks branch-free and only on the tiles that need them.
+constexpr int kBwdBlk = 4;
+
+// This wave's share of a 32-row tile of D columns: rows RPI (LPW wv + i) + l / CH, chunk l % CH.
+template <int D>
+struct BlkRows {
+  static constexpr int CH = D / 8, RPI = 64 / CH, LPW = 32 / RPI / kBwdBlk;
+  static_assert(LPW >= 1 && LPW * RPI * kBwdBlk == 32, "tile rows split evenly over the waves");
+  u32x4 v[LPW];
+  __device__ __forceinline__ void load(const bf16* rows, int64_t st, int r0, int n, int wv) {
+    const int l = lane_id();
+    const int nr = min(32, n - r0);
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(rows + (int64_t)r0 * st, (uint32_t)(((int64_t)(nr - 1) * st + D) * 2));
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int r = RPI * (LPW * wv + i) + l / CH;
+      v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(((int64_t)r * st + 8 * (l % CH)) * 2), 0, 0);
+    }
+  }
+  __device__ __forceinline__ void store(bf16* tile, int wv) const {
+    const int l = lane_id();
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int r = RPI * (LPW * wv + i) + l / CH;
+      *reinterpret_cast<u32x4*>(tile + r * D + 8 * ((l % CH) ^ bswz<D>(r))) = v[i];
+    }
+  }
+};
+
+// Query-major: kBwdBlk query tiles of one (branch, head), streaming K, V and the key norms.
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(64 * kBwdBlk) __attribute__((amdgpu_waves_per_eu(2))) bwd_dq_blk(BwdParams P) {
+  constexpr int W = kBwdBlk, NT = D / 16, ND = D / 32;
+  constexpr int STAGE = 2 * 32 * D;  // K tile, V tile
+  __shared__ __attribute__((aligned(16))) bf16 ring[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) float nring[2][32];
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int BH = P.B * P.H, nqt = P.nqt, Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
+  const int nqb = (nqt + W - 1) / W;
+  // longest blocks (last query tiles) of every (head, branch) first, the branches adjacent
+  const int bid = blockIdx.x, jb = nqb - 1 - bid / (BR * BH), rem = bid % (BR * BH);
+  const int br = BR == 2 ? rem & 1 : 0, bh = BR == 2 ? rem >> 1 : rem;
+  const int b = bh / P.H, h = bh % P.H;
+  const uint32_t* counts = P.pairs ? P.pairs + pair_lists(BR, BH, nqt) * 4 * kPairCap : nullptr;
+  const int64_t lrow0 = ((int64_t)br * BH + bh) * nqt + W * jb;  // list / bitmask row of the block's first tile
+  // the tiles whose lists did not fit (or all, without lists): the same for every wave
+  uint32_t needm = 0u;
+#pragma unroll
+  for (int r = 0; r < W; ++r) {
+    const int q = W * jb + r;
+    const bool nd = q < nqt && (!counts || (uint32_t)__builtin_amdgcn_readfirstlane((int)counts[lrow0 + r]) > (uint32_t)kPairCap);
+    needm |= nd ? 1u << r : 0u;
+  }
+  if (!needm) return;
+  const int qt = W * jb + wv;
+  const bool need = (needm >> wv) & 1u;
+  const int qtc = min(qt, nqt - 1);
+  const int i = 32 * qt + n32;
+  const bool qvalid = need && i < Nq;
+  const int ic = min(32 * qtc + n32, Nq - 1);
+  const int pq = qoff + i;
+  const bool rowpad = 32 * qt + 31 >= Nq;
+  auto base = [&](int slot) {
+    return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
+  };
+  const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
+  bf16x8 DO[NT], Q[NT];
+  {
+    const bf16* r = base(B_DO) + (int64_t)ic * P.s[B_DO][2];
+    const bf16* rq_ = base(qslot) + (int64_t)ic * P.s[qslot][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      DO[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+      Q[t] = *reinterpret_cast<const bf16x8*>(rq_ + 16 * t + 8 * g);
+    }
+  }
+  const float rq = NORM ? P.norms[norm_base(P, br == 0 ? N_Q1 : N_Q2, bh) + ic] : 1.f;
+  const float ci = tau_coeff(pq, P.inv_d);
+  const float tau = (*P.beta) * ci;
+  const float pw = P.p;
+  float coef = 1.f;
+  if constexpr (BR == 2) coef = br == 0 ? 1.f : -clamp01(*P.lam);
+  const bool want_l = BR == 2 && br == 1;  // dlambda comes from branch 2 alone
+  const bf16* vb = base(B_V);
+  const int64_t sv = P.s[B_V][2];
+  const bf16* kb = base(kslot);
+  const int64_t sk = P.s[kslot][2];
+  const float* nk = nullptr;
+  if constexpr (NORM) nk = P.norms + norm_base(P, br == 0 ? N_K1 : N_K2, bh);
+  float bsum = 0.f, lsum = 0.f;
+  unsigned visited = 0, computed = 0;
+
+  f32x16 A[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) A[c] = f32x16{};
+
+  // word w of the block's row r, masked to the key tiles the row sees (uniform); every causal
+  // tile without a bitmask
+  const int klast_b = kt_last(min(W * jb + W - 1, nqt - 1), qoff, P.nkt);
+  auto row_word = [&](int r, int w) -> uint32_t {
+    if (!((needm >> r) & 1u)) return 0u;
+    const int kl = kt_last(W * jb + r, qoff, P.nkt);
+    if (w > (kl >> 5)) return 0u;
+    uint32_t x = P.occ ? (uint32_t)__builtin_amdgcn_readfirstlane((int)P.occ[(lrow0 + r) * P.occ_w + w]) : 0xffffffffu;
+    if (w == (kl >> 5) && (kl & 31) != 31) x &= (2u << (kl & 31)) - 1u;
+    return x;
+  };
+  int sw = -1;
+  uint32_t ub = 0u, sown = 0u;
+  auto next_tile = [&](uint32_t& own_out) -> int {
+    while (ub == 0u) {
+      if (++sw > (klast_b >> 5)) return -1;
+      uint32_t u = 0u, o = 0u;
+#pragma unroll
+      for (int r = 0; r < W; ++r) {
+        const uint32_t x = row_word(r, sw);
+        u |= x;
+        o = r == wv ? x : o;
+      }
+      ub = u;
+      sown = o;
+    }
+    const int kt = 32 * sw + __builtin_ctz(ub);
+    ub &= ub - 1u;
+    own_out = sown;
+    return kt;
+  };
+  BlkRows<D> kr, vr;
+  f32x4 nr = {};
+  auto issue = [&](int kt) {
+    kr.load(kb, sk, 32 * kt, Nk, wv);
+    vr.load(vb, sv, 32 * kt, Nk, wv);
+    if (NORM && wv == 0 && l < 8)
+      nr = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          rows_rsrc(nk + 32 * kt, (uint32_t)(min(32, Nk - 32 * kt) * 4)), 16u * (uint32_t)l, 0, 0));
+  };
+  uint32_t cown = 0u;
+  int kt = next_tile(cown);
+  if (kt >= 0) issue(kt);
+  int it = 0;
+  while (kt >= 0) {
+    bf16* kst = ring + (it & 1) * STAGE;
+    bf16* vst = kst + 32 * D;
+    float* nst = nring[it & 1];
+    kr.store(kst, wv);
+    vr.store(vst, wv);
+    if (NORM && wv == 0 && l < 8) *reinterpret_cast<f32x4*>(nst + 4 * l) = nr;
+    uint32_t nown = 0u;
+    const int kt2 = next_tile(nown);
+    if (kt2 >= 0) issue(kt2);  // in flight during this tile's work
+    lds_barrier();
+    ++it;
+    if ((cown >> (kt & 31)) & 1u) {
+      ++visited;
+      const int k0 = 32 * kt;
+      bool anyw = true;  // without a bitmask the counters count the tiles with a weight
+      f32x16 S = f32x16{}, Dp = f32x16{};
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        S = PolBF16::mma(tile_row_frag<D>(kst, t), Q[t], S);
+        Dp = PolBF16::mma(tile_row_frag<D>(vst, t), DO[t], Dp);
+      }
+      float rk[16];
+      if constexpr (NORM) crow_vals(nst, rk);
+      // exact x, branch-free; keys after the query's position, padding keys and rows past Nq
+      // set to -1 (only on the tiles that have any)
+      f32x16 X;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) X[r] = __builtin_fmaf(NORM ? S[r] * rk[r] : S[r], rq, -tau);
+      if (k0 + 31 > min(qoff + 32 * qt, Nk - 1) || rowpad) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + crow(r, g);
+          X[r] = qvalid && key <= pq && key < Nk ? X[r] : -1.f;
+        }
+      }
+      f32x16 E;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool pos = X[r] > 0.f;
+        const float ds = pos ? coef * dpow_p<PK>(X[r], pw) * Dp[r] : 0.f;
+        bsum += ds;
+        if (want_l) lsum = __builtin_fmaf(pos ? pow_p<PK>(X[r], pw) : 0.f, Dp[r], lsum);
+        E[r] = NORM ? ds * rk[r] : ds;
+      }
+      if (!P.occ) {
+        float xm = X[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) xm = fmaxf(xm, X[r]);
+        anyw = wave_ballot(xm > 0.f) != 0ull;
+      }
+      computed += anyw ? 1u : 0u;
+      const bf16x8 E0 = PolBF16::pack_c(E, 0), E1 = PolBF16::pack_c(E, 1);
+#pragma unroll
+      for (int c = 0; c < ND; ++c) {
+        A[c] = PolBF16::mma(tile_tr_frag<D>(kst, 0, c), E0, A[c]);
+        A[c] = PolBF16::mma(tile_tr_frag<D>(kst, 1, c), E1, A[c]);
+      }
+    }
+    cown = nown;  // the own row's word of the next tile
+    kt = kt2;
+  }
+  if (!need) return;
+  if (qvalid) {
+    GradRow<D> XR;  // the query row for the normalize backward
+    if constexpr (NORM) load_grad_row<D>(base(qslot) + (int64_t)ic * P.s[qslot][2], XR);
+    const int gslot = br == 0 ? B_DQ1 : B_DQ2;
+    bf16* grow = (bf16*)P.grad[br == 0 ? 0 : 2] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
+                 (int64_t)i * P.s[gslot][2];
+    store_grad_rows<D, NORM>(A, XR, grow, rq);
+  }
+  const float pb = wave_sum(-ci * bsum);
+  const float pl = wave_sum(-lsum);
+  if (l == 0) {
+    const int64_t lidx = lrow0 + wv;
+    P.ws[2 * lidx + 0] = pb;  // slot of (branch, head, query tile), whichever pass takes it
+    P.ws[2 * lidx + 1] = pl;
+    if (P.stats) {
+      atomicAdd(P.stats + 0, (unsigned long long)visited);
+      atomicAdd(P.stats + 1, (unsigned long long)computed);
+    }
+  }
+}
+
+// Key-major: kBwdBlk consecutive key tiles of one head (aligned: one bitmask word holds their
+// bits), streaming per branch the query tiles' Q and dO rows, query norms and tau values.  A key
+// tile takes this pass when a list of its column did not fit (the test bwd_dkv_pairs queues
+// by; it writes nothing for such a key tile), or always without lists.
+template <int D, int BR, int PK, bool NORM>
+__global__ void __launch_bounds__(64 * kBwdBlk) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1))) bwd_dkv_blk(BwdParams P) {
+  constexpr int W = kBwdBlk, NT = D / 16, ND = D / 32;
+  constexpr int STAGE = 2 * 32 * D;  // Q tile, dO tile
+  __shared__ __attribute__((aligned(16))) bf16 ring[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) float vring[2][2][32];  // [stage][query norms, tau values]
+  __shared__ __attribute__((aligned(16))) bf16 ktiles[W][32 * D];  // each wave's key rows (swizzled)
+  __shared__ uint32_t needs[W];
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int BH = P.B * P.H, nqt = P.nqt, nkt = P.nkt, Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
+  const int nkb = (nkt + W - 1) / W;
+  // longest blocks (first key tiles) of every head first
+  const int bid = blockIdx.x, jb = bid / BH, bh = bid % BH;
+  const int b = bh / P.H, h = bh % P.H;
+  const int kt0 = W * jb, kt = kt0 + wv;
+  const int qtf_b = qt_first(kt0, qoff);  // first query tile of the block
+  const uint32_t* counts = P.pairs ? P.pairs + pair_lists(BR, BH, nqt) * 4 * kPairCap : nullptr;
+  // this wave's key tile: does a list of its column not fit (every branch, query tiles from
+  // the first that sees it)?
+  {
+    bool nd = kt < nkt;
+    if (nd && counts) {
+      const int qtf = qt_first(kt, qoff);
+      bool ovf = false;
+      for (int q0c = qtf; q0c < nqt && !ovf; q0c += 64) {
+        bool o = false;
+#pragma unroll
+        for (int br = 0; br < BR; ++br) {
+          const int qtl = q0c + l;
+          const bool in = qtl < nqt;
+          const int64_t row = ((int64_t)br * BH + bh) * nqt + (in ? qtl : nqt - 1);
+          const uint32_t w = P.occ ? P.occ[row * P.occ_w + (kt >> 5)] : 0xffffffffu;
+          o = o || (in && ((w >> (kt & 31)) & 1u) && counts[row] > (uint32_t)kPairCap);
+        }
+        ovf = wave_ballot(o) != 0ull;
+      }
+      nd = ovf;
+    }
+    if (l == 0) needs[wv] = nd ? 1u : 0u;
+  }
+  __syncthreads();
+  uint32_t needm = 0u;
+#pragma unroll
+  for (int r = 0; r < W; ++r) needm |= needs[r] ? 1u << r : 0u;
+  needm = (uint32_t)__builtin_amdgcn_readfirstlane((int)needm);
+  if (!needm) return;
+  const bool need = (needm >> wv) & 1u;
+  const int j = 32 * kt + n32;
+  const bool kvalid = need && j < Nk;
+  const int jc = min(j, Nk - 1);
+  const int qtf_w = qt_first(kt, qoff);  // first query tile that sees this wave's key tile
+  auto base = [&](int slot) {
+    return (const bf16*)P.in[slot] + (int64_t)b * P.s[slot][0] + (int64_t)h * P.s[slot][1];
+  };
+
+  bf16x8 V[NT];
+  {
+    const bf16* r = base(B_V) + (int64_t)jc * P.s[B_V][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) V[t] = *reinterpret_cast<const bf16x8*>(r + 16 * t + 8 * g);
+  }
+  const float beta = *P.beta;
+  const float pw = P.p;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+  const bf16* dob = base(B_DO);
+  const int64_t sdo = P.s[B_DO][2];
+  f32x16 AV[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) AV[c] = f32x16{};
+  unsigned visited = 0, computed = 0;
+  int it = 0;  // ring position, continued across the branches
+  bf16* kti = ktiles[wv];
+
+#pragma unroll
+  for (int br = 0; br < BR; ++br) {
+    const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
+    const bf16* qb = base(qslot);
+    const int64_t sq = P.s[qslot][2];
+    const float rk = NORM ? P.norms[norm_base(P, br == 0 ? N_K1 : N_K2, bh) + jc] : 1.f;
+    const float* nq = nullptr;
+    if constexpr (NORM) nq = P.norms + norm_base(P, br == 0 ? N_Q1 : N_Q2, bh);
+    const float coef = br == 0 ? 1.f : -lam;
+    // the wave's key rows (swizzled tile; rows past Nk read as zeros), read as score operands
+    {
+      BlkRows<D> kr4[kBwdBlk];
+#pragma unroll
+      for (int s4 = 0; s4 < kBwdBlk; ++s4) kr4[s4].load(base(kslot), P.s[kslot][2], 32 * min(kt, nkt - 1), Nk, s4);
+#pragma unroll
+      for (int s4 = 0; s4 < kBwdBlk; ++s4) kr4[s4].store(kti, s4);
+    }
+    f32x16 AK[ND];
+#pragma unroll
+    for (int c = 0; c < ND; ++c) AK[c] = f32x16{};
+    const int64_t row0 = ((int64_t)br * BH + bh) * nqt;  // bitmask / list row of query tile 0
+
+    // union walk over query tiles qtf_b .. nqt-1, 64 per round: lane q tests query tile q0c + q
+    int q0c = qtf_b - 64;
+    uint64_t um = 0ull, om = 0ull;
+    auto next_tile = [&](bool& own_out) -> int {
+      while (um == 0ull) {
+        q0c += 64;
+        if (q0c >= nqt) return -1;
+        const int qtl = q0c + l;
+        const bool in = qtl < nqt;
+        const uint32_t w = !in ? 0u : P.occ ? P.occ[(row0 + qtl) * P.occ_w + (kt0 >> 5)] : 0xffffffffu;
+        uint32_t bits = (w >> (kt0 & 31)) & 0xfu & needm;
+        // causal: key tile kt0 + r is seen from query tile qt_first(kt0 + r) on
+#pragma unroll
+        for (int r = 0; r < W; ++r)
+          if (qtl < qt_first(kt0 + r, qoff)) bits &= ~(1u << r);
+        um = wave_ballot(bits != 0u);
+        om = wave_ballot((bits >> wv) & 1u);
+      }
+      const int q = __builtin_ctzll(um);
+      um &= um - 1ull;
+      own_out = (om >> q) & 1ull;
+      return q0c + q;
+    };
+    BlkRows<D> qr, dr;
+    float vrq = 1.f, vtq = 0.f;
+    auto issue = [&](int qt) {
+      qr.load(qb, sq, 32 * qt, Nq, wv);
+      dr.load(dob, sdo, 32 * qt, Nq, wv);
+      if (wv == 0 && l < 32) {
+        const int qi = min(32 * qt + l, Nq - 1);
+        vrq = NORM ? nq[qi] : 1.f;
+        vtq = beta * tau_coeff(qoff + 32 * qt + l, P.inv_d);
+      }
+    };
+    bool cown = false;
+    int qt = next_tile(cown);
+    if (qt >= 0) issue(qt);
+    while (qt >= 0) {
+      bf16* qst = ring + (it & 1) * STAGE;
+      bf16* dst = qst + 32 * D;
+      float* rqs = vring[it & 1][0];
+      float* tqs = vring[it & 1][1];
+      qr.store(qst, wv);
+      dr.store(dst, wv);
+      if (wv == 0 && l < 32) {
+        rqs[l] = vrq;
+        tqs[l] = vtq;
+      }
+      bool nown = false;
+      const int qt2 = next_tile(nown);
+      if (qt2 >= 0) issue(qt2);  // in flight during this tile's work
+      lds_barrier();
+      ++it;
+      if (cown) {
+        ++visited;
+        const int q0 = 32 * qt;
+        f32x16 S = f32x16{}, Dp = f32x16{};
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          S = PolBF16::mma(tile_row_frag<D>(qst, t), tile_row_frag<D>(kti, t), S);
+          Dp = PolBF16::mma(tile_row_frag<D>(dst, t), V[t], Dp);
+        }
+        float rq[16], tq[16];
+        if constexpr (NORM) crow_vals(rqs, rq);
+        crow_vals(tqs, tq);
+        f32x16 X;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) X[r] = __builtin_fmaf(NORM ? S[r] * rk : S[r], NORM ? rq[r] : 1.f, -tq[r]);
+        // masks only on the tiles that need them: queries before the key (the diagonal), rows
+        // past Nq, keys past Nk
+        if (32 * kt + 31 > qoff + q0 || q0 + 31 >= Nq || 32 * kt + 31 >= Nk) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int qi = q0 + crow(r, g);
+            X[r] = kvalid && qi < Nq && j <= qoff + qi ? X[r] : -1.f;
+          }
+        }
+        f32x16 EV, EK;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const bool pos = X[r] > 0.f;
+          EV[r] = pos ? coef * pow_p<PK>(X[r], pw) : 0.f;
+          const float ds = pos ? coef * dpow_p<PK>(X[r], pw) * Dp[r] : 0.f;
+          EK[r] = NORM ? ds * rq[r] : ds;
+        }
+        bool anyw = true;  // without a bitmask the counters count the tiles with a weight
+        if (!P.occ) {
+          float xm = X[0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r) xm = fmaxf(xm, X[r]);
+          anyw = wave_ballot(xm > 0.f) != 0ull;
+        }
+        computed += anyw ? 1u : 0u;
+        const bf16x8 V0 = PolBF16::pack_c(EV, 0), V1 = PolBF16::pack_c(EV, 1);
+        const bf16x8 K0 = PolBF16::pack_c(EK, 0), K1 = PolBF16::pack_c(EK, 1);
+#pragma unroll
+        for (int c = 0; c < ND; ++c) {
+          AV[c] = PolBF16::mma(tile_tr_frag<D>(dst, 0, c), V0, AV[c]);
+          AV[c] = PolBF16::mma(tile_tr_frag<D>(dst, 1, c), V1, AV[c]);
+          AK[c] = PolBF16::mma(tile_tr_frag<D>(qst, 0, c), K0, AK[c]);
+          AK[c] = PolBF16::mma(tile_tr_frag<D>(qst, 1, c), K1, AK[c]);
+        }
+      }
+      cown = nown;
+      qt = qt2;
+    }
+    if (kvalid) {
+      GradRow<D> XR;  // the key row for the normalize backward
+      if constexpr (NORM) load_grad_row<D>(base(kslot) + (int64_t)jc * P.s[kslot][2], XR);
+      const int gslot = br == 0 ? B_DK1 : B_DK2;
+      bf16* grow = (bf16*)P.grad[br == 0 ? 1 : 3] + (int64_t)b * P.s[gslot][0] + (int64_t)h * P.s[gslot][1] +
+                   (int64_t)j * P.s[gslot][2];
+      store_grad_rows<D, NORM>(AK, XR, grow, rk);
+    }
+    lds_barrier();  // every wave is done with its key tile before the next branch's rows
+  }
+  if (kvalid) {
+    bf16* vrow = (bf16*)P.grad[4] + (int64_t)b * P.s[B_DV][0] + (int64_t)h * P.s[B_DV][1] + (int64_t)j * P.s[B_DV][2];
+    store_grad_rows<D, false>(AV, GradRow<D>{}, vrow, 1.f);
+  }
+  if (P.stats && l == 0 && need) {
+    atomicAdd(P.stats + 0, (unsigned long long)visited);
+    atomicAdd(P.stats + 1, (unsigned long long)computed);
+  }
+}
+
 // ------------------------------------------------------------------ dispatch
 template <int D, int BR, int PK, bool NORM>
 static int launch_t(const BwdParams& p, void* stream) {
   const int64_t qitems = (int64_t)BR * p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
+  if constexpr (!NORM) {
+    // The forward ran its block tile pass (every query tile): the pair passes take the lists
+    // that fit, then the block tile passes everything else (no key-tile queue), the sum.
+    BwdParams q = p;
+    q.dkvq = nullptr;
+    if (q.pairs) {
+      hipLaunchKernelGGL((bwd_dq_pairs<D, BR, PK, NORM>), dim3((unsigned)qitems), dim3(64), 0, s, q);
+      launched(s, "bwd_dq_pairs");
+      hipLaunchKernelGGL((bwd_dkv_pairs<D, BR, PK, NORM>), dim3((unsigned)kitems), dim3(64), 0, s, q);
+      launched(s, "bwd_dkv_pairs");
+    }
+    const int BH = q.B * q.H;
+    hipLaunchKernelGGL((bwd_dq_blk<D, BR, PK, NORM>), dim3((unsigned)(BR * BH * ((q.nqt + kBwdBlk - 1) / kBwdBlk))),
+                       dim3(64 * kBwdBlk), 0, s, q);
+    launched(s, "bwd_dq_blk");
+    hipLaunchKernelGGL((bwd_dkv_blk<D, BR, PK, NORM>), dim3((unsigned)(BH * ((q.nkt + kBwdBlk - 1) / kBwdBlk))),
+                       dim3(64 * kBwdBlk), 0, s, q);
+    launched(s, "bwd_dkv_blk");
+    const int e = (int)hipGetLastError();
+    return e ? e : launch_bwd_finish(q, BR, qitems, stream);
+  }
   if (p.pairs && p.dkvq) {  // the pair passes, both tile passes in one launch, the sum
     hipLaunchKernelGGL((bwd_dq_pairs<D, BR, PK, NORM>), dim3((unsigned)qitems), dim3(64), 0, s, p);
     launched(s, "bwd_dq_pairs");
