@@ -398,7 +398,7 @@ __global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
     float kh[16], m = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) kh[j] = x[u][j] * rk[u];
-    if (!__builtin_isfinite(ss[u])) {
+    if (wave_ballot(!__builtin_isfinite(ss[u])) != 0ull) {  // a branch only where a row has any
 #pragma unroll
       for (int j = 0; j < 16; ++j) kh[j] = __builtin_isfinite(kh[j]) ? kh[j] : 0.f;
     }
