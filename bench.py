@@ -39,11 +39,12 @@ SCREEN_UNITS = 2.0                           # fwd_screen: Q1 K1^T and Q2 K2^T o
 # (with normalize, fwd_screen runs v_mfma_i32_32x32x32_i8: 2U int8 operations, priced at the int8 peak)
 # HBM bytes per forward-only launch of the dominant kernel (fwd_screen) at SHAPE, from rocprofv3
 # --pmc FETCH_SIZE and --pmc WRITE_SIZE runs of this script, each scaled by what the same counter
-# reads for --copy-probe (a 2^30-byte device copy): FETCH_SIZE x 2.000, WRITE_SIZE x 1.000 (341.0 MB
-# read + 47.9 MB written).  The command lines and the per-kernel figures are in
+# reads for --copy-probe (a 2^30-byte device copy): FETCH_SIZE x 2.000, WRITE_SIZE x 1.000 (329.0 MB
+# read + 49.9 MB written).  The command lines and the per-kernel figures are in
 # profiles/tda_c2_bf16_counters.md; re-measure after kernel changes.
-SCREEN_HBM_BYTES = 3.889e8
+SCREEN_HBM_BYTES = 3.789e8
 SCREEN_KERNEL = "fwd_screen"
+SETTLE_S = 0.3  # seconds of untimed steps before the first timed region (see settle)
 
 
 def units(shape, u):
@@ -157,6 +158,20 @@ def time_calls(stream, fn, steps, warmup):
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def settle(fn, seconds):
+    """Run fn() back to back for `seconds` of wall time, untimed, then synchronise.  The GPU's
+    clocks ramp up over the first tens of milliseconds of work after an idle period: measured on
+    the box, 20 steps right after 0.5 s idle took 381 us per step, the same 20 steps once the GPU
+    had been busy 333-337 us, and 100 steps after 50 warm-ups 330 us.  Every timed region of this
+    script starts on a busy GPU, so it measures the kernels at their steady clock."""
+    import torch
+
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        fn()
+    torch.cuda.synchronize()
 
 
 def time_launches(fn, calls, warmup):
@@ -387,6 +402,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-side", action="store_true", help="skip the configs[1] / configs[4] / fp32 report figures")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--dense-only", action="store_true",
+                    help="only the dense-regime figures (side_configs.dense), for a kernel trace of that regime")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy 3 times (calibrates HBM byte counters)")
     args = ap.parse_args(argv)
@@ -411,6 +428,9 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_read": 1 << 30, "copy_probe_bytes_written": 1 << 30, "dispatches": 3}))
         return 0
+    if args.dense_only:
+        print(json.dumps({"dense": dense_figures(dev, torch.cuda.current_stream(dev), args.steps)}))
+        return 0
     g = torch.Generator("cpu").manual_seed(2)
     xs = [torch.randn(SHAPE, generator=g).to(torch.bfloat16).to(dev) for _ in range(5)]
     do = torch.randn(SHAPE, generator=torch.Generator("cpu").manual_seed(3)).to(torch.bfloat16).to(dev)
@@ -419,14 +439,7 @@ def main(argv=None) -> int:
     lam = torch.tensor(LAM, device=dev)
     stream = torch.cuda.current_stream(dev)
 
-    # ---- forward only (key_prep, fwd_screen, fwd_pv_cand, fwd_pv per call), events around the calls
     fwd = lambda: ops.forward(q1, k1, q2, k2, v, beta, lam, POWER, True, 2)  # noqa: E731
-    with torch.no_grad():
-        fwd_ms = time_calls(stream, fwd, args.steps, args.warmup)
-        # ---- each launch of the forward on its own (events between the launches)
-        fwd_launch_us, fwd_launch_total = time_launches(fwd, args.steps, 2)
-
-    # ---- forward + backward through the public API (the step)
     leaves = [x.clone().requires_grad_(True) for x in xs]
     bt = beta.clone().requires_grad_(True)
     lt = lam.clone().requires_grad_(True)
@@ -437,6 +450,15 @@ def main(argv=None) -> int:
         out = tda_amd.differential_threshold_rela_triton(*leaves, bt, lt, relu_power=POWER, normalize=True)
         out.backward(do)
 
+    # the GPU busy before the first timed region (see settle); the timed regions then follow
+    # one another with no idle time, and the per-launch timings (a synchronisation per call) come
+    # after them
+    settle(step, SETTLE_S)
+    # ---- forward only (key_prep, fwd_screen, fwd_pv_cand, fwd_pv per call), events around the calls
+    with torch.no_grad():
+        fwd_ms = time_calls(stream, fwd, args.steps, args.warmup)
+
+    # ---- forward + backward through the public API (the step)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -449,6 +471,10 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     step_ms = s0.elapsed_time(s1) / args.steps
+
+    # ---- each launch of the forward on its own (events between the launches)
+    with torch.no_grad():
+        fwd_launch_us, fwd_launch_total = time_launches(fwd, args.steps, 2)
 
     # ---- each launch of the backward on its own: the call autograd makes in the step, on this
     # thread (gradient buffers cleared by the forward, only the non-zero rows stored: repeating
