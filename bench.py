@@ -426,7 +426,10 @@ def main(argv=None) -> int:
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes_read": 1 << 30, "copy_probe_bytes_written": 1 << 30, "dispatches": 3}))
+        # and its rate: the HBM rate a kernel that reads and writes equal amounts can reach here
+        ms = time_calls(torch.cuda.current_stream(dev), lambda: dst.copy_(src), 20, 3)
+        print(json.dumps({"copy_probe_bytes_read": 1 << 30, "copy_probe_bytes_written": 1 << 30, "dispatches": 26,
+                          "copy_gbs_read_plus_written": 2.0 * (1 << 30) / (ms * 1e-3) / 1e9}))
         return 0
     if args.dense_only:
         print(json.dumps({"dense": dense_figures(dev, torch.cuda.current_stream(dev), args.steps)}))
