@@ -160,6 +160,13 @@ def time_calls(stream, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+def settled_calls(stream, fn, steps, warmup, seconds=0.05):
+    """time_calls after `seconds` of untimed calls (the side figures follow per-launch timings,
+    which synchronise per call and leave the GPU idle between calls)."""
+    settle(fn, seconds)
+    return time_calls(stream, fn, steps, warmup)
+
+
 def settle(fn, seconds):
     """Run fn() back to back for `seconds` of wall time, untimed, then synchronise.  The GPU's
     clocks ramp up over the first tens of milliseconds of work after an idle period: measured on
@@ -222,7 +229,7 @@ def side_configs(steps: int, warmup: int):
 
     def timed(fn, n=steps, w=warmup):
         with torch.no_grad():
-            return time_calls(stream, fn, n, w)
+            return settled_calls(stream, fn, n, w)
 
     def per_launch(fn, n=steps):
         with torch.no_grad():
@@ -306,7 +313,7 @@ def dense_figures(dev, stream, steps):
         beta = torch.tensor(1.0, device=dev)
         fwd = lambda: ops.forward(q, k, None, None, v, beta, None, 2.0, False, 1)  # noqa: E731
         with torch.no_grad():
-            ms_f = time_calls(stream, fwd, steps, 2)
+            ms_f = settled_calls(stream, fwd, steps, 2)
             lu, _ = time_launches(fwd, max(3, steps // 2), 1)
         st = tile_stats(lambda s: ops.forward(q, k, None, None, v, beta, None, 2.0, False, 1, stats=s), dev)
         leaves = [x.clone().requires_grad_(True) for x in (q, k, v)]
@@ -316,6 +323,7 @@ def dense_figures(dev, stream, steps):
                 t.grad = None
             threshold_rela_triton(*leaves, beta, relu_power=2.0).backward(do)
 
+        settle(step, 0.05)
         for _ in range(2):
             step()
         torch.cuda.synchronize()
@@ -362,7 +370,7 @@ def fp32_figures(dev, stream):
     q, k, v = (torch.randn(shp, generator=g).to(dev) for _ in range(3))
     beta = torch.tensor(1.0, device=dev)
     with torch.no_grad():
-        ms = time_calls(stream, lambda: ops.forward(q, k, None, None, v, beta, None, 2.0, False, 1), 50, 10)
+        ms = settled_calls(stream, lambda: ops.forward(q, k, None, None, v, beta, None, 2.0, False, 1), 50, 10)
     out["readme_tra"] = {"workload": "TRA fwd fp32 (1,8,128,64), beta=1, p=2 (README usage)", "ms": ms,
                          "tflops": units(shp, 2.0) / (ms * 1e-3) / 1e12,
                          "pct_f32_peak": 100.0 * units(shp, 2.0) / (ms * 1e-3) / 1e12 / PEAK_F32_TFLOPS}
@@ -373,7 +381,7 @@ def fp32_figures(dev, stream):
     beta, lam = torch.tensor(BETA, device=dev), torch.tensor(LAM, device=dev)
     fwd = lambda: ops.forward(q1, k1, q2, k2, v, beta, lam, POWER, True, 2)  # noqa: E731
     with torch.no_grad():
-        ms_f = time_calls(stream, fwd, 10, 2)
+        ms_f = settled_calls(stream, fwd, 10, 2)
     # the backward as a training step runs it: on the side outputs and pair lists of its forward
     norms, occ = ops.side_buffers(SHAPE, 2, True, dev)
     pairs = ops.pair_buffer(SHAPE, 2, dev)
@@ -381,7 +389,7 @@ def fp32_figures(dev, stream):
         ops.forward(q1, k1, q2, k2, v, beta, lam, POWER, True, 2, norms, occ, pairs=pairs)
         bwd = lambda: ops.backward(q1, k1, q2, k2, v, do, beta, lam, POWER, True, 2, norms, occ,  # noqa: E731
                                    pairs=pairs)
-        ms_b = time_calls(stream, bwd, 10, 2)
+        ms_b = settled_calls(stream, bwd, 10, 2)
         bwd_launch_us, _ = time_launches(bwd, 5, 1)
     out["c2_tda"] = {"workload": "TDA fp32 (4,16,4096,128) seed 2, beta=1, lambda=0.5, p=2, normalize",
                      "fwd_ms": ms_f, "fwd_tflops": units(SHAPE, 3.0) / (ms_f * 1e-3) / 1e12,
