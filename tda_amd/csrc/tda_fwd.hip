@@ -294,6 +294,180 @@ __device__ __forceinline__ void fwd_wave_tile(const FwdParams& P, int qt, int bh
   }
 }
 
+// ------------------------------------------------------------------ fwd_wave_blk
+// The fp32 pass without normalisation (every causal tile scored) over blocks of four
+// consecutive query tiles of one head, one wave each, as fwd_pv_blk does for bf16: the waves walk
+// the block's causal key tiles in step and share each tile's key rows (every branch) and V rows,
+// which the workgroup loads once (each wave a quarter of the rows, one tile ahead into
+// registers) into LDS; two barriers per tile (the tile is rewritten once every wave is done with
+// it).  A wave scores only the tiles its own query tile sees, with fwd_wave's arithmetic: the
+// key rows' fragments in the load_rows order (lane half g: elements g D/2 .. of row n), V^T one
+// key per lane half and step, the same test, weights, bitmask, counters and output.
+template <int D, int BR, int PK>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1)))
+fwd_wave_blk(FwdParams P) {
+  using Pol = PolF32;
+  constexpr int W = 4, NT = D / 2, NS = 16, ND = D / 32;
+  constexpr int KS = D + 4;          // key tile row stride (floats)
+  constexpr int VS = D + 8;          // V tile row stride: rows 4 apart 32 banks apart
+  constexpr int CPR = D / 4;         // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;      // rows per load instruction
+  constexpr int LPW = 32 / RPI / W;  // load instructions per wave and matrix
+  static_assert(LPW >= 1 && LPW * RPI * W == 32, "tile rows split evenly over the waves");
+  __shared__ __attribute__((aligned(16))) float klds[BR][32 * KS];
+  __shared__ __attribute__((aligned(16))) float vlds[32 * VS];
+
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
+  const int nqb = (nqt + W - 1) / W;
+  // longest blocks (last query tiles) of every head first
+  const int bid = blockIdx.x, jb = nqb - 1 - bid / BH, bh = bid % BH;
+  const int b = bh / P.H, h = bh % P.H;
+  const int qt = W * jb + wv;
+  const bool act = qt < nqt;  // wave-uniform: waves past the last query tile only load
+  const int i = 32 * qt + n32;
+  const bool qvalid = act && i < Nq;
+  const int pq = qoff + i;
+  const int ktl = act ? kt_last(qt, qoff, P.nkt) : -1;                       // this wave's last key tile
+  const int ktl_b = kt_last(min(W * jb + W - 1, nqt - 1), qoff, P.nkt);  // the block's
+
+  const TRef<const float> qr[2] = {{(const float*)P.in[F_Q1], P.s[F_Q1][0], P.s[F_Q1][1], P.s[F_Q1][2]},
+                                   {(const float*)P.in[F_Q2], P.s[F_Q2][0], P.s[F_Q2][1], P.s[F_Q2][2]}};
+  const TRef<const float> kr[2] = {{(const float*)P.in[F_K1], P.s[F_K1][0], P.s[F_K1][1], P.s[F_K1][2]},
+                                   {(const float*)P.in[F_K2], P.s[F_K2][0], P.s[F_K2][1], P.s[F_K2][2]}};
+  const TRef<const float> vv{(const float*)P.in[F_V], P.s[F_V][0], P.s[F_V][1], P.s[F_V][2]};
+  const TRef<float> out{(float*)P.out, P.s[F_OUT][0], P.s[F_OUT][1], P.s[F_OUT][2]};
+
+  float Q[BR][NT];
+#pragma unroll
+  for (int br = 0; br < BR; ++br) Pol::template load_rows<NT>(qvalid ? qr[br].row(b, h, i) : nullptr, g, Q[br]);
+  const float pw = P.p;
+  const float tau = (*P.beta) * tau_coeff(pq, P.inv_d);
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+
+  // this wave's rows of a tile: RPI (LPW wv + u) + l / CPR, chunk l % CPR (rows past Nk: Nk - 1)
+  f32x4 kreg[BR][LPW], vreg[LPW];
+  auto issue = [&](int kt) {
+#pragma unroll
+    for (int u = 0; u < LPW; ++u) {
+      const int r = min(32 * kt + RPI * (LPW * wv + u) + l / CPR, Nk - 1);
+#pragma unroll
+      for (int br = 0; br < BR; ++br) kreg[br][u] = *reinterpret_cast<const f32x4*>(kr[br].row(b, h, r) + 4 * (l % CPR));
+      vreg[u] = *reinterpret_cast<const f32x4*>(vv.row(b, h, r) + 4 * (l % CPR));
+    }
+  };
+
+  f32x16 O[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) O[c] = f32x16{};
+  uint32_t* occrow = P.occ && act ? P.occ + ((int64_t)bh * nqt + qt) * P.occ_w : nullptr;
+  const int64_t occ_br = (int64_t)BH * nqt * P.occ_w;  // distance between the branch planes
+  uint32_t word = 0, word2 = 0;
+  unsigned visited = 0, computed = 0;
+
+  issue(0);
+  for (int kt = 0; kt <= ktl_b; ++kt) {
+    lds_barrier();  // every wave is done with the previous tile
+#pragma unroll
+    for (int u = 0; u < LPW; ++u) {
+      const int r = RPI * (LPW * wv + u) + l / CPR;
+#pragma unroll
+      for (int br = 0; br < BR; ++br) *reinterpret_cast<f32x4*>(klds[br] + r * KS + 4 * (l % CPR)) = kreg[br][u];
+      *reinterpret_cast<f32x4*>(vlds + r * VS + 4 * (l % CPR)) = vreg[u];
+    }
+    if (kt < ktl_b) issue(kt + 1);  // in flight during this tile's products
+    lds_barrier();                  // tile kt in LDS
+    if (kt > ktl) continue;         // (uniform) not seen by this wave's query tile
+    const int k0 = 32 * kt;
+    f32x16 S[BR];
+#pragma unroll
+    for (int br = 0; br < BR; ++br) {
+      S[br] = f32x16{};
+      const float* kp = klds[br] + n32 * KS + g * NT;
+#pragma unroll
+      for (int m = 0; m < NT / 4; ++m) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(kp + 4 * m);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[br] = Pol::mma(v[e], Q[br][4 * m + e], S[br]);
+      }
+    }
+    // threshold test: the tile max of the valid scores decides "any x > 0" exactly
+    bool any[2] = {false, false};
+#pragma unroll
+    for (int br = 0; br < BR; ++br) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + crow(r, g);
+        const bool valid = qvalid && key <= pq && key < Nk;
+        m = fmaxf(m, valid ? S[br][r] : -INFINITY);
+      }
+      any[br] = wave_ballot(m - tau > 0.f) != 0ull;
+    }
+    visited += BR;
+    computed += (any[0] ? 1 : 0) + (any[1] ? 1 : 0);
+    if (any[0]) word |= 1u << (kt & 31);
+    if (any[1]) word2 |= 1u << (kt & 31);
+    // the query tile's pairs are in no list: the column bucket of the key tile is incomplete
+    if (P.colcnt && (any[0] || any[1]) && l == 0) atomicOr(P.colcnt + (int64_t)bh * P.nkt + kt, kColTaint);
+    if (any[0] || any[1]) {
+      f32x16 C;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + crow(r, g);
+        const bool valid = qvalid && key <= pq && key < Nk;
+        const float x1 = __builtin_fmaf(S[0][r], 1.f, -tau);
+        float a = (valid && any[0] && x1 > 0.f) ? pow_p<PK>(x1, pw) : 0.f;
+        if constexpr (BR == 2) {
+          const float x2 = __builtin_fmaf(S[1][r], 1.f, -tau);
+          const float a2 = (valid && any[1] && x2 > 0.f) ? pow_p<PK>(x2, pw) : 0.f;
+          a = __builtin_fmaf(-lam, a2, a);
+        }
+        C[r] = a;
+      }
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        const float* vp = vlds + crow(st, g) * VS + n32;
+#pragma unroll
+        for (int c = 0; c < ND; ++c) O[c] = Pol::mma(vp[32 * c], C[st], O[c]);
+      }
+    }
+    if (occrow && (((kt & 31) == 31) || kt == ktl)) {
+      if (l == 0) {
+        occrow[kt >> 5] = word;
+        if constexpr (BR == 2) occrow[occ_br + (kt >> 5)] = word2;
+      }
+      word = word2 = 0;
+    }
+  }
+  if (!act) return;
+  if (occrow && l == 0) {
+    for (int w = (ktl >> 5) + 1; w < P.occ_w; ++w) {
+      occrow[w] = 0u;
+      if constexpr (BR == 2) occrow[occ_br + w] = 0u;
+    }
+  }
+  if (P.pairs && l == 0) {  // this pass writes no pair list: the backward walks the tiles
+#pragma unroll
+    for (int br = 0; br < BR; ++br)
+      P.pairs[pair_lists(BR, BH, nqt) * 4 * kPairCap + ((int64_t)br * BH + bh) * nqt + qt] = kPairOverflow;
+  }
+  if (qvalid) {
+    float* orow = out.row(b, h, i);
+#pragma unroll
+    for (int c = 0; c < ND; ++c)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        store4(orow + 32 * c + 8 * u + 4 * g, O[c][4 * u], O[c][4 * u + 1], O[c][4 * u + 2], O[c][4 * u + 3]);
+  }
+  if (P.stats && l == 0) {
+    atomicAdd(P.stats + 0, (unsigned long long)visited);
+    atomicAdd(P.stats + 1, (unsigned long long)computed);
+  }
+}
+
 // ------------------------------------------------------------------ fwd_cand_f32
 // The fp32 exact pass over the screen's candidate keys (normalised, more than one query tile):
 // one workgroup per query tile whose candidate lists (every branch) fit, one wave per branch.
@@ -533,6 +707,9 @@ static int launch_fwd_t(const FwdParams& p, const KernelKey& k, void* stream) {
     launched(stream, "fwd_cand_f32");
     const unsigned qgrid = (unsigned)(((items < 2048 ? items : 2048) + 3) / 4);
     hipLaunchKernelGGL((fwd_wave<Pol, D, BR, PK, NORM, NORM, NORM>), dim3(qgrid), dim3(256), 0, (hipStream_t)stream, p);
+  } else if (!NORM && p.nqt > 1) {  // blocks of query tiles sharing their key and V tiles
+    const unsigned blocks = (unsigned)(p.B * p.H * ((p.nqt + 3) / 4));
+    hipLaunchKernelGGL((fwd_wave_blk<D, BR, PK>), dim3(blocks), dim3(256), 0, (hipStream_t)stream, p);
   } else {
     hipLaunchKernelGGL((fwd_wave<Pol, D, BR, PK, NORM>), dim3(grid), dim3(256), 0, (hipStream_t)stream, p);
   }
