@@ -513,6 +513,352 @@ __device__ __forceinline__ void bwd_dkv_item(const BwdParams& P, int64_t item, i
   }
 }
 
+// ------------------------------------------------------------------ block tile passes (fp32)
+// The fp32 backward without normalisation (the forward ran fwd_wave_blk: every query tile, the
+// bitmask rows exact, no pair lists): four consecutive tiles of one head per workgroup, one
+// wave each, walking the union of their bitmask tiles in step, as the bf16 block passes do.
+// Each streamed tile's rows are loaded once per workgroup (each wave a quarter of the rows, one
+// tile ahead into registers) into LDS, two barriers per tile.  The score and dp products take
+// both operands in the load_rows element order (lane half g: elements g D/2 .., step t), so
+// every score is bitwise the forward's; the contractions over a tile's 32 rows read the rows
+// as A^T fragments (row crow(st, g), one column per lane), as fwd_wave_blk's A.V does.
+constexpr int kF32Blk = 4;
+
+// This wave's share of a 32-row fp32 tile: rows RPI (LPW wv + u) + l / CPR, 16-byte chunk
+// l % CPR; rows past n read row n - 1 (their products are masked).
+template <int D>
+struct F32Rows {
+  static constexpr int CPR = D / 4, RPI = 64 / CPR, LPW = 32 / RPI / kF32Blk;
+  static_assert(LPW >= 1 && LPW * RPI * kF32Blk == 32, "tile rows split evenly over the waves");
+  f32x4 v[LPW];
+  __device__ __forceinline__ void load(const TRef<const float>& x, int b, int h, int r0, int n, int wv) {
+    const int l = lane_id();
+#pragma unroll
+    for (int u = 0; u < LPW; ++u) {
+      const int r = min(r0 + RPI * (LPW * wv + u) + l / CPR, n - 1);
+      v[u] = *reinterpret_cast<const f32x4*>(x.row(b, h, r) + 4 * (l % CPR));
+    }
+  }
+  template <int KS>
+  __device__ __forceinline__ void store(float* tile, int wv) const {
+    const int l = lane_id();
+#pragma unroll
+    for (int u = 0; u < LPW; ++u)
+      *reinterpret_cast<f32x4*>(tile + (RPI * (LPW * wv + u) + l / CPR) * KS + 4 * (l % CPR)) = v[u];
+  }
+};
+
+// S^T-layout product of a 32-row LDS tile (A operand: lane (m, g) row m, elements g D/2 + t)
+// with a lane's register fragments (B operand, load_rows order): lane n, value r = row crow(r, g).
+template <int D, int KS>
+__device__ __forceinline__ f32x16 lds_rows_mma(const float* tile, const float (&bf)[D / 2], f32x16 acc) {
+  constexpr int NT = D / 2;
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const float* p = tile + n32 * KS + g * NT;
+#pragma unroll
+  for (int m = 0; m < NT / 4; ++m) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * m);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = PolF32::mma(v[e], bf[4 * m + e], acc);
+  }
+  return acc;
+}
+// acc[c] += tile^T E over the tile's 32 rows (lane n, value r of block c = column 32 c + crow(r, g)):
+// step st takes rows crow(st, 0) and crow(st, 1), E's values st of lane n.
+template <int D, int KS>
+__device__ __forceinline__ void lds_tr_mma(const float* tile, const f32x16& E, f32x16 (&acc)[D / 32]) {
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+#pragma unroll
+  for (int st = 0; st < 16; ++st) {
+    const float* p = tile + crow(st, g) * KS + n32;
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) acc[c] = PolF32::mma(p[32 * c], E[st], acc[c]);
+  }
+}
+
+// Query-major: four query tiles of one (branch, head), streaming K and V.  dq rows, the
+// (branch, head, query tile) dbeta / dlambda partials and the counters.
+template <int D, int BR, int PK>
+__global__ void __launch_bounds__(64 * kF32Blk) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1)))
+bwd_dq_blk_f32(BwdParams P) {
+  constexpr int W = kF32Blk, NT = D / 2, ND = D / 32;
+  constexpr int KS = D + 4;  // row stride: the row-fragment reads (lane n32 at row n32) spread over the banks
+  __shared__ __attribute__((aligned(16))) float klds[32 * KS];
+  __shared__ __attribute__((aligned(16))) float vlds[32 * KS];
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int BH = P.B * P.H, nqt = P.nqt, Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
+  const int nqb = (nqt + W - 1) / W;
+  // longest blocks (last query tiles) of every (head, branch) first, the branches adjacent
+  const int bid = blockIdx.x, jb = nqb - 1 - bid / (BR * BH), rem = bid % (BR * BH);
+  const int br = BR == 2 ? rem & 1 : 0, bh = BR == 2 ? rem >> 1 : rem;
+  const int b = bh / P.H, h = bh % P.H;
+  const int qt = W * jb + wv;
+  const bool act = qt < nqt;  // wave-uniform: waves past the last query tile only load
+  const int i = 32 * qt + n32;
+  const bool qvalid = act && i < Nq;
+  const int pq = qoff + i;
+  const bool edge_rows = !act || 32 * qt + 31 >= Nq;
+  const int64_t lrow0 = ((int64_t)br * BH + bh) * nqt + W * jb;  // bitmask row of the block's first tile
+  const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
+  const TRef<const float> qx{(const float*)P.in[br == 0 ? 0 : 2], P.s[qslot][0], P.s[qslot][1], P.s[qslot][2]};
+  const TRef<const float> kx{(const float*)P.in[br == 0 ? 1 : 3], P.s[kslot][0], P.s[kslot][1], P.s[kslot][2]};
+  const TRef<const float> vx{(const float*)P.in[4], P.s[B_V][0], P.s[B_V][1], P.s[B_V][2]};
+  const TRef<const float> dox{(const float*)P.in[5], P.s[B_DO][0], P.s[B_DO][1], P.s[B_DO][2]};
+
+  float Q[NT], DO[NT];
+  PolF32::load_rows<NT>(qvalid ? qx.row(b, h, i) : nullptr, g, Q);
+  PolF32::load_rows<NT>(qvalid ? dox.row(b, h, i) : nullptr, g, DO);
+  const float ci = tau_coeff(pq, P.inv_d);
+  const float tau = (*P.beta) * ci;
+  const float pw = P.p;
+  float coef = 1.f;
+  if constexpr (BR == 2) coef = br == 0 ? 1.f : -clamp01(*P.lam);
+  const bool want_l = BR == 2 && br == 1;  // dlambda comes from branch 2 alone
+  float bsum = 0.f, lsum = 0.f;
+  unsigned visited = 0, computed = 0;
+  f32x16 A[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) A[c] = f32x16{};
+
+  // word w of the block's row r, masked to the key tiles the row sees (uniform); every causal
+  // tile without a bitmask
+  const int klast_b = kt_last(min(W * jb + W - 1, nqt - 1), qoff, P.nkt);
+  auto row_word = [&](int r, int w) -> uint32_t {
+    if (W * jb + r >= nqt) return 0u;
+    const int kl = kt_last(W * jb + r, qoff, P.nkt);
+    if (w > (kl >> 5)) return 0u;
+    uint32_t x = P.occ ? (uint32_t)__builtin_amdgcn_readfirstlane((int)P.occ[(lrow0 + r) * P.occ_w + w]) : 0xffffffffu;
+    if (w == (kl >> 5) && (kl & 31) != 31) x &= (2u << (kl & 31)) - 1u;
+    return x;
+  };
+  int sw = -1;
+  uint32_t ub = 0u, sown = 0u;
+  auto next_tile = [&](uint32_t& own_out) -> int {
+    while (ub == 0u) {
+      if (++sw > (klast_b >> 5)) return -1;
+      uint32_t u = 0u, o = 0u;
+#pragma unroll
+      for (int r = 0; r < W; ++r) {
+        const uint32_t x = row_word(r, sw);
+        u |= x;
+        o = r == wv ? x : o;
+      }
+      ub = u;
+      sown = o;
+    }
+    const int kt = 32 * sw + __builtin_ctz(ub);
+    ub &= ub - 1u;
+    own_out = sown;
+    return kt;
+  };
+  F32Rows<D> kr, vr;
+  auto issue = [&](int kt) {
+    kr.load(kx, b, h, 32 * kt, Nk, wv);
+    vr.load(vx, b, h, 32 * kt, Nk, wv);
+  };
+  uint32_t cown = 0u;
+  int kt = next_tile(cown);
+  if (kt >= 0) issue(kt);
+  while (kt >= 0) {
+    lds_barrier();  // every wave is done with the previous tile
+    kr.template store<KS>(klds, wv);
+    vr.template store<KS>(vlds, wv);
+    uint32_t nown = 0u;
+    const int kt2 = next_tile(nown);
+    if (kt2 >= 0) issue(kt2);  // in flight during this tile's products
+    lds_barrier();             // tile kt in LDS
+    if ((cown >> (kt & 31)) & 1u) {
+      ++visited;
+      const int k0 = 32 * kt;
+      f32x16 S = lds_rows_mma<D, KS>(klds, Q, f32x16{});
+      const f32x16 Dp = lds_rows_mma<D, KS>(vlds, DO, f32x16{});
+      // exact x (the forward's expression), branch-free; keys after the query's position,
+      // padding keys and rows past Nq set to -1 (only on the tiles that have any)
+      f32x16 X;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) X[r] = __builtin_fmaf(S[r], 1.f, -tau);
+      if (k0 + 31 > min(qoff + 32 * qt, Nk - 1) || edge_rows) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + crow(r, g);
+          X[r] = qvalid && key <= pq && key < Nk ? X[r] : -1.f;
+        }
+      }
+      f32x16 E;
+      float xm = X[0];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool pos = X[r] > 0.f;
+        const float ds = pos ? coef * dpow_p<PK>(X[r], pw) * Dp[r] : 0.f;
+        bsum += ds;
+        if (want_l) lsum = __builtin_fmaf(pos ? pow_p<PK>(X[r], pw) : 0.f, Dp[r], lsum);
+        E[r] = ds;
+        xm = fmaxf(xm, X[r]);
+      }
+      computed += (P.occ || wave_ballot(xm > 0.f) != 0ull) ? 1u : 0u;
+      lds_tr_mma<D, KS>(klds, E, A);
+    }
+    cown = nown;  // the own row's word of the next tile
+    kt = kt2;
+  }
+  if (!act) return;
+  const int gslot = br == 0 ? B_DQ1 : B_DQ2;
+  const TRef<float> dqx{(float*)P.grad[br == 0 ? 0 : 2], P.s[gslot][0], P.s[gslot][1], P.s[gslot][2]};
+  finish_rows<PolF32, D, false>(A, nullptr, qvalid ? dqx.row(b, h, i) : nullptr, 1.f);
+  const float pb = wave_sum(-ci * bsum);
+  const float pl = wave_sum(-lsum);
+  if (l == 0) {
+    const int64_t lidx = lrow0 + wv;
+    P.ws[2 * lidx + 0] = pb;  // slot of (branch, head, query tile)
+    P.ws[2 * lidx + 1] = pl;
+    if (P.stats) {
+      atomicAdd(P.stats + 0, (unsigned long long)visited);
+      atomicAdd(P.stats + 1, (unsigned long long)computed);
+    }
+  }
+}
+
+// Key-major: four consecutive key tiles of one head (aligned: one bitmask word holds their
+// bits), streaming per branch the query tiles' Q and dO rows and tau values; K (per branch) and
+// V rows of the wave's key tile in registers.  dk rows per branch, dv rows at the end.
+template <int D, int BR, int PK>
+__global__ void __launch_bounds__(64 * kF32Blk) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1)))
+bwd_dkv_blk_f32(BwdParams P) {
+  constexpr int W = kF32Blk, NT = D / 2, ND = D / 32;
+  constexpr int KS = D + 4;
+  __shared__ __attribute__((aligned(16))) float qlds[32 * KS];
+  __shared__ __attribute__((aligned(16))) float dlds[32 * KS];
+  __shared__ __attribute__((aligned(16))) float tlds[32];  // tau of the tile's query rows
+  const int l = lane_id(), n32 = l & 31, g = l >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int BH = P.B * P.H, nqt = P.nqt, nkt = P.nkt, Nq = P.Nq, Nk = P.Nk, qoff = P.qoff;
+  // longest blocks (first key tiles) of every head first
+  const int bid = blockIdx.x, jb = bid / BH, bh = bid % BH;
+  const int b = bh / P.H, h = bh % P.H;
+  const int kt0 = W * jb, kt = kt0 + wv;
+  const bool act = kt < nkt;
+  const int j = 32 * kt + n32;
+  const bool kvalid = act && j < Nk;
+  const int qtf_b = qt_first(kt0, qoff);  // first query tile of the block
+  const TRef<const float> vx{(const float*)P.in[4], P.s[B_V][0], P.s[B_V][1], P.s[B_V][2]};
+  const TRef<const float> dox{(const float*)P.in[5], P.s[B_DO][0], P.s[B_DO][1], P.s[B_DO][2]};
+  float Vf[NT];
+  PolF32::load_rows<NT>(kvalid ? vx.row(b, h, j) : nullptr, g, Vf);
+  const float beta = *P.beta;
+  const float pw = P.p;
+  float lam = 0.f;
+  if constexpr (BR == 2) lam = clamp01(*P.lam);
+  const bool edge_keys = !act || 32 * kt + 31 >= Nk;
+  // the block's active key tiles (bits r: key tile kt0 + r)
+  const uint32_t actm = nkt - kt0 >= W ? (1u << W) - 1u : (1u << (nkt - kt0)) - 1u;
+  f32x16 AV[ND];
+#pragma unroll
+  for (int c = 0; c < ND; ++c) AV[c] = f32x16{};
+  unsigned visited = 0, computed = 0;
+
+#pragma unroll
+  for (int br = 0; br < BR; ++br) {
+    const int qslot = br == 0 ? B_Q1 : B_Q2, kslot = br == 0 ? B_K1 : B_K2;
+    const TRef<const float> qx{(const float*)P.in[br == 0 ? 0 : 2], P.s[qslot][0], P.s[qslot][1], P.s[qslot][2]};
+    const TRef<const float> kx{(const float*)P.in[br == 0 ? 1 : 3], P.s[kslot][0], P.s[kslot][1], P.s[kslot][2]};
+    float Kf[NT];
+    PolF32::load_rows<NT>(kvalid ? kx.row(b, h, j) : nullptr, g, Kf);
+    const float coef = br == 0 ? 1.f : -lam;
+    f32x16 AK[ND];
+#pragma unroll
+    for (int c = 0; c < ND; ++c) AK[c] = f32x16{};
+    const int64_t row0 = ((int64_t)br * BH + bh) * nqt;  // bitmask row of query tile 0
+
+    // union walk over query tiles qtf_b .. nqt - 1, 64 per round: lane q tests query tile q0c + q
+    int q0c = qtf_b - 64;
+    uint64_t um = 0ull, om = 0ull;
+    auto next_tile = [&](bool& own_out) -> int {
+      while (um == 0ull) {
+        q0c += 64;
+        if (q0c >= nqt) return -1;
+        const int qtl = q0c + l;
+        const bool in = qtl < nqt;
+        const uint32_t w = !in ? 0u : P.occ ? P.occ[(row0 + qtl) * P.occ_w + (kt0 >> 5)] : 0xffffffffu;
+        uint32_t bits = (w >> (kt0 & 31)) & actm;
+        // causal: key tile kt0 + r is seen from query tile qt_first(kt0 + r) on
+#pragma unroll
+        for (int r = 0; r < W; ++r)
+          if (qtl < qt_first(kt0 + r, qoff)) bits &= ~(1u << r);
+        um = wave_ballot(bits != 0u);
+        om = wave_ballot((bits >> wv) & 1u);
+      }
+      const int q = __builtin_ctzll(um);
+      um &= um - 1ull;
+      own_out = (om >> q) & 1ull;
+      return q0c + q;
+    };
+    F32Rows<D> qr, dr;
+    float vtq = 0.f;
+    auto issue = [&](int qt) {
+      qr.load(qx, b, h, 32 * qt, Nq, wv);
+      dr.load(dox, b, h, 32 * qt, Nq, wv);
+      if (wv == 0 && l < 32) vtq = beta * tau_coeff(qoff + 32 * qt + l, P.inv_d);
+    };
+    bool cown = false;
+    int qt = next_tile(cown);
+    if (qt >= 0) issue(qt);
+    while (qt >= 0) {
+      lds_barrier();  // every wave is done with the previous tile
+      qr.template store<KS>(qlds, wv);
+      dr.template store<KS>(dlds, wv);
+      if (wv == 0 && l < 32) tlds[l] = vtq;
+      bool nown = false;
+      const int qt2 = next_tile(nown);
+      if (qt2 >= 0) issue(qt2);  // in flight during this tile's products
+      lds_barrier();             // tile qt in LDS
+      if (cown) {
+        ++visited;
+        const int q0 = 32 * qt;
+        // S = Q K^T: lane = key, values = query rows crow(r, g)
+        const f32x16 S = lds_rows_mma<D, KS>(qlds, Kf, f32x16{});
+        const f32x16 Dp = lds_rows_mma<D, KS>(dlds, Vf, f32x16{});
+        f32x16 X;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) X[r] = __builtin_fmaf(S[r], 1.f, -tlds[crow(r, g)]);
+        // masks only on the tiles that need them: queries before the key (the diagonal), rows
+        // past Nq, keys past Nk
+        if (32 * kt + 31 > qoff + q0 || q0 + 31 >= Nq || edge_keys) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int qi = q0 + crow(r, g);
+            X[r] = kvalid && qi < Nq && j <= qoff + qi ? X[r] : -1.f;
+          }
+        }
+        f32x16 EV, EK;
+        float xm = X[0];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const bool pos = X[r] > 0.f;
+          EV[r] = pos ? coef * pow_p<PK>(X[r], pw) : 0.f;
+          EK[r] = pos ? coef * dpow_p<PK>(X[r], pw) * Dp[r] : 0.f;
+          xm = fmaxf(xm, X[r]);
+        }
+        computed += (P.occ || wave_ballot(xm > 0.f) != 0ull) ? 1u : 0u;
+        lds_tr_mma<D, KS>(dlds, EV, AV);
+        lds_tr_mma<D, KS>(qlds, EK, AK);
+      }
+      cown = nown;
+      qt = qt2;
+    }
+    const int gslot = br == 0 ? B_DK1 : B_DK2;
+    const TRef<float> dkx{(float*)P.grad[br == 0 ? 1 : 3], P.s[gslot][0], P.s[gslot][1], P.s[gslot][2]};
+    if (act) finish_rows<PolF32, D, false>(AK, nullptr, kvalid ? dkx.row(b, h, j) : nullptr, 1.f);
+  }
+  if (!act) return;
+  const TRef<float> dvx{(float*)P.grad[4], P.s[B_DV][0], P.s[B_DV][1], P.s[B_DV][2]};
+  finish_rows<PolF32, D, false>(AV, nullptr, kvalid ? dvx.row(b, h, j) : nullptr, 1.f);
+  if (P.stats && l == 0) {
+    atomicAdd(P.stats + 0, (unsigned long long)visited);
+    atomicAdd(P.stats + 1, (unsigned long long)computed);
+  }
+}
+
 // Deterministic second stage: fixed-order fp64 sum of the per-wave partials.
 constexpr int kFinThreads = kFinSlices;  // one thread per slice
 // The partials in the fixed order of tda_fin.hpp: kFinSlices slice sums, then one wave's total.
@@ -534,6 +880,21 @@ template <class Pol, int D, int BR, int PK, bool NORM>
 static int launch_bwd_t(const BwdParams& p, void* stream) {
   const int64_t qitems = (int64_t)p.B * p.H * p.nqt, kitems = (int64_t)p.B * p.H * p.nkt;
   hipStream_t s = (hipStream_t)stream;
+  if constexpr (!NORM && sizeof(typename Pol::T) == 4) {
+    if (!p.pairs) {
+      // the forward's block tile pass (every query tile, no lists): the block passes, then the
+      // sum over the (branch, head, query tile) partials
+      const int BH = p.B * p.H;
+      hipLaunchKernelGGL((bwd_dq_blk_f32<D, BR, PK>), dim3((unsigned)(BR * BH * ((p.nqt + kF32Blk - 1) / kF32Blk))),
+                         dim3(64 * kF32Blk), 0, s, p);
+      launched(s, "bwd_dq");
+      hipLaunchKernelGGL((bwd_dkv_blk_f32<D, BR, PK>), dim3((unsigned)(BH * ((p.nkt + kF32Blk - 1) / kF32Blk))),
+                         dim3(64 * kF32Blk), 0, s, p);
+      launched(s, "bwd_dkv");
+      const int e = (int)hipGetLastError();
+      return e ? e : launch_bwd_finish(p, BR, (int64_t)BR * qitems, stream);
+    }
+  }
   if (p.pairs && p.dkvq) {
     // the forward's pair lists (the fp32 candidate pass): the pair passes (tda_bwd_fast.hip),
     // then the tile passes over the lists and key tiles they left, then the sum over the lists'

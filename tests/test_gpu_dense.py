@@ -148,3 +148,42 @@ def test_dense_bitmask_counts_and_determinism(branches):
     for a, name in zip(g1, names):
         if a is not None:
             assert rel_err(a, ref[name]) <= 2e-2, name
+
+
+@pytest.mark.parametrize("branches", [1, 2])
+def test_dense_fp32_bitmask_and_offset(branches):
+    """fp32 without normalisation (the fp32 block passes): the gradients with the forward's
+    bitmask and without one (every causal tile walked) agree bitwise, with a sparse bitmask
+    (scaled-down queries: most tiles hold no weight); a second call is bitwise equal; and a
+    chunked-prefill offset with keys past the last query position is held to 1e-4 against the
+    oracle."""
+    from tda_amd import ops
+    dtype = torch.float32
+    shape = (1, 2, 230, 64)
+    xs = make_inputs(shape, 1500 + branches, 5, dtype)
+    q1, q2, k1, k2, v = xs
+    q1, q2 = 0.02 * q1, 0.02 * q2
+    if branches == 1:
+        q2 = k2 = None
+    (do,) = make_inputs(shape, 1510, 1, dtype)
+    beta = torch.tensor(1.5, device="cuda")
+    lam = torch.tensor(0.4, device="cuda") if branches == 2 else None
+    norms, occ = ops.side_buffers(shape, branches, False, "cuda")
+    st = torch.zeros(3, dtype=torch.int64, device="cuda")
+    ops.forward(q1, k1, q2, k2, v, beta, lam, 2.0, False, branches, norms=norms, occupancy=occ, stats=st)
+    assert 0 < int(st[1]) < int(st[0]), st.tolist()  # some tiles hold no weight
+    args = (q1, k1, q2, k2, v, do, beta, lam, 2.0, False, branches)
+    g1 = ops.backward(*args, norms=norms, occupancy=occ)
+    g2 = ops.backward(*args, norms=norms, occupancy=None)
+    g3 = ops.backward(*args, norms=norms, occupancy=occ)
+    for a, b2, c in zip(g1, g2, g3):
+        if a is not None:
+            assert torch.equal(a, b2)
+            assert torch.equal(a, c)
+    # offset: 100 query rows at positions 200.., 330 keys
+    q1, q2 = make_inputs((1, 2, 100, 64), 1520, 2, dtype)
+    k1, k2, v = make_inputs((1, 2, 330, 64), 1521, 3, dtype)
+    (do,) = make_inputs((1, 2, 100, 64), 1522, 1, dtype)
+    xs = [q1, q2, k1, k2, v] if branches == 2 else [q1, k1, v]
+    out, leaves, bt, lt = _run(xs, do, 1.0, 0.3, 1.5, branches, q_offset=200)
+    _check(out, leaves, bt, lt, xs, do, 1.0, 0.3, 1.5, branches, dtype, q_offset=200)
