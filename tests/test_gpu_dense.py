@@ -2,13 +2,15 @@
 README.md:20-31), where raw dot products of N(0, 1) rows pass their threshold about half the
 time and every causal tile holds weights.  The bf16 forward then runs the block tile pass
 (fwd_pv_blk: four query tiles per workgroup sharing each key tile) and the backward the block
-passes (bwd_dq_blk, bwd_dkv_blk) for every list past its cap.
+passes (bwd_dq_blk, bwd_dkv_blk) for every list past its cap; fp32 runs its own block passes
+(fwd_wave_blk, bwd_dq_blk_f32, bwd_dkv_blk_f32).
 
 Against the CPU oracle (fp64 autograd of the formula): the output and every gradient (dq1,
 dq2, dk1, dk2, dv, dbeta, dlambda) at 2e-2 (bf16) / 1e-4 (fp32) normwise, on shapes whose
 query-tile count is not a multiple of four (workgroups with idle waves), the last query tile
 partial, one and two branches, d = 64 and 128, p = 1, 1.5, 2; position offsets (chunked
-prefill, keys past the last query); strided (B, N, H, d) views; the tile bitmask against the
+prefill, keys past the last query); strided (B, N, H, d) views; beta < 0 (most weights
+non-zero); the fp32 gradients with and without the bitmask bitwise equal; the tile bitmask against the
 oracle's non-zero tiles; the pair-list counts past the cap against the oracle's number of
 non-zero weights; and bitwise determinism of forward and backward."""
 import pytest
@@ -86,15 +88,30 @@ def test_dense_offsets(nq, nk, off):
     _check(out, leaves, bt, lt, xs, do, 1.0, 0.3, 2.0, 2, dtype, q_offset=off)
 
 
-def test_dense_strided_views():
-    """(B, N, H, d) storage viewed as (B, H, N, d), bf16, two branches."""
-    dtype = torch.bfloat16
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_dense_strided_views(dt):
+    """(B, N, H, d) storage viewed as (B, H, N, d), two branches."""
+    dtype = DT[dt]
     base = make_inputs((1, 230, 2, 128), 1300, 5, dtype)
     (dob,) = make_inputs((1, 230, 2, 128), 1301, 1, dtype)
     xs = [x.transpose(1, 2) for x in base]
     do = dob.transpose(1, 2)
     out, leaves, bt, lt = _run(xs, do, 1.0, 0.5, 2.0, 2)
     _check(out, leaves, bt, lt, xs, do, 1.0, 0.5, 2.0, 2, dtype)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("branches", [1, 2])
+def test_dense_negative_beta(dt, branches):
+    """beta < 0: the thresholds are negative (x = s + |beta| c_i), so most causal weights are
+    non-zero, scores below zero included; the gradient with respect to beta sums over all of
+    them."""
+    dtype = DT[dt]
+    shape = (1, 2, 170, 64)
+    xs = make_inputs(shape, 1600 + branches, 5 if branches == 2 else 3, dtype)
+    (do,) = make_inputs(shape, 1601, 1, dtype)
+    out, leaves, bt, lt = _run(xs, do, -20.0, 0.6, 1.5, branches)
+    _check(out, leaves, bt, lt, xs, do, -20.0, 0.6, 1.5, branches, dtype)
 
 
 @pytest.mark.parametrize("branches", [1, 2])
