@@ -204,3 +204,18 @@ def test_dense_fp32_bitmask_and_offset(branches):
     xs = [q1, q2, k1, k2, v] if branches == 2 else [q1, k1, v]
     out, leaves, bt, lt = _run(xs, do, 1.0, 0.3, 1.5, branches, q_offset=200)
     _check(out, leaves, bt, lt, xs, do, 1.0, 0.3, 1.5, branches, dtype, q_offset=200)
+
+
+@pytest.mark.parametrize("n", [1, 20, 33])
+@pytest.mark.parametrize("branches", [1, 2])
+def test_dense_fp32_short_sequences(n, branches):
+    """fp32 without normalisation at one and two query tiles: the single-tile forward
+    (fwd_wave) and the block backward passes with three or two idle waves per workgroup.  The
+    query and key rows are non-negative, so the first position (tau = 0) holds a weight."""
+    dtype = torch.float32
+    shape = (2, 2, n, 64)
+    xs = make_inputs(shape, 1700 + n, 5 if branches == 2 else 3, dtype)
+    xs = [x.abs() for x in xs[:-1]] + [xs[-1]]
+    (do,) = make_inputs(shape, 1701, 1, dtype)
+    out, leaves, bt, lt = _run(xs, do, 1.0, 0.5, 2.0, branches)
+    _check(out, leaves, bt, lt, xs, do, 1.0, 0.5, 2.0, branches, dtype)
