@@ -28,6 +28,29 @@ namespace {
 
 constexpr int kDecWaves = 4;  // waves per workgroup; key tiles per chunk = 32
 
+// Sum of squares of a row held as NT bf16x8 fragments per lane half (the row's two halves in
+// lanes n and n + 32): bf16 pairs by dot2 (each product exact in fp32), two chains over the
+// even and odd fragments, then the other half's sum.  A quarter of the instructions of
+// converting and multiplying each element; the decode kernel computes every norm it uses (and
+// writes to the norms table) with it.
+template <int NT>
+__device__ __forceinline__ float dec_sumsq(const bf16x8 (&f)[NT]) {
+  float a[2] = {0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const bf16x8 w = f[t];
+    const bf16x2 p0 = __builtin_shufflevector(w, w, 0, 1), p1 = __builtin_shufflevector(w, w, 2, 3);
+    const bf16x2 p2 = __builtin_shufflevector(w, w, 4, 5), p3 = __builtin_shufflevector(w, w, 6, 7);
+    float& x = a[t & 1];
+    x = __builtin_amdgcn_fdot2_f32_bf16(p0, p0, x, false);
+    x = __builtin_amdgcn_fdot2_f32_bf16(p1, p1, x, false);
+    x = __builtin_amdgcn_fdot2_f32_bf16(p2, p2, x, false);
+    x = __builtin_amdgcn_fdot2_f32_bf16(p3, p3, x, false);
+  }
+  const float v = a[0] + a[1];
+  return v + __shfl_xor(v, 32);
+}
+
 template <int D, int BR, int PK, bool NORM>
 __global__ void __launch_bounds__(64 * kDecWaves, 2) fwd_decode(FwdParams P, float* part) {
   using Pol = PolBF16;
@@ -64,7 +87,7 @@ __global__ void __launch_bounds__(64 * kDecWaves, 2) fwd_decode(FwdParams P, flo
     for (int t = 0; t < NT; ++t) Q[br][t] = Pol::load_row(row, t, g);
     rq[br] = 1.f;
     if constexpr (NORM) {
-      rq[br] = inv_norm(row_sumsq<Pol, NT>(Q[br]));
+      rq[br] = inv_norm(dec_sumsq<NT>(Q[br]));
       if (chunk == 0 && wv == 0 && g == 0 && qvalid) P.norms[norm_base(P, br ? N_Q2 : N_Q1, bh) + i] = rq[br];
     }
   }
@@ -98,7 +121,7 @@ __global__ void __launch_bounds__(64 * kDecWaves, 2) fwd_decode(FwdParams P, flo
     const int j = 32 * kt + n32;
     float rk = 1.f;
     if constexpr (NORM) {
-      rk = inv_norm(row_sumsq<Pol, NT>(K));
+      rk = inv_norm(dec_sumsq<NT>(K));
       if (store && g == 0 && j < Nk) P.norms[norm_base(P, br ? N_K2 : N_K1, bh) + j] = rk;
     }
     if (g == 0) rkw[n32] = rk;
