@@ -1467,11 +1467,11 @@ __global__ void __launch_bounds__(64 * kBwdBlk) __attribute__((amdgpu_waves_per_
 #pragma unroll
       for (int r = 0; r < 16; ++r) X[r] = __builtin_fmaf(NORM ? S[r] * rk[r] : S[r], rq, -tau);
       if (k0 + 31 > min(qoff + 32 * qt, Nk - 1) || rowpad) {
+        // key crow(r, g) = c_r + 4 g (c_r = 8 (r / 4) + r % 4) is visible iff c_r <= lim: one
+        // comparison per value
+        const int lim = (qvalid ? min(pq, Nk - 1) - k0 : -1) - 4 * g;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + crow(r, g);
-          X[r] = qvalid && key <= pq && key < Nk ? X[r] : -1.f;
-        }
+        for (int r = 0; r < 16; ++r) X[r] = 8 * (r >> 2) + (r & 3) <= lim ? X[r] : -1.f;
       }
       f32x16 E;
 #pragma unroll
@@ -1693,11 +1693,15 @@ __global__ void __launch_bounds__(64 * kBwdBlk) __attribute__((amdgpu_waves_per_
         // masks only on the tiles that need them: queries before the key (the diagonal), rows
         // past Nq, keys past Nk
         if (32 * kt + 31 > qoff + q0 || q0 + 31 >= Nq || 32 * kt + 31 >= Nk) {
+          // query row crow(r, g) = c_r + 4 g (c_r = 8 (r / 4) + r % 4) sees the key iff
+          // lo <= c_r <= lo + span: one unsigned comparison per value (an empty range: lo past
+          // every c_r)
+          const int lo0 = j - qoff - q0 - 4 * g, hi0 = Nq - 1 - q0 - 4 * g;
+          const bool some = kvalid && hi0 >= lo0;
+          const int lo = some ? lo0 : 64;
+          const uint32_t span = some ? (uint32_t)(hi0 - lo0) : 0u;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int qi = q0 + crow(r, g);
-            X[r] = kvalid && qi < Nq && j <= qoff + qi ? X[r] : -1.f;
-          }
+          for (int r = 0; r < 16; ++r) X[r] = (uint32_t)(8 * (r >> 2) + (r & 3) - lo) <= span ? X[r] : -1.f;
         }
         f32x16 EV, EK;
 #pragma unroll

@@ -1291,11 +1291,11 @@ __global__ void __launch_bounds__(64 * kBlkTiles) __attribute__((amdgpu_waves_pe
 #pragma unroll
           for (int e = 0; e < 4; ++e) X[4 * u + e] = __builtin_fmaf(NORM ? S[4 * u + e] * rk4[u][e] : S[4 * u + e], rq, -tau);
         if (32 * kt + 31 > min(qoff + 32 * qt, Nk - 1) || rowpad) {
+          // key crow(r, g) = c_r + 4 g (c_r = 8 (r / 4) + r % 4) is visible iff c_r <= lim: one
+          // comparison per value
+          const int lim = (valid ? min(pq, Nk - 1) - 32 * kt : -1) - 4 * g;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = 32 * kt + crow(r, g);
-            X[r] = valid && key <= pq && key < Nk ? X[r] : -1.f;
-          }
+          for (int r = 0; r < 16; ++r) X[r] = 8 * (r >> 2) + (r & 3) <= lim ? X[r] : -1.f;
         }
         // weights coef relu(x)^p and the lane's largest x (some weight of the tile is non-zero
         // iff a lane's is > 0), on the bits: a float is > 0 iff its bits as an int32 are, so the
