@@ -1299,6 +1299,15 @@ __global__ void __launch_bounds__(64) bwd_tiles(BwdParams P) {
 // masks branch-free and only on the tiles that need them.
 constexpr int kBwdBlk = 4;
 
+// max(x, 0) of 16 values on their bits: a float is > 0 iff its bits as an int32 are.
+__device__ __forceinline__ f32x16 relu_bits(const f32x16& x) {
+  typedef int i32x16_ __attribute__((ext_vector_type(16)));
+  i32x16_ b = __builtin_bit_cast(i32x16_, x);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) b[r] = max(b[r], 0);
+  return __builtin_bit_cast(f32x16, b);
+}
+
 // This wave's share of a 32-row tile of D columns: rows RPI (LPW wv + i) + l / CH, chunk l % CH.
 template <int D>
 struct BlkRows {
@@ -1474,13 +1483,27 @@ __global__ void __launch_bounds__(64 * kBwdBlk) __attribute__((amdgpu_waves_per_
         for (int r = 0; r < 16; ++r) X[r] = 8 * (r >> 2) + (r & 3) <= lim ? X[r] : -1.f;
       }
       f32x16 E;
+      if constexpr (PK == 2) {
+        // relu on the bits (a float is > 0 iff its bits as an int32 are): t = max(x, 0) with no
+        // comparison per value; 2 t and t^2 vanish with t.  (Whole-vector bit casts: hipcc
+        // compiled a bit cast of one element of an ext_vector to element 0.)
+        const f32x16 T = relu_bits(X);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const bool pos = X[r] > 0.f;
-        const float ds = pos ? coef * dpow_p<PK>(X[r], pw) * Dp[r] : 0.f;
-        bsum += ds;
-        if (want_l) lsum = __builtin_fmaf(pos ? pow_p<PK>(X[r], pw) : 0.f, Dp[r], lsum);
-        E[r] = NORM ? ds * rk[r] : ds;
+        for (int r = 0; r < 16; ++r) {
+          const float ds = coef * (T[r] + T[r]) * Dp[r];
+          bsum += ds;
+          if (want_l) lsum = __builtin_fmaf(T[r] * T[r], Dp[r], lsum);
+          E[r] = NORM ? ds * rk[r] : ds;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const bool pos = X[r] > 0.f;
+          const float ds = pos ? coef * dpow_p<PK>(X[r], pw) * Dp[r] : 0.f;
+          bsum += ds;
+          if (want_l) lsum = __builtin_fmaf(pos ? pow_p<PK>(X[r], pw) : 0.f, Dp[r], lsum);
+          E[r] = NORM ? ds * rk[r] : ds;
+        }
       }
       if (!P.occ) {
         float xm = X[0];
@@ -1704,12 +1727,22 @@ __global__ void __launch_bounds__(64 * kBwdBlk) __attribute__((amdgpu_waves_per_
           for (int r = 0; r < 16; ++r) X[r] = (uint32_t)(8 * (r >> 2) + (r & 3) - lo) <= span ? X[r] : -1.f;
         }
         f32x16 EV, EK;
+        if constexpr (PK == 2) {  // relu on the bits, as in bwd_dq_blk
+          const f32x16 T = relu_bits(X);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const bool pos = X[r] > 0.f;
-          EV[r] = pos ? coef * pow_p<PK>(X[r], pw) : 0.f;
-          const float ds = pos ? coef * dpow_p<PK>(X[r], pw) * Dp[r] : 0.f;
-          EK[r] = NORM ? ds * rq[r] : ds;
+          for (int r = 0; r < 16; ++r) {
+            EV[r] = coef * (T[r] * T[r]);
+            const float ds = coef * (T[r] + T[r]) * Dp[r];
+            EK[r] = NORM ? ds * rq[r] : ds;
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const bool pos = X[r] > 0.f;
+            EV[r] = pos ? coef * pow_p<PK>(X[r], pw) : 0.f;
+            const float ds = pos ? coef * dpow_p<PK>(X[r], pw) * Dp[r] : 0.f;
+            EK[r] = NORM ? ds * rq[r] : ds;
+          }
         }
         bool anyw = true;  // without a bitmask the counters count the tiles with a weight
         if (!P.occ) {
