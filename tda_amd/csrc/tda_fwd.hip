@@ -755,8 +755,8 @@ int launch_zero(const FwdParams& p, void* stream) {
 
 // head_dim 256 runs tda_wide.hip; otherwise bf16 runs the screen + sparse A.V kernels (tda_fwd_sparse.hip), or with a single query tile
 // the split-key decode kernels (tda_fwd_decode.hip); fp32 runs fwd_wave, after the int8 screen
-// when normalised with more than one query tile.  The screen clears the call's zero range; the
-// other paths launch zero_range.
+// when normalised with more than one query tile.  The screens, and the bf16 block tile pass
+// without normalisation, clear the call's zero range; the other paths launch zero_range.
 int launch_fwd(const FwdParams& p, const KernelKey& k, void* stream) {
   if (p.zero && p.zero_per_it == 0) {
     // a zero range too large for the screen's per-item slices: cleared whole first

@@ -6,33 +6,32 @@
 // (TTA:19-115: scores, threshold, ReLU^p, causal mask, A.V) and the differential composition
 // out = A1 V - clamp(lambda, 0, 1) A2 V (TTA:489-519).
 //
-// Launches, in stream order:
-//   key_prep    (normalize) inverse L2 norms rk_j of the key rows into the norms table, and the
-//               normalised key rows quantised to int8 with a per-row scale and residual bound.
-//   fwd_screen  for every causal (query tile, key tile) pair of a branch, a score tile on the
-//               matrix cores and a test that keeps every tile holding a non-zero weight
-//               (x_ij = fma(s_ij rk_j, rq_i, -tau_i) > 0 for some pair).  Without normalisation
-//               (fwd_screen) the test is exact on the bf16 scores; with it (fwd_screen_i8) the
-//               scores are int8 products of the quantised normalised rows and the test carries a
-//               bound on the quantisation residuals, so it may keep tiles and keys whose weights
-//               are all zero, never drop a non-zero one.  No V and no output accumulators, so
-//               several waves share a SIMD.  With normalisation it also lists each query
-//               tile's candidate keys (the keys of its passing lanes).
-//   fwd_pv_cand (normalize) one wave per branch of a query tile whose candidate lists fit:
-//               the score tile of its rows against the candidate keys (the same MFMA sequence
-//               and operand values as fwd_pv, so the same scores), the exact weights and
-//               coef A V over the candidates' V rows, the branches' sums added through LDS;
-//               the bitmask row is rewritten exactly.  Query tiles whose lists overflow go to
-//               a queue for fwd_pv.
-//   fwd_pv      the tile pass, one wave per query tile (every tile without normalisation, the
-//               queued ones with it): walks the set bits of both branches, recomputes the
-//               score tile, forms the exact weights ReLU(x)^p with the causal mask, and
-//               accumulates out += coef A V.  Tiles whose exact weights are all zero lose their
-//               bit, so the bitmask ends exact.
-// The screen tests every key of the tile, including keys after the query on the diagonal tile
-// (and, without normalisation, padding keys past Nk): it may keep a tile the mask empties, never
-// drop a non-zero one.  With normalisation padding keys are cleared from the hit bits, so no
-// candidate list names a key row past Nk.
+// Launches, in stream order, with normalisation:
+//   key_prep    inverse L2 norms rk_j of the key rows into the norms table, and the normalised
+//               key rows quantised to int8 with a per-row scale and residual bound.
+//   fwd_screen  (fwd_screen_i8) for every causal (query tile, key tile) pair of a branch, an int8
+//               score tile of the quantised normalised rows on the matrix cores and a test that
+//               carries a bound on the quantisation residuals: it keeps every tile holding a
+//               non-zero weight (x_ij = fma(s_ij rk_j, rq_i, -tau_i) > 0 for some pair) and may
+//               keep tiles and keys whose weights are all zero.  No V and no output
+//               accumulators, so several waves share a SIMD.  It also lists each query tile's
+//               candidate keys (the keys of its passing lanes).
+//   fwd_pv_cand one wave per branch of a query tile whose candidate lists fit: the score tile
+//               of its rows against the candidate keys (the same MFMA sequence and operand
+//               values as fwd_pv, so the same scores), the exact weights and coef A V over the
+//               candidates' V rows, the branches' sums added through LDS; the bitmask row is
+//               rewritten exactly.  Query tiles whose lists overflow go to a queue for fwd_pv.
+//   fwd_pv      the tile pass for the queued query tiles, one wave per query tile: walks the set
+//               bits of both branches, recomputes the score tile, forms the exact weights
+//               ReLU(x)^p with the causal mask, and accumulates out += coef A V.  Tiles whose
+//               exact weights are all zero lose their bit, so the bitmask ends exact.
+// Without normalisation one launch, fwd_pv_blk: every query tile, four per workgroup sharing
+// each key tile's rows, scores every causal key tile and forms the weights, A V and the exact
+// bitmask itself (a screen would compute the same bf16 scores once more); its workgroups also
+// clear the call's zero range, a share each after their own tiles.
+// The screen tests every key of the tile, including keys after the query on the diagonal tile:
+// it may keep a tile the mask empties, never drop a non-zero one.  Padding keys are cleared from
+// the hit bits, so no candidate list names a key row past Nk.
 #include <type_traits>
 
 #include "tda_common.hpp"
@@ -431,155 +430,9 @@ __global__ void __launch_bounds__(256) key_prep(FwdParams P, int BR) {
   }
 }
 
-// ------------------------------------------------------------------ fwd_screen (unnormalised)
-// The exact screen of dot-product scores.  Workgroup = one work item (ScreenItem): 256 query rows
-// of one branch of one head against key tiles [k0, k1), QPW 32-row query tiles per wave (8 / QPW
-// waves).  Key tiles stream through LDS in groups of TPB tiles ("super-stages", two of them in a
-// ring): buffer loads into VGPRs one iteration ahead, LDS writes of the next group while the
-// current one is read, one barrier per group.  Score tiles are computed transposed, S^T = K Q^T:
-// each lane holds one query i and 16 of its keys, so "max_j s_ij > tau_i" is the exact test with
-// one compare per lane (the exact pass computes the same scores with the same MFMA sequence).
-// Dispatch uses QPW = 2 (three waves per SIMD) and TPB = 1.
-template <int D, int QPW, int TPB>
-__global__ void __launch_bounds__(512 / QPW, 2) fwd_screen(FwdParams P, int BR) {
-  constexpr int NT = D / 16;                // MFMA steps over d
-  constexpr int KS = D + 8;                 // LDS row stride (elements): conflict-free fragment reads
-  constexpr int NTHR = 512 / QPW;           // threads per workgroup
-  constexpr int CPR = D / 8;                // 16-byte chunks per key row
-  constexpr int TPR = CPR < NTHR / 32 ? CPR : NTHR / 32;  // staging threads per row
-  constexpr int CPT = CPR / TPR;            // chunks per staging thread
-  __shared__ __attribute__((aligned(16))) bf16 kst[2 * TPB][32 * KS];
-
-  const int l = lane_id(), n32 = l & 31, g = l >> 5, tid = threadIdx.x;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int BH = P.B * P.H, Nq = P.Nq, Nk = P.Nk, nqt = P.nqt, qoff = P.qoff;
-  const ScreenItem it = screen_item(P, BR);
-  const int k0 = it.k0, k1 = it.k1;
-  const int br = it.sidx / BH, bh = it.sidx % BH;
-  const int b = bh / P.H, h = bh % P.H;
-  const int qslot = br ? F_Q2 : F_Q1, kslot = br ? F_K2 : F_K1;
-  const int q0w = it.qb * 256 + 32 * QPW * wv;  // first row of this wave
-  const int qt0 = q0w >> 5;                     // this wave's query tiles: qt0 .. qt0 + QPW - 1
-  const int nit = (k1 - k0 + TPB - 1) / TPB;
-  bool live[QPW];
-  int ktl[QPW];  // last key tile each query tile sees
-#pragma unroll
-  for (int s = 0; s < QPW; ++s) {
-    live[s] = qt0 + s < nqt;
-    ktl[s] = kt_last(qt0 + s, qoff, P.nkt);
-  }
-
-  // ---- staging
-  const bf16* khead = (const bf16*)P.in[kslot] + (int64_t)b * P.s[kslot][0] + (int64_t)h * P.s[kslot][1];
-  const int64_t sk = P.s[kslot][2];
-  const int srow = tid / TPR, sch = tid % TPR;
-  const bool stager = tid < 32 * TPR;
-  const uint32_t soff = (uint32_t)((srow * sk + 8 * sch) * 2);
-  u32x4 R[TPB][CPT];
-  auto fetch = [&](int i) {  // tiles of group i into registers
-#pragma unroll
-    for (int j = 0; j < TPB; ++j) {
-      const int kt = k0 + TPB * i + j;
-      if (kt >= k1) break;
-      if (stager) {
-        const __amdgpu_buffer_rsrc_t rs = tile_rsrc<D>(khead, sk, kt, Nk);  // rows past Nk read 0
-#pragma unroll
-        for (int c = 0; c < CPT; ++c) R[j][c] = buf_load16(rs, soff + 16 * TPR * c);
-      }
-    }
-  };
-  auto commit = [&](int i) {  // group i into its super-stage
-#pragma unroll
-    for (int j = 0; j < TPB; ++j) {
-      const int kt = k0 + TPB * i + j;
-      if (kt >= k1) break;
-      if (stager) {
-        bf16* k = &kst[TPB * (i & 1) + j][srow * KS + 8 * sch];
-#pragma unroll
-        for (int c = 0; c < CPT; ++c) *reinterpret_cast<u32x4*>(k + 8 * TPR * c) = R[j][c];
-      }
-    }
-  };
-
-  // ---- resident query fragments and thresholds
-  const bf16* qhead = (const bf16*)P.in[qslot] + (int64_t)b * P.s[qslot][0] + (int64_t)h * P.s[qslot][1];
-  const float beta = *P.beta;
-  bf16x8 Q[QPW][NT];
-  float tau[QPW];  // tau_i of the lane's query
-  bool valid[QPW];
-#pragma unroll
-  for (int s = 0; s < QPW; ++s) {
-    const int iq = q0w + 32 * s + n32;
-    valid[s] = iq < Nq;
-    const bf16* row = qhead + (int64_t)min(iq, Nq - 1) * P.s[qslot][2];  // rows >= Nq: never vote
-#pragma unroll
-    for (int t = 0; t < NT; ++t) Q[s][t] = *reinterpret_cast<const bf16x8*>(row + 16 * t + 8 * g);
-    tau[s] = beta * tau_coeff(qoff + iq, P.inv_d);
-  }
-  ZeroSlice zs;
-  zs.init(P, it);
-
-  uint32_t hb[QPW], cn[QPW];  // hit bits; candidate keys met per query tile (may pass the cap)
-#pragma unroll
-  for (int s = 0; s < QPW; ++s) hb[s] = cn[s] = 0u;
-  const int koff = n32 * KS + 8 * g;
-
-  // Threshold test of key tile kt (in stage st) against this wave's query tiles.
-  auto process = [&](int kt, int st) {
-    if (!(live[0] && kt <= ktl[QPW - 1])) return;
-    const bf16* kp = &kst[st][koff];
-    bf16x8 fk[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {  // in MFMA order: LDS returns in order, the chain waits per step
-      fk[t] = *reinterpret_cast<const bf16x8*>(kp + 16 * t);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    f32x16 S[QPW];
-#pragma unroll
-    for (int s = 0; s < QPW; ++s) S[s] = f32x16{};
-    // One query tile's chain at a time: dependent MFMAs back to back on the same accumulator
-    // take the accumulate fast path.
-#pragma unroll
-    for (int s = 0; s < QPW; ++s) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) S[s] = PolBF16::mma(fk[t], Q[s][t], S[s]);  // S^T = K Q^T
-      __builtin_amdgcn_sched_barrier(0);  // keep the chains apart
-    }
-    const uint32_t bit = 1u << (kt & 31);
-    // Both tests run on every path, masked by selects: the MFMA results are read only in
-    // straight-line code after the chains, where the compiler counts the wait states the
-    // hardware needs between an MFMA writing a register and a VALU reading it.
-#pragma unroll
-    for (int s = 0; s < QPW; ++s) {
-      const bool hit = valid[s] && max16(S[s]) > tau[s];  // largest score of the lane's query
-      hb[s] |= live[s] && hit && kt <= ktl[s] ? bit : 0u;
-    }
-  };
-
-  fetch(0);
-  commit(0);
-  if (nit > 1) fetch(1);
-  lds_barrier();
-  for (int i = 0; i < nit; ++i) {
-#pragma unroll
-    for (int j = 0; j < TPB; ++j) {
-      const int kt = k0 + TPB * i + j;
-      if (kt >= k1) break;
-      if (P.zero) zs.clear<NTHR>(P, kt - k0, tid);
-      process(kt, TPB * (i & 1) + j);
-      screen_flush<QPW, false>(P, BR, it, qt0, live, hb, cn, kt);
-    }
-    // the other super-stage was last read before the previous barrier
-    if (i + 1 < nit) commit(i + 1);
-    if (i + 2 < nit) fetch(i + 2);
-    lds_barrier();  // the fetch stays in flight across it
-  }
-  screen_count<QPW>(P, it, live, ktl);
-}
-
 // ------------------------------------------------------------------ fwd_screen_i8 (normalised)
 // The normalised screen on int8 matrix cores (v_mfma_i32_32x32x32_i8, twice the bf16 rate, half
-// the operand bytes).  Workgroup = one work item (as fwd_screen), four waves of two 32-row query
+// the operand bytes).  Workgroup = one work item (ScreenItem), four waves of two 32-row query
 // tiles.  Per wave the query rows are normalised (their inverse norms rq go to the norms table),
 // quantised to int8 with one scale per query tile and held as A fragments.  The int8 key tiles
 // of key_prep (32 x D bytes, contiguous) and their {s_j, ek_j} stream through a ring of
@@ -830,7 +683,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) f
       __builtin_amdgcn_sched_barrier(0);  // keep the chains apart
     }
     const uint32_t bit = 1u << (kt & 31);
-    // straight-line tests on every path (see fwd_screen)
+    // straight-line tests on every path: the compiler counts the wait states after an MFMA on
+    // the fall-through path only, so a branch here could read scores not yet written
 #pragma unroll
     for (int s = 0; s < QPW; ++s) {
       const float thr = __builtin_fmaf(-kq.y, cq[s], tq[s]);
@@ -1122,8 +976,9 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
 // the wave only counts its non-zero weights (one wave sum at the end) instead of placing them.
 constexpr int kBlkTiles = 4;
 
-template <int D, int BR, int PK, bool NORM>
+template <int D, int BR, int PK, bool NORM, bool WALK = false, bool ZR = false>
 __global__ void __launch_bounds__(64 * kBlkTiles) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 2))) fwd_pv_blk(FwdParams P) {
+  static_assert(!ZR || WALK, "the zero range is cleared by the walk");
   constexpr int W = kBlkTiles;
   constexpr int NT = D / 16, ND = D / 32;
   constexpr int VS = D + 32;     // LDS row stride of a V tile: conflict-free transpose reads
@@ -1211,7 +1066,7 @@ __global__ void __launch_bounds__(64 * kBlkTiles) __attribute__((amdgpu_waves_pe
       if (q >= nqt) return 0u;
       const int kl = kt_last(q, qoff, P.nkt);
       if (w > (kl >> 5)) return 0u;
-      uint32_t x = (uint32_t)__builtin_amdgcn_readfirstlane((int)orow0[(int64_t)r * P.occ_w + w]);
+      uint32_t x = WALK ? 0xffffffffu : (uint32_t)__builtin_amdgcn_readfirstlane((int)orow0[(int64_t)r * P.occ_w + w]);
       if (w == (kl >> 5) && (kl & 31) != 31) x &= (2u << (kl & 31)) - 1u;
       return x;
     };
@@ -1361,16 +1216,29 @@ __global__ void __launch_bounds__(64 * kBlkTiles) __attribute__((amdgpu_waves_pe
         }
       }
       if (kt2 < 0 || nw != cw) {  // the own row's word cw is done
-        if (act && keep != cown && l == 0) orow0[(int64_t)wv * P.occ_w + cw] = keep;
+        if (act && (WALK || keep != cown) && l == 0) orow0[(int64_t)wv * P.occ_w + cw] = keep;
         cw = nw;
         cown = keep = nown;
       }
       kt = kt2;
     }
+    if (WALK && act && l == 0) {  // the own row's words past its last key tile (no screen wrote them)
+      for (int w = (kt_last(qt, qoff, P.nkt) >> 5) + 1; w < P.occ_w; ++w) orow0[(int64_t)wv * P.occ_w + w] = 0u;
+    }
     if (pent) {
       npairs += wave_sum_u32(extra);
       if (l == 0) P.pairs[pair_lists(P.nbr, BH, nqt) * 4 * kPairCap + lidx] = npairs;
     }
+  }
+
+  if (ZR) {
+    // the call's zero range (the backward's gradients in training): the workgroup's even share of
+    // the 16-byte units, streaming stores that drain while other workgroups still compute (the
+    // host picks ZR only when a share has fewer than 2^31 units)
+    const int64_t nwg = gridDim.x, z0 = P.zero_units * (int64_t)blockIdx.x / nwg;
+    u32x4* zbase = reinterpret_cast<u32x4*>(P.zero) + z0;
+    const uint32_t zn = (uint32_t)(P.zero_units * ((int64_t)blockIdx.x + 1) / nwg - z0);
+    for (uint32_t u = threadIdx.x; u < zn; u += 64 * W) __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u}, zbase + u);
   }
 
   // Output rows through LDS (the wave's slice of the ring, free once every wave has passed the
@@ -1397,6 +1265,7 @@ __global__ void __launch_bounds__(64 * kBlkTiles) __attribute__((amdgpu_waves_pe
     }
   }
   if (P.stats && l == 0 && checked) {
+    if (WALK) atomicAdd(P.stats + 0, (unsigned long long)checked);  // every causal tile is tested
     atomicAdd(P.stats + 1, (unsigned long long)computed);
     atomicAdd(P.stats + 2, (unsigned long long)checked);
   }
@@ -1696,13 +1565,22 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
     hipLaunchKernelGGL((key_prep<D, bf16>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, BR);
     launched(s, "key_prep");
   }
-  const dim3 grid((unsigned)(BR * BH) * (unsigned)p.screen_items);
-  if constexpr (NORM) {
-    hipLaunchKernelGGL((fwd_screen_i8<D, bf16>), grid, dim3(256), 0, s, p, BR);
-  } else {
-    constexpr int QPW = 2, TPB = 1;
-    hipLaunchKernelGGL((fwd_screen<D, QPW, TPB>), grid, dim3(512 / QPW), 0, s, p, BR);
+  if constexpr (!NORM) {
+    // without normalisation every query tile runs the block tile pass over all its causal key
+    // tiles (its scores decide the weights and write the bitmask; a screen would compute the
+    // same scores once more); it also clears the call's zero range
+    const unsigned blocks = (unsigned)(BH * ((p.nqt + kBlkTiles - 1) / kBlkTiles));
+    const bool zr = p.zero && p.zero_units > 0 && p.zero_units / blocks < (int64_t(1) << 31);
+    if (zr)
+      hipLaunchKernelGGL((fwd_pv_blk<D, BR, PK, NORM, true, true>), dim3(blocks), dim3(64 * kBlkTiles), 0, s, p);
+    else
+      hipLaunchKernelGGL((fwd_pv_blk<D, BR, PK, NORM, true>), dim3(blocks), dim3(64 * kBlkTiles), 0, s, p);
+    launched(s, "fwd_pv");
+    const int e = (int)hipGetLastError();
+    return e || zr ? e : launch_zero(p, s);
   }
+  const dim3 grid((unsigned)(BR * BH) * (unsigned)p.screen_items);
+  hipLaunchKernelGGL((fwd_screen_i8<D, bf16>), grid, dim3(256), 0, s, p, BR);
   launched(s, "fwd_screen");
   if (NORM && p.cand) {
     hipLaunchKernelGGL((fwd_pv_cand<D, BR, PK>), dim3((unsigned)(BH * p.nqt)), dim3(64 * BR), 0, s, p);

@@ -24,7 +24,8 @@ CASES = [
     # (shape, keys, q_offset, branches, dtype, normalize)
     ((2, 3, 300, 128), None, 0, 2, torch.bfloat16, True),    # screen path, ragged last block
     ((1, 2, 70, 64), None, 0, 1, torch.bfloat16, True),      # one branch, d = 64
-    ((2, 2, 600, 64), None, 0, 2, torch.bfloat16, False),    # unnormalised screen
+    ((2, 2, 600, 64), None, 0, 2, torch.bfloat16, False),    # unnormalised: the block tile pass
+    ((1, 3, 333, 128), None, 0, 1, torch.bfloat16, False),   # the same, one branch, d = 128, ragged
     ((2, 2, 5, 128), 200, 195, 2, torch.bfloat16, True),     # decode kernels (one query tile)
     ((1, 2, 100, 64), None, 0, 2, torch.float32, True),      # fp32 path
 ]
