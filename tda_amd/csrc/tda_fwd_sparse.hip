@@ -1578,23 +1578,23 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
     launched(s, "fwd_pv");
     const int e = (int)hipGetLastError();
     return e || zr ? e : launch_zero(p, s);
+  } else {
+    const dim3 grid((unsigned)(BR * BH) * (unsigned)p.screen_items);
+    hipLaunchKernelGGL((fwd_screen_i8<D, bf16>), grid, dim3(256), 0, s, p, BR);
+    launched(s, "fwd_screen");
+    if (p.cand) {
+      hipLaunchKernelGGL((fwd_pv_cand<D, BR, PK>), dim3((unsigned)(BH * p.nqt)), dim3(64 * BR), 0, s, p);
+      launched(s, "fwd_pv_cand");
+      // the query tiles the candidate pass could not take, from its queue
+      const int items = BH * p.nqt;
+      hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)(items < 2048 ? items : 2048)), dim3(64), 0, s, p, 0);
+    } else {  // every query tile runs: blocks of query tiles sharing their key tiles
+      const unsigned blocks = (unsigned)(BH * ((p.nqt + kBlkTiles - 1) / kBlkTiles));
+      hipLaunchKernelGGL((fwd_pv_blk<D, BR, PK, NORM>), dim3(blocks), dim3(64 * kBlkTiles), 0, s, p);
+    }
+    launched(s, "fwd_pv");
+    return (int)hipGetLastError();
   }
-  const dim3 grid((unsigned)(BR * BH) * (unsigned)p.screen_items);
-  hipLaunchKernelGGL((fwd_screen_i8<D, bf16>), grid, dim3(256), 0, s, p, BR);
-  launched(s, "fwd_screen");
-  if (NORM && p.cand) {
-    hipLaunchKernelGGL((fwd_pv_cand<D, BR, PK>), dim3((unsigned)(BH * p.nqt)), dim3(64 * BR), 0, s, p);
-    launched(s, "fwd_pv_cand");
-  }
-  if (NORM && p.cand) {  // the query tiles the candidate pass could not take, from its queue
-    const int items = BH * p.nqt;
-    hipLaunchKernelGGL((fwd_pv<D, BR, PK, NORM>), dim3((unsigned)(items < 2048 ? items : 2048)), dim3(64), 0, s, p, 0);
-  } else {  // every query tile runs: blocks of query tiles sharing their key tiles
-    const unsigned blocks = (unsigned)(BH * ((p.nqt + kBlkTiles - 1) / kBlkTiles));
-    hipLaunchKernelGGL((fwd_pv_blk<D, BR, PK, NORM>), dim3(blocks), dim3(64 * kBlkTiles), 0, s, p);
-  }
-  launched(s, "fwd_pv");
-  return (int)hipGetLastError();
 }
 
 template <int D, int BR, int PK>
