@@ -349,7 +349,7 @@ def dense_figures(dev, stream, steps):
                                 "executed_gflop": executed / 1e9,
                                 "achieved_tflops": executed / (pv * 1e-6) / 1e12,
                                 "frac_of_peak": executed / (pv * 1e-6) / 1e12 / peak,
-                                "note": "a score tile and an A.V tile per non-zero tile (the fp32 pass also "
+                                "note": "a score tile and an A.V tile per non-zero tile (the block pass "
                                         "scores every causal tile: executed counts the non-zero ones only)"}
         out[name] = rec
         del q, k, v, do, leaves

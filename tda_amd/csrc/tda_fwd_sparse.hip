@@ -59,6 +59,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const bf16* head, in
   return make_rsrc(head + (int64_t)(32 * kt) * stride, (uint32_t)(((int64_t)(rows - 1) * stride + D) * 2));
 }
 
+// Descriptor over the whole (N, D) head, for tile loads at a per-tile offset added to the lane's
+// offset (the range check covers the vector offset only): rows past N read as zeros.  Usable
+// when the byte offsets of 32 ceil(N / 32) rows stay below 2^31 (head_fits).
+template <int D>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const bf16* head, int64_t stride, int N) {
+  return make_rsrc(head, (uint32_t)(((int64_t)(N - 1) * stride + D) * 2));
+}
+__device__ __forceinline__ bool head_fits(int64_t stride, int N) {
+  return (int64_t)(32 * ((N + 31) / 32)) * stride * 2 < ((int64_t)1 << 31);
+}
+
 __device__ __forceinline__ float max16(const f32x16& v) {
   const float a = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
   const float b = fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7]));
@@ -1094,13 +1105,25 @@ __global__ void __launch_bounds__(64 * kBlkTiles) __attribute__((amdgpu_waves_pe
     };
     u32x4 kr[LPW], vr[LPW];
     f32x4 nr = {};
+    // one descriptor per head and a per-tile offset when the heads' offsets fit 31 bits (uniform),
+    // else one descriptor per tile
+    const bool whole = head_fits(sk, Nk) && head_fits(sv, Nk);
+    const __amdgpu_buffer_rsrc_t rkh = head_rsrc<D>(khead, sk, Nk), rvh = head_rsrc<D>(vhead, sv, Nk);
     auto issue = [&](int kt) {
-      const __amdgpu_buffer_rsrc_t rk = tile_rsrc<D>(khead, sk, kt, Nk);
-      const __amdgpu_buffer_rsrc_t rv = tile_rsrc<D>(vhead, sv, kt, Nk);
+      if (whole) {
+        const uint32_t tk = (uint32_t)(32 * kt) * (uint32_t)(2 * sk), tv = (uint32_t)(32 * kt) * (uint32_t)(2 * sv);
 #pragma unroll
-      for (int i = 0; i < LPW; ++i) kr[i] = buf_load16(rk, (uint32_t)(((vrow0 + RPI * i) * sk + 8 * vch) * 2));
+        for (int i = 0; i < LPW; ++i) kr[i] = buf_load16(rkh, tk + (uint32_t)(((vrow0 + RPI * i) * sk + 8 * vch) * 2));
 #pragma unroll
-      for (int i = 0; i < LPW; ++i) vr[i] = buf_load16(rv, (uint32_t)(((vrow0 + RPI * i) * sv + 8 * vch) * 2));
+        for (int i = 0; i < LPW; ++i) vr[i] = buf_load16(rvh, tv + (uint32_t)(((vrow0 + RPI * i) * sv + 8 * vch) * 2));
+      } else {
+        const __amdgpu_buffer_rsrc_t rk = tile_rsrc<D>(khead, sk, kt, Nk);
+        const __amdgpu_buffer_rsrc_t rv = tile_rsrc<D>(vhead, sv, kt, Nk);
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) kr[i] = buf_load16(rk, (uint32_t)(((vrow0 + RPI * i) * sk + 8 * vch) * 2));
+#pragma unroll
+        for (int i = 0; i < LPW; ++i) vr[i] = buf_load16(rv, (uint32_t)(((vrow0 + RPI * i) * sv + 8 * vch) * 2));
+      }
       if (NORM && wv == 0 && l < 8) nr = __builtin_bit_cast(f32x4, buf_load16(rn, (uint32_t)(32 * kt + 4 * l) * 4));
     };
 

@@ -26,8 +26,8 @@ class TileStats:
     tiles_causal: (branch, head, query tile, key tile) blocks holding a causal pair.
     tiles_nonzero: those holding a non-zero weight (the A.V work actually done).
     tiles_screened: those the int8 screen passed on to the exact pass (a superset of the
-    non-zero ones), for bf16 and for normalised float32 with more than 32 query rows; None
-    otherwise (float32 without the screen: its single pass tests every tile exactly)."""
+    non-zero ones), for normalised bf16 and for normalised float32 with more than 32 query rows;
+    None otherwise (no screen: the single pass tests every causal tile exactly)."""
     occupancy: torch.Tensor
     tiles_causal: int
     tiles_nonzero: int
@@ -84,9 +84,8 @@ def tile_sparsity(q, k, v, beta, relu_power=2.0, normalize=False, *, q2=None, k2
     t, tk = (n + TILE - 1) // TILE, (nk + TILE - 1) // TILE
     occupancy = _unpack(occ, branches, b, h, t, tk)
     return out, TileStats(occupancy=occupancy, tiles_causal=causal, tiles_nonzero=nonzero,
-                          tiles_screened=screened if q.shape[-1] <= 128 and (q.dtype == torch.bfloat16 or
-                                                                             (normalize and n > TILE))
-                          else None)
+                          tiles_screened=screened if q.shape[-1] <= 128 and normalize and
+                          (q.dtype == torch.bfloat16 or n > TILE) else None)
 
 
 __all__ = ["TileStats", "tile_sparsity", "TILE"]

@@ -74,6 +74,9 @@ def test_tile_sparsity_tra_unnormalized():
     q, k, v = make_inputs((1, 2, 300, 64), 12, 3, torch.bfloat16)
     out, st = tile_sparsity(q, k, v, 25.0, 1.0)
     assert torch.equal(out, threshold_rela_triton(q, k, v, 25.0, 1.0))
+    # no screen without normalisation: the block tile pass scores all 2 x 55 causal tiles
+    assert st.tiles_causal == 2 * 10 * 11 // 2 and st.tiles_screened is None
+    assert st.tiles_nonzero == int(st.occupancy.sum())
     want = _tile_map(q, k, 300, 64, 25.0, False).unsqueeze(0)
     assert (st.occupancy.cpu() != want).sum().item() <= 4
     strong = _tile_map(q, k, 300, 64, 25.0, False, 1e-4).unsqueeze(0)
