@@ -116,8 +116,9 @@ typedef struct tda_fwd_args {
   unsigned long long* stats;/* 3 counters: [0] += (query tile, key tile, branch) triples
                                on or below the diagonal, [1] += those with a non-zero
                                weight tile (A.V issued), [2] += those whose exact weights
-                               were evaluated (bf16: the tiles the screen kept, a superset
-                               of [1]; f32 leaves [2] alone); tiles are 32x32 */
+                               were evaluated (bf16: the tiles the screen kept, or every
+                               causal tile without normalisation; a superset of [1]; f32
+                               leaves [2] alone); tiles are 32x32 */
   void*  workspace;         /* device scratch of tda_fwd_workspace_bytes_for(args) bytes (or
                                the larger tda_fwd_workspace_bytes_kv()), 16-byte aligned: holds
                                the tile bitmask when occupancy is NULL and, when seq_len <= 32,
