@@ -248,7 +248,7 @@ int32_t tda_fwd_noalloc(const tda_fwd_args* args, void* stream);
  * with TDA_ERR_HIP. */
 int32_t tda_time_next_call(void* const* events, int32_t n);
 /* Kernel launches of the last timed call on this thread, and the name of launch k (0-based;
- * NULL past the end).  Names are the kernel families: "key_norms", "fwd_screen", ... */
+ * NULL past the end).  Names are the kernel families: "key_prep", "fwd_screen", ... */
 int32_t     tda_timed_launches(void);
 const char* tda_timed_launch_name(int32_t k);
 

@@ -54,7 +54,7 @@ constexpr int64_t pair_words(int64_t branches, int64_t bh, int64_t nqt) {
 // weight in the query tile; the exact pass gathers only these rows.  Layout: the keys,
 // kCandCap u32 per list, each distinct (increasing when the list has one producer; a query tile
 // whose key range the screen splits over several work items gets its keys in any order, which the
-// exact pass sorts); then the counts, u32 per list (zeroed by key_norms, raised by the screen's
+// exact pass sorts); then the counts, u32 per list (zeroed by key_prep, raised by the screen's
 // atomic adds).  A count above kCandCap marks a list that did not fit: the exact pass then walks
 // the bitmask tiles of that query tile.
 constexpr int kCandCap = 32;

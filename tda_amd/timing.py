@@ -11,7 +11,7 @@ next tda_fwd / tda_fwd_noalloc / tda_bwd call made by that thread.
         ops.forward(...)          # exactly one C-ABI call after arm()
         timer.collect()
     torch.cuda.synchronize()
-    timer.mean_us()               # {"key_norms": ..., "fwd_screen": ..., ...}
+    timer.mean_us()               # {"key_prep": ..., "fwd_screen": ..., ...}
 """
 from __future__ import annotations
 
