@@ -9,8 +9,8 @@ Against the CPU oracle (fp64 autograd of the formula): the output and every grad
 dq2, dk1, dk2, dv, dbeta, dlambda) at 2e-2 (bf16) / 1e-4 (fp32) normwise, on shapes whose
 query-tile count is not a multiple of four (workgroups with idle waves), the last query tile
 partial, one and two branches, d = 64 and 128, p = 1, 1.5, 2; position offsets (chunked
-prefill, keys past the last query); strided (B, N, H, d) views; beta < 0 (most weights
-non-zero); the fp32 gradients with and without the bitmask bitwise equal; the tile bitmask against the
+prefill, keys past the last query); strided (B, N, H, d) views; key and value rows 2^24 + 64
+elements apart; beta < 0 (most weights non-zero); the fp32 gradients with and without the bitmask bitwise equal; the tile bitmask against the
 oracle's non-zero tiles; the pair-list counts past the cap against the oracle's number of
 non-zero weights; and bitwise determinism of forward and backward."""
 import pytest
@@ -98,6 +98,34 @@ def test_dense_strided_views(dt):
     do = dob.transpose(1, 2)
     out, leaves, bt, lt = _run(xs, do, 1.0, 0.5, 2.0, 2)
     _check(out, leaves, bt, lt, xs, do, 1.0, 0.5, 2.0, 2, dtype)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_dense_key_rows_far_apart(dt):
+    """Key and value rows 2^24 + 64 elements apart (views into a buffer of about 2 GiB per
+    tensor in bf16): the bf16 block pass's tile offsets then no longer fit 31 bits from one
+    descriptor per head, so it takes one descriptor per key tile.  The output and every gradient
+    against the oracle on the same values."""
+    from tda_amd import threshold_rela_triton
+    dtype = DT[dt]
+    shape = (1, 1, 64, 64)
+    q, k0, v0 = make_inputs(shape, 1700, 3, dtype)
+    (do,) = make_inputs(shape, 1701, 1, dtype)
+    st = (1 << 24) + 64
+
+    def far(x):
+        y = torch.empty_strided(shape, (64 * st, 64 * st, st, 1), dtype=dtype, device="cuda")
+        y.copy_(x)
+        return y.requires_grad_(True)
+
+    leaves = [q.clone().requires_grad_(True), far(k0), far(v0)]
+    assert leaves[1].stride(2) == st and leaves[2].stride(2) == st
+    bt = torch.tensor(1.0, device="cuda", requires_grad=True)
+    out = threshold_rela_triton(*leaves, bt, relu_power=2.0, normalize=False)
+    out.backward(do)
+    _check(out, leaves, bt, bt, [q, k0, v0], do, 1.0, 0.0, 2.0, 1, dtype)
+    del leaves
+    torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
