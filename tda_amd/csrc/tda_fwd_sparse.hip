@@ -1257,7 +1257,7 @@ __global__ void __launch_bounds__(64 * kBlkTiles) __attribute__((amdgpu_waves_pe
   if (ZR) {
     // the call's zero range (the backward's gradients in training): the workgroup's even share of
     // the 16-byte units, streaming stores that drain while other workgroups still compute (the
-    // host picks ZR only when a share has fewer than 2^31 units)
+    // host picks ZR only for shares of at most 65536 units)
     const int64_t nwg = gridDim.x, z0 = P.zero_units * (int64_t)blockIdx.x / nwg;
     u32x4* zbase = reinterpret_cast<u32x4*>(P.zero) + z0;
     const uint32_t zn = (uint32_t)(P.zero_units * ((int64_t)blockIdx.x + 1) / nwg - z0);
@@ -1591,9 +1591,11 @@ int launch_sparse_t(const FwdParams& p, hipStream_t s) {
   if constexpr (!NORM) {
     // without normalisation every query tile runs the block tile pass over all its causal key
     // tiles (its scores decide the weights and write the bitmask; a screen would compute the
-    // same scores once more); it also clears the call's zero range
+    // same scores once more); it also clears the call's zero range when each workgroup's share
+    // is at most 1 MiB (a training step's gradients: 48 d units of 16 bytes per workgroup), else
+    // zero_range clears it across the whole GPU afterwards
     const unsigned blocks = (unsigned)(BH * ((p.nqt + kBlkTiles - 1) / kBlkTiles));
-    const bool zr = p.zero && p.zero_units > 0 && p.zero_units / blocks < (int64_t(1) << 31);
+    const bool zr = p.zero && p.zero_units > 0 && p.zero_units <= (int64_t)blocks * 65536;
     if (zr)
       hipLaunchKernelGGL((fwd_pv_blk<D, BR, PK, NORM, true, true>), dim3(blocks), dim3(64 * kBlkTiles), 0, s, p);
     else

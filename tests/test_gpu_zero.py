@@ -47,6 +47,28 @@ def test_forward_clears_its_zero_range(shape, nk, off, br, dtype, norm):
     assert int(torch.count_nonzero(zbuf)) == 0
 
 
+@pytest.mark.parametrize("mib,want", [(1, ["fwd_pv"]), (8, ["fwd_pv", "zero_range"])])
+def test_unnormalised_zero_range_shares(mib, want):
+    """The unnormalised bf16 forward (two workgroups of the block tile pass at (1, 1, 256, 64))
+    clears the zero range itself when each workgroup's share is at most 1 MiB (1 MiB in all),
+    else with zero_range after it (8 MiB); the range ends all zeros either way and the output
+    does not change."""
+    from tda_amd.timing import LaunchTimer
+    q1, _, k1, _, v = _inputs((1, 1, 256, 64), torch.bfloat16, 31)
+    beta = torch.tensor(0.4, device="cuda")
+    with torch.no_grad():
+        ref = ops.forward(q1, k1, None, None, v, beta, None, 2.0, False, 1)
+        zbuf = torch.full((mib << 19,), 7.0, dtype=torch.bfloat16, device="cuda")
+        timer = LaunchTimer(1)
+        timer.arm()
+        out = ops.forward(q1, k1, None, None, v, beta, None, 2.0, False, 1, zero=zbuf)
+        names = timer.collect()
+        torch.cuda.synchronize()
+    assert names == want
+    assert torch.equal(out, ref)
+    assert int(torch.count_nonzero(zbuf)) == 0
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_large_zero_range_against_small_problem(dtype):
     """A zero range far larger than the problem (one head of 64 rows: two key-tile steps of the
