@@ -985,6 +985,11 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) fw
 // own row keeps, exactly as fwd_pv_tile does (the same MFMA sequence on the same operands: the
 // same rows, bitmask rewrite, pair lists and counters).  Once a pair list has passed its cap
 // the wave only counts its non-zero weights (one wave sum at the end) instead of placing them.
+// WALK (no screen ran before it): every causal key tile of a row counts as kept, the row's
+// bitmask words are all written (the words past its last key tile as zeros) and the causal
+// tiles are counted into stats[0].  ZR (with WALK): the workgroup then clears its even share of
+// the call's zero range.  K and V tiles load through one descriptor per head at a per-tile
+// offset when the head's offsets fit 31 bits, else through one descriptor per tile.
 constexpr int kBlkTiles = 4;
 
 template <int D, int BR, int PK, bool NORM, bool WALK = false, bool ZR = false>
