@@ -1263,9 +1263,10 @@ __global__ void __launch_bounds__(64 * kBlkTiles) __attribute__((amdgpu_waves_pe
     // the call's zero range (the backward's gradients in training): the workgroup's even share of
     // the 16-byte units, streaming stores that drain while other workgroups still compute (the
     // host picks ZR only for shares of at most 65536 units)
-    const int64_t nwg = gridDim.x, z0 = P.zero_units * (int64_t)blockIdx.x / nwg;
-    u32x4* zbase = reinterpret_cast<u32x4*>(P.zero) + z0;
-    const uint32_t zn = (uint32_t)(P.zero_units * ((int64_t)blockIdx.x + 1) / nwg - z0);
+    // (units / nwg each, the first units % nwg one more; no product that could pass 64 bits)
+    const int64_t nwg = gridDim.x, per = P.zero_units / nwg, extra = P.zero_units % nwg, bid = blockIdx.x;
+    u32x4* zbase = reinterpret_cast<u32x4*>(P.zero) + (bid * per + min(bid, extra));
+    const uint32_t zn = (uint32_t)(per + (bid < extra ? 1 : 0));
     for (uint32_t u = threadIdx.x; u < zn; u += 64 * W) __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u}, zbase + u);
   }
 
