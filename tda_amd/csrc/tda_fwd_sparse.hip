@@ -473,7 +473,7 @@ __device__ __forceinline__ void wait_vm() {  // vmcnt(N) with the other counters
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 template <int D, class T>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) fwd_screen_i8(FwdParams P, int BR) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) fwd_screen_i8(FwdParams P, int BR) {
   constexpr int QPW = 2, NTHR = 256, TPI = I8_TPI;
   constexpr int NK = D / 32;                     // int8 MFMA steps over d
   constexpr int CPR = D / 16;                    // 16-byte chunks per int8 key row
