@@ -39,10 +39,10 @@ SCREEN_UNITS = 2.0                           # fwd_screen: Q1 K1^T and Q2 K2^T o
 # (with normalize, fwd_screen runs v_mfma_i32_32x32x32_i8: 2U int8 operations, priced at the int8 peak)
 # HBM bytes per forward-only launch of the dominant kernel (fwd_screen) at SHAPE, from rocprofv3
 # --pmc FETCH_SIZE and --pmc WRITE_SIZE runs of this script, each scaled by what the same counter
-# reads for --copy-probe (a 2^30-byte device copy): FETCH_SIZE x 2.000, WRITE_SIZE x 1.000 (329.1 MB
-# read + 50.0 MB written, the mean of the forward-only dispatches).  The command lines and the
+# reads for --copy-probe (a 2^30-byte device copy): FETCH_SIZE x 2.000, WRITE_SIZE x 1.000 (300.2 MB
+# read + 3.8 MB written, the mean of the forward-only dispatches).  The command lines and the
 # per-kernel figures are in profiles/tda_c2_bf16_counters.md; re-measure after kernel changes.
-SCREEN_HBM_BYTES = 3.791e8
+SCREEN_HBM_BYTES = 3.040e8
 SCREEN_KERNEL = "fwd_screen"
 SETTLE_S = 0.3  # seconds of untimed steps before the first timed region (see settle)
 
