@@ -1549,7 +1549,7 @@ __global__ void __launch_bounds__(64 * kBwdBlk) __attribute__((amdgpu_waves_per_
 // tile takes this pass when a list of its column did not fit (the test bwd_dkv_pairs queues
 // by; it writes nothing for such a key tile), or always without lists.
 template <int D, int BR, int PK, bool NORM>
-__global__ void __launch_bounds__(64 * kBwdBlk) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 2))) bwd_dkv_blk(BwdParams P) {
+__global__ void __launch_bounds__(64 * kBwdBlk) __attribute__((amdgpu_waves_per_eu(BR == 2 ? (D <= 64 ? 2 : 1) : (D <= 64 ? 3 : 2)))) bwd_dkv_blk(BwdParams P) {
   constexpr int W = kBwdBlk, NT = D / 16, ND = D / 32;
   constexpr int STAGE = 2 * 32 * D;  // Q tile, dO tile
   __shared__ __attribute__((aligned(16))) bf16 ring[2 * STAGE];
